@@ -1,0 +1,178 @@
+#!/usr/bin/env python3
+"""MoE-layer decode benchmark on one MI355X.
+
+Workload: the Mixtral-shaped MoE layer (hidden 4096, expert FFN 14336, 8
+experts, top-2, F32 router, Q4_0 experts) at decode batch 1: 1000 seeded
+tokens processed one at a time, each token's RMSNorm -> router -> top-k ->
+gate/up/SwiGLU -> down -> combine -> residual run to completion before the
+next starts. One step = the 1000 tokens. Inputs and weights are resident in
+HBM before timing starts.
+
+Prints one JSON line (the driver's contract) with:
+  value        whole-job tokens/s
+  roofline     the gate/up kernel (the dominant one): algorithmic bytes per
+               launch / its mean duration from HIP events, against 8 TB/s
+  cpu_baseline the reference's own kernels (oracle/_ref, AVX2 + WorkerPool
+               threads) on a bounded sample of the same tokens, host cores
+  parity       GPU vs reference outputs on that sample
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "MoE-layer tokens/s + % HBM roofline (decode) / % MFMA peak (prefill), 1 GPU"
+WORKLOAD = "mixtral-q4_0"
+
+
+def algorithmic_bytes(H, F, E, K, row_bytes_h, row_bytes_f):
+    """Bytes one token must move at minimum: K experts' gate+up+down weights,
+    the F32 router, and the activations in and out."""
+    gate_up = K * 2 * F * row_bytes_h + H * 4 + K * F * 4
+    down = K * H * row_bytes_f + K * F * 4 + 2 * H * 4 + K * 8
+    route = E * H * 4 + H * 4 * 2 + K * 8
+    return gate_up, down, route
+
+
+def cpu_baseline(lw, x, target_s=12.0, max_tokens=256):
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import fmoracle as fo
+    hl = fo.host_layer(lw)
+    threads = int(fo.ref().fmr_resolved_threads(0))
+    t0 = time.perf_counter()
+    out, ids, w = hl.ref_forward_batch(x[:4], fo.ISA_AVX2, threads=0)
+    per_tok = (time.perf_counter() - t0) / 4
+    n = int(max(8, min(max_tokens, target_s / max(per_tok, 1e-6))))
+    t0 = time.perf_counter()
+    out, ids, w = hl.ref_forward_batch(x[:n], fo.ISA_AVX2, threads=0)
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"first {n} of the 1000 tokens, reference gemv/gemv_quant (KernelIsa::Auto = AVX2, "
+                      f"WorkerPool {threads} threads) composed in the engine's MoE order"}, (out, ids, w, n)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--tokens", type=int, default=1000)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+    from freemoe_amd import fmx
+    from freemoe_amd import workloads as wl
+    from freemoe_amd.device import DeviceLayer
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    info = fmx.DeviceInfo()
+    fmx.call("fmx_device_info_get", 0, ctypes.byref(info))
+
+    spec = wl.WORKLOADS[WORKLOAD]
+    H, F, E, K, T = spec["hidden"], spec["ffn"], spec["experts"], spec["top_k"], args.tokens
+    seed = 1234
+    t_gen = time.perf_counter()
+    lw = wl.make_layer(H, F, E, K, spec["type_id"], seed)
+    x = wl.inputs(H, T, seed + 1)
+    print(f"[bench] generated weights in {time.perf_counter() - t_gen:.1f}s", file=sys.stderr, flush=True)
+
+    dl = DeviceLayer(lw, dev)
+    xd = torch.from_numpy(x).to(dev)
+    out = torch.empty_like(xd)
+    ids = torch.empty((T, K), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, K), dtype=torch.float32, device=dev)
+    dl.ensure_workspace(T)
+    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        dl.decode(xd, out, ids, wts)
+    torch.cuda.synchronize()
+    if dl.status() != 0:
+        print("device reported a routing error", file=sys.stderr)
+        return 1
+    print("[bench] warmup done", file=sys.stderr, flush=True)
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        dl.decode(xd, out, ids, wts)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    tok_s = T * args.steps / elapsed
+    print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
+
+    # per-kernel durations with HIP events on the launch stream
+    kernel_ms = (ctypes.c_double * 3)()
+    ws = dl.workspace
+    fmx.call("fmx_moe_decode_timed", ctypes.byref(dl.desc), xd.data_ptr(), out.data_ptr(), T, ids.data_ptr(),
+             wts.data_ptr(), ws.data_ptr(), ws.numel(), fmx.stream_handle(), kernel_ms)
+    route_us, gu_us, dn_us = (kernel_ms[i] * 1e3 / T for i in range(3))
+    rb_h = fmx.raw_row_bytes(lw.gate_type, H)
+    rb_f = fmx.raw_row_bytes(lw.down_type, F)
+    gu_bytes, dn_bytes, route_bytes = algorithmic_bytes(H, F, E, K, rb_h, rb_f)
+    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded random Q4_0 experts, F32 router, N(0,1) inputs)",
+        "config": {"workload": "Mixtral-shaped MoE layer decode, batch 1", "hidden": H, "ffn": F,
+                   "experts": E, "top_k": K, "expert_weights": "Q4_0", "router": "F32",
+                   "tokens_per_step": T, "seed": seed},
+        "roofline": {"bound": "hbm", "kernel": "gate_up_kernel<Q4_0>", "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": None, "bytes_per_launch": gu_bytes, "mean_us": round(gu_us, 3)},
+        "kernels_us_per_token": {"route": round(route_us, 3), "gate_up": round(gu_us, 3),
+                                 "down": round(dn_us, 3),
+                                 "down_GBs": round(dn_bytes / (dn_us * 1e-6) / 1e9, 1)},
+        "layer_hbm_frac": round((gu_bytes + dn_bytes + route_bytes) / (elapsed / (T * args.steps)) / 1e9
+                                / HBM_PEAK_GBS, 4),
+        "device": {"name": info.name.decode(), "arch": info.arch.decode(), "cus": info.compute_units,
+                   "clock_mhz": info.clock_khz // 1000, "mem_clock_mhz": info.memory_clock_khz // 1000},
+    }
+
+    if not args.no_cpu_baseline:
+        try:
+            base, (rout, rids, rw, n) = cpu_baseline(lw, x)
+            result["cpu_baseline"] = base
+            go = out[:n].cpu().numpy()
+            gi = ids[:n].cpu().numpy().astype(np.uint32)
+            result["parity"] = {"tokens": n, "ids_equal": bool(np.array_equal(gi, rids)),
+                                "max_abs": float(np.abs(go.astype(np.float64) - rout).max()),
+                                "bitwise_fraction": float(np.mean(go.view(np.uint32) == rout.view(np.uint32)))}
+        except Exception as e:  # the baseline is reported, never the target
+            result["cpu_baseline"] = {"value": None, "error": f"{type(e).__name__}: {e}"}
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

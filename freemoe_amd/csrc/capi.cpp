@@ -1,0 +1,413 @@
+// capi.cpp — host side of the C ABI: devices, memory, fences, faults, and the
+// MoE entry points that validate arguments and sequence the kernels.
+#include "bucket.hpp"
+#include "fmx_internal.hpp"
+#include "moe.hpp"
+
+#include <atomic>
+#include <chrono>
+#include <cstdio>
+#include <thread>
+
+namespace fmx {
+
+namespace {
+
+std::atomic<int> g_fault{FMX_FAULT_NONE};
+
+constexpr uint64_t kStatusBytes = 256;
+
+struct Fence {
+    hipEvent_t event = nullptr;
+    bool deferred = false;
+};
+
+// Workspace layout of the MoE entry points (all offsets 256-byte aligned):
+//   [0, 256)     error word (uint32)
+//   h            tokens x hidden floats (decode: one token)
+//   act          top_k x ffn floats (decode)
+struct DecodeWorkspace {
+    uint64_t h = 0, act = 0, total = 0;
+};
+
+DecodeWorkspace decode_workspace(const fmx_moe_layer *L) {
+    DecodeWorkspace w;
+    w.h = kStatusBytes;
+    w.act = w.h + align_up(static_cast<uint64_t>(L->hidden) * 4, 256);
+    w.total = w.act + align_up(static_cast<uint64_t>(L->top_k) * L->ffn * 4, 256);
+    return w;
+}
+
+__global__ void clear_word_kernel(uint32_t *word) { *word = 0; }
+
+int validate_layer(const fmx_moe_layer *L) {
+    if (!L) return FMX_ERR_INVALID_ARGUMENT;
+    if (L->hidden == 0 || L->ffn == 0 || L->experts == 0 || L->top_k == 0) return FMX_ERR_INVALID_ARGUMENT;
+    if (L->top_k > L->experts) return FMX_ERR_INVALID_ARGUMENT;      // engine.cpp:408
+    if (L->top_k > 32 || L->experts > 1024) return FMX_ERR_INVALID_ARGUMENT;
+    if (L->hidden > 16384) return FMX_ERR_SHAPE_MISMATCH;             // route kernel LDS
+    if (!L->router || !L->gate || !L->up || !L->down) return FMX_ERR_INVALID_ARGUMENT;
+    if (L->router_type != FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    return FMX_OK;
+}
+
+RouteArgs route_args(const fmx_moe_layer *L) {
+    RouteArgs a;
+    a.hidden = L->hidden;
+    a.experts = L->experts;
+    a.top_k = L->top_k;
+    a.norm_weight = L->norm_weight;
+    a.rms_eps = L->rms_eps;
+    a.norm_bias = L->norm_bias;
+    a.router = static_cast<const float *>(L->router);
+    a.router_bias = L->router_bias;
+    a.weights_norm = L->weights_norm;
+    a.epsilon_additive = L->epsilon_additive;
+    a.weights_epsilon = L->weights_epsilon;
+    a.weights_scale = L->weights_scale;
+    return a;
+}
+
+} // namespace
+
+int current_fault() { return g_fault.load(); }
+
+void consume_fault(int fault) {
+    int expected = fault;
+    g_fault.compare_exchange_strong(expected, FMX_FAULT_NONE);
+}
+
+int fault_gate() { return g_fault.load() == FMX_FAULT_DEVICE_LOSS ? FMX_ERR_DEVICE_LOSS : FMX_OK; }
+
+int status_of_hip(hipError_t e) {
+    switch (e) {
+    case hipSuccess: return FMX_OK;
+    case hipErrorOutOfMemory: return FMX_ERR_ALLOCATION_FAILED;
+    case hipErrorNoDevice:
+    case hipErrorInvalidDevice:
+    case hipErrorNoBinaryForGpu: return FMX_ERR_NO_DEVICE;
+    case hipErrorInvalidValue: return FMX_ERR_INVALID_ARGUMENT;
+    default: return FMX_ERR_LAUNCH_FAILED;
+    }
+}
+
+} // namespace fmx
+
+using namespace fmx;
+
+extern "C" {
+
+int fmx_abi_version(void) { return FMX_ABI_VERSION; }
+
+// Spelled as fm::error_name spells fm::ErrorCode (common.cpp).
+const char *fmx_status_name(int status) {
+    switch (status) {
+    case FMX_OK: return "OK";
+    case FMX_ERR_INVALID_ARGUMENT: return "INVALID_ARGUMENT";
+    case FMX_ERR_UNSUPPORTED_QUANTISATION: return "UNSUPPORTED_QUANTISATION";
+    case FMX_ERR_SHAPE_MISMATCH: return "SHAPE_MISMATCH";
+    case FMX_ERR_INTERNAL: return "INTERNAL_ERROR";
+    case FMX_ERR_ALLOCATION_FAILED: return "ALLOCATION_FAILED";
+    case FMX_ERR_TRANSFER_FAILED: return "TRANSFER_FAILED";
+    case FMX_ERR_FENCE_TIMEOUT: return "FENCE_TIMEOUT";
+    case FMX_ERR_DEVICE_LOSS: return "DEVICE_LOSS";
+    case FMX_ERR_NO_DEVICE: return "GPU_BACKEND_UNIMPLEMENTED";
+    case FMX_ERR_LAUNCH_FAILED: return "INTERNAL_ERROR";
+    }
+    return "UNKNOWN";
+}
+
+int fmx_device_info_get(int ordinal, fmx_device_info *info) {
+    if (!info) return FMX_ERR_INVALID_ARGUMENT;
+    if (int rc = fault_gate()) return rc;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= ordinal || ordinal < 0) return FMX_ERR_NO_DEVICE;
+    hipDeviceProp_t p;
+    FMX_HIP_TRY(hipGetDeviceProperties(&p, ordinal));
+    if (std::strncmp(p.gcnArchName, "gfx950", 6) != 0) return FMX_ERR_NO_DEVICE;
+    std::memset(info, 0, sizeof(*info));
+    std::snprintf(info->name, sizeof(info->name), "%s", p.name);
+    std::snprintf(info->arch, sizeof(info->arch), "%s", p.gcnArchName);
+    size_t free_b = 0, total_b = 0;
+    int prev = 0;
+    FMX_HIP_TRY(hipGetDevice(&prev));
+    FMX_HIP_TRY(hipSetDevice(ordinal));
+    const hipError_t me = hipMemGetInfo(&free_b, &total_b);
+    FMX_HIP_TRY(hipSetDevice(prev));
+    FMX_HIP_TRY(me);
+    info->total_memory_bytes = total_b;
+    info->free_memory_bytes = free_b;
+    info->compute_units = p.multiProcessorCount;
+    info->wavefront_size = p.warpSize;
+    info->lds_bytes_per_cu = static_cast<uint32_t>(p.maxSharedMemoryPerMultiProcessor);
+    info->clock_khz = p.clockRate;
+    info->memory_clock_khz = p.memoryClockRate;
+    info->memory_bus_bits = p.memoryBusWidth;
+    return FMX_OK;
+}
+
+int fmx_alloc(uint64_t bytes, void **device_ptr) {
+    if (!device_ptr || bytes == 0) return FMX_ERR_INVALID_ARGUMENT;
+    if (int rc = fault_gate()) return rc;
+    *device_ptr = nullptr;
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess) return FMX_ERR_ALLOCATION_FAILED;
+    if (hipMemset(p, 0, bytes) != hipSuccess) {
+        (void)hipFree(p);
+        return FMX_ERR_ALLOCATION_FAILED;
+    }
+    *device_ptr = p;
+    return FMX_OK;
+}
+
+int fmx_free(void *device_ptr) {
+    if (!device_ptr) return FMX_OK;
+    FMX_HIP_TRY(hipFree(device_ptr));
+    return FMX_OK;
+}
+
+int fmx_host_alloc(uint64_t bytes, void **host_ptr) {
+    if (!host_ptr || bytes == 0) return FMX_ERR_INVALID_ARGUMENT;
+    if (int rc = fault_gate()) return rc;
+    *host_ptr = nullptr;
+    void *p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) return FMX_ERR_ALLOCATION_FAILED;
+    std::memset(p, 0, bytes);
+    *host_ptr = p;
+    return FMX_OK;
+}
+
+int fmx_host_free(void *host_ptr) {
+    if (!host_ptr) return FMX_OK;
+    FMX_HIP_TRY(hipHostFree(host_ptr));
+    return FMX_OK;
+}
+
+int fmx_upload(void *device_dst, const void *host_src, uint64_t bytes, void *stream, void **fence) {
+    if (fence) *fence = nullptr;
+    const int fault = current_fault();
+    if (fault == FMX_FAULT_TRANSFER) return FMX_ERR_TRANSFER_FAILED;
+    if (fault == FMX_FAULT_DEVICE_LOSS) return FMX_ERR_DEVICE_LOSS;
+    if (!device_dst || (!host_src && bytes)) return FMX_ERR_INVALID_ARGUMENT;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (bytes) FMX_HIP_TRY(hipMemcpyAsync(device_dst, host_src, bytes, hipMemcpyHostToDevice, s));
+    if (fence) {
+        Fence *f = new Fence();
+        f->deferred = fault == FMX_FAULT_FENCE_DEFERRED;
+        if (hipEventCreateWithFlags(&f->event, hipEventDisableTiming) != hipSuccess ||
+            hipEventRecord(f->event, s) != hipSuccess) {
+            if (f->event) (void)hipEventDestroy(f->event);
+            delete f;
+            return FMX_ERR_TRANSFER_FAILED;
+        }
+        *fence = f;
+    }
+    return FMX_OK;
+}
+
+int fmx_download(void *host_dst, const void *device_src, uint64_t bytes, void *stream) {
+    if (int rc = fault_gate()) return rc;
+    if (current_fault() == FMX_FAULT_TRANSFER) return FMX_ERR_TRANSFER_FAILED;
+    if (!host_dst || (!device_src && bytes)) return FMX_ERR_INVALID_ARGUMENT;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (bytes) FMX_HIP_TRY(hipMemcpyAsync(host_dst, device_src, bytes, hipMemcpyDeviceToHost, s));
+    FMX_HIP_TRY(hipStreamSynchronize(s));
+    return FMX_OK;
+}
+
+int fmx_fence_query(void *fence, int *complete) {
+    if (!fence || !complete) return FMX_ERR_INVALID_ARGUMENT;
+    if (int rc = fault_gate()) return rc;
+    Fence *f = static_cast<Fence *>(fence);
+    if (f->deferred && current_fault() == FMX_FAULT_FENCE_DEFERRED) {
+        *complete = 0;
+        return FMX_OK;
+    }
+    const hipError_t e = hipEventQuery(f->event);
+    if (e == hipSuccess) *complete = 1;
+    else if (e == hipErrorNotReady) *complete = 0;
+    else return status_of_hip(e);
+    return FMX_OK;
+}
+
+// Polls with a 1 ms sleep, as Backend::wait_fence (backend.cpp:128-135).
+int fmx_fence_wait(void *fence, uint32_t timeout_ms) {
+    if (!fence) return FMX_ERR_INVALID_ARGUMENT;
+    if (current_fault() == FMX_FAULT_FENCE_TIMEOUT) {
+        consume_fault(FMX_FAULT_FENCE_TIMEOUT); // CpuBackend clears the fault when it fires
+        return FMX_ERR_FENCE_TIMEOUT;
+    }
+    const auto start = std::chrono::steady_clock::now();
+    for (;;) {
+        int done = 0;
+        if (int rc = fmx_fence_query(fence, &done)) return rc;
+        if (done) return FMX_OK;
+        const auto ms = std::chrono::duration_cast<std::chrono::milliseconds>(
+                            std::chrono::steady_clock::now() - start).count();
+        if (static_cast<uint64_t>(ms) >= timeout_ms) return FMX_ERR_FENCE_TIMEOUT;
+        std::this_thread::sleep_for(std::chrono::milliseconds(1));
+    }
+}
+
+int fmx_fence_release(void *fence) {
+    if (!fence) return FMX_OK;
+    Fence *f = static_cast<Fence *>(fence);
+    (void)hipEventSynchronize(f->event);
+    (void)hipEventDestroy(f->event);
+    delete f;
+    return FMX_OK;
+}
+
+int fmx_stream_sync(void *stream) {
+    if (int rc = fault_gate()) return rc;
+    FMX_HIP_TRY(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+    return FMX_OK;
+}
+
+int fmx_inject_fault(int fault) {
+    if (fault < FMX_FAULT_NONE || fault > FMX_FAULT_DEVICE_LOSS) return FMX_ERR_INVALID_ARGUMENT;
+    g_fault.store(fault);
+    return FMX_OK;
+}
+
+int fmx_clear_faults(void) {
+    g_fault.store(FMX_FAULT_NONE);
+    return FMX_OK;
+}
+
+// ------------------------------------------------------------------- MoE --
+
+uint64_t fmx_moe_workspace_bytes(const fmx_moe_layer *L, uint32_t tokens) {
+    if (validate_layer(L)) return 0;
+    (void)tokens;
+    return decode_workspace(L).total;
+}
+
+int fmx_moe_route(const fmx_moe_layer *L, const float *x, uint32_t tokens, float *h, float *logits,
+                  uint32_t *ids, float *weights, void *workspace, uint64_t workspace_bytes,
+                  void *stream) {
+    if (int rc = fault_gate()) return rc;
+    if (int rc = validate_layer(L)) return rc;
+    if (tokens == 0) return FMX_OK;
+    if (!x || !ids || !weights || !workspace || workspace_bytes < kStatusBytes) return FMX_ERR_INVALID_ARGUMENT;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t *status = static_cast<uint32_t *>(workspace);
+    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
+    FMX_LAUNCH_CHECK();
+    return launch_route(route_args(L), x, tokens, h, logits, ids, weights, status, s);
+}
+
+int fmx_moe_decode(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
+                   float *weights, void *workspace, uint64_t workspace_bytes, void *stream) {
+    if (int rc = fault_gate()) return rc;
+    if (int rc = validate_layer(L)) return rc;
+    if (tokens == 0) return FMX_OK;
+    if (!x || !out || !ids || !weights || !workspace) return FMX_ERR_INVALID_ARGUMENT;
+    const DecodeWorkspace ws = decode_workspace(L);
+    if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
+    ExpertArgs ea;
+    if (int rc = prepare_expert_args(L, &ea)) return rc;
+    const RouteArgs ra = route_args(L);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint8_t *base = static_cast<uint8_t *>(workspace);
+    uint32_t *status = reinterpret_cast<uint32_t *>(base);
+    float *h = reinterpret_cast<float *>(base + ws.h);
+    float *act = reinterpret_cast<float *>(base + ws.act);
+    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
+    FMX_LAUNCH_CHECK();
+    const uint64_t H = L->hidden, K = L->top_k;
+    for (uint32_t t = 0; t < tokens; ++t) {
+        if (int rc = launch_route(ra, x + t * H, 1, h, nullptr, ids + t * K, weights + t * K, status, s)) return rc;
+        if (int rc = launch_experts(ea, x + t * H, h, ids + t * K, weights + t * K, act, out + t * H, status, s))
+            return rc;
+    }
+    return FMX_OK;
+}
+
+int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
+                         float *weights, void *workspace, uint64_t workspace_bytes, void *stream,
+                         double *kernel_ms) {
+    if (int rc = fault_gate()) return rc;
+    if (int rc = validate_layer(L)) return rc;
+    if (!kernel_ms) return FMX_ERR_INVALID_ARGUMENT;
+    kernel_ms[0] = kernel_ms[1] = kernel_ms[2] = 0.0;
+    if (tokens == 0) return FMX_OK;
+    if (!x || !out || !ids || !weights || !workspace) return FMX_ERR_INVALID_ARGUMENT;
+    const DecodeWorkspace ws = decode_workspace(L);
+    if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
+    ExpertArgs ea;
+    if (int rc = prepare_expert_args(L, &ea)) return rc;
+    const RouteArgs ra = route_args(L);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint8_t *base = static_cast<uint8_t *>(workspace);
+    uint32_t *status = reinterpret_cast<uint32_t *>(base);
+    float *h = reinterpret_cast<float *>(base + ws.h);
+    float *act = reinterpret_cast<float *>(base + ws.act);
+    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
+    FMX_LAUNCH_CHECK();
+    // events in batches: [token][route start, route end = experts start, gate/up end, down end]
+    constexpr uint32_t kBatch = 64;
+    hipEvent_t ev[kBatch][4];
+    for (auto &row : ev)
+        for (auto &e : row) FMX_HIP_TRY(hipEventCreate(&e));
+    int rc = FMX_OK;
+    const uint64_t H = L->hidden, K = L->top_k;
+    for (uint32_t t0 = 0; t0 < tokens && rc == FMX_OK; t0 += kBatch) {
+        const uint32_t n = tokens - t0 < kBatch ? tokens - t0 : kBatch;
+        for (uint32_t i = 0; i < n && rc == FMX_OK; ++i) {
+            const uint64_t t = t0 + i;
+            (void)hipEventRecord(ev[i][0], s);
+            rc = launch_route(ra, x + t * H, 1, h, nullptr, ids + t * K, weights + t * K, status, s);
+            (void)hipEventRecord(ev[i][1], s);
+            if (rc == FMX_OK)
+                rc = launch_experts(ea, x + t * H, h, ids + t * K, weights + t * K, act, out + t * H, status, s,
+                                    ev[i][2]);
+            (void)hipEventRecord(ev[i][3], s);
+        }
+        if (hipStreamSynchronize(s) != hipSuccess) rc = FMX_ERR_LAUNCH_FAILED;
+        for (uint32_t i = 0; i < n && rc == FMX_OK; ++i) {
+            float a = 0, b = 0, c = 0;
+            if (hipEventElapsedTime(&a, ev[i][0], ev[i][1]) != hipSuccess ||
+                hipEventElapsedTime(&b, ev[i][1], ev[i][2]) != hipSuccess ||
+                hipEventElapsedTime(&c, ev[i][2], ev[i][3]) != hipSuccess)
+                rc = FMX_ERR_LAUNCH_FAILED;
+            kernel_ms[0] += a;
+            kernel_ms[1] += b;
+            kernel_ms[2] += c;
+        }
+    }
+    for (auto &row : ev)
+        for (auto &e : row) (void)hipEventDestroy(e);
+    return rc;
+}
+
+int fmx_moe_status(void *workspace, void *stream) {
+    if (!workspace) return FMX_ERR_INVALID_ARGUMENT;
+    if (int rc = fault_gate()) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t word = 0;
+    FMX_HIP_TRY(hipMemcpyAsync(&word, workspace, 4, hipMemcpyDeviceToHost, s));
+    FMX_HIP_TRY(hipStreamSynchronize(s));
+    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, static_cast<uint32_t *>(workspace));
+    FMX_LAUNCH_CHECK();
+    if (word & STATUS_BAD_EXPERT) return FMX_ERR_INVALID_ARGUMENT;
+    if (word & STATUS_NONFINITE_SCORE) return FMX_ERR_INTERNAL;
+    return FMX_OK;
+}
+
+int fmx_moe_bucket(const uint32_t *ids, uint32_t tokens, uint32_t top_k, uint32_t experts,
+                   uint32_t *offsets, uint32_t *token_list, uint32_t *rank_list, void *workspace,
+                   uint64_t workspace_bytes, void *stream) {
+    if (int rc = fault_gate()) return rc;
+    if (experts == 0 || experts > kBucketMaxExperts || top_k == 0 || top_k > experts)
+        return FMX_ERR_INVALID_ARGUMENT;
+    if (!offsets || !workspace || workspace_bytes < kStatusBytes) return FMX_ERR_INVALID_ARGUMENT;
+    if (tokens && (!ids || !token_list || !rank_list)) return FMX_ERR_INVALID_ARGUMENT;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint32_t *status = static_cast<uint32_t *>(workspace);
+    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
+    FMX_LAUNCH_CHECK();
+    return launch_bucket(ids, tokens, top_k, experts, offsets, token_list, rank_list, nullptr, status, s);
+}
+
+} // extern "C"

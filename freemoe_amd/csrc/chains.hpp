@@ -1,0 +1,328 @@
+// chains.hpp — the reference's per-lane FMA chains as wavefront building blocks.
+//
+// The reference's AVX2 row dots (kernels.cpp:639-653, 673-694, 720-771) keep
+// eight float lanes per row and fold blocks into them in order. Here eight
+// consecutive lanes of a wavefront are those eight lanes: lane l (= lane & 7)
+// owns chain l of its row and walks the row's blocks in order, so every
+// rounding happens in the same sequence as on the CPU. A wavefront holds 8 rows
+// ("row slots"); a thread may carry NR rows that share the same x values.
+//
+// x is staged per K-tile in LDS in the order the lanes consume it, so a lane's
+// four x values of a block are one 16-byte LDS read and lanes of different row
+// slots read the same address (broadcast).
+#pragma once
+
+#include "fmx_internal.hpp"
+
+namespace fmx {
+
+// ---------------------------------------------------------------- Q4_0 --
+// Block = 32 elements; chunk = 8 blocks (one 16-byte lane load per row).
+// LDS per block: 8 lanes x float4 x-values, then 8 floats of 8*sum(x).
+struct Q40 {
+    static constexpr uint32_t kType = FMX_TYPE_Q4_0;
+    static constexpr uint32_t kBlock = 32;
+    static constexpr uint32_t kPerChunk = 8;
+    static constexpr uint32_t kLdsFloatsPerBlock = 40;
+
+    // Stage blocks [b0, b0 + nb) of x into lds (xs: nb*32 floats, s8: nb*8).
+    __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb,
+                                 float *lds, uint32_t tid, uint32_t nthreads) {
+        float4 *xs = reinterpret_cast<float4 *>(lds);
+        float *s8 = lds + nb * 32;
+        for (uint32_t e = tid; e < nb * 8; e += nthreads) {
+            const uint32_t b = e >> 3, l = e & 7;
+            const float *xb = x + static_cast<uint64_t>(b0 + b) * 32;
+            const float x0 = xb[l], x1 = xb[8 + l], x2 = xb[16 + l], x3 = xb[24 + l];
+            xs[e] = make_float4(x0, x1, x2, x3);
+            // 8 * ((x[l] + x[8+l]) + (x[16+l] + x[24+l])): the scaling is exact
+            s8[e] = 8.0f * ((x0 + x1) + (x2 + x3));
+        }
+    }
+
+    // Row base pointers for this lane: scales of the row, and the lane's
+    // 16-byte slot of chunk 0 of the row.
+    struct Row {
+        const uint8_t *scales;
+        const uint8_t *quants;
+    };
+    __device__ static Row row(const uint8_t *packed, uint64_t scale_bytes, uint32_t blocks_padded,
+                              uint32_t chunks, uint32_t r, uint32_t l) {
+        Row w;
+        w.scales = packed + static_cast<uint64_t>(r) * blocks_padded * 2;
+        w.quants = packed + scale_bytes + (static_cast<uint64_t>(r) * chunks * 8 + l) * 16;
+        return w;
+    }
+
+    struct Chunk {
+        uint4 q, s;
+    };
+    __device__ static Chunk load(const Row &w, uint32_t c) {
+        Chunk k;
+        k.q = ld16(w.quants + static_cast<uint64_t>(c) * 128);
+        k.s = ld16(w.scales + static_cast<uint64_t>(c) * 16);
+        return k;
+    }
+
+    // Blocks j < nblk of chunk `k` (block index within the LDS tile: tb0 + j).
+    template <int NR>
+    __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t nb_tile,
+                                uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
+        const float4 *xs = reinterpret_cast<const float4 *>(lds);
+        const float *s8 = lds + nb_tile * 32;
+#pragma unroll
+        for (uint32_t jj = 0; jj < 4; ++jj) {
+            // dword jj holds blocks 2jj and 2jj+1: bytes (A, B, A', B')
+            uint32_t qw[NR], lo4[NR], hi4[NR], sw[NR];
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                qw[i] = jj == 0 ? k[i].q.x : jj == 1 ? k[i].q.y : jj == 2 ? k[i].q.z : k[i].q.w;
+                sw[i] = jj == 0 ? k[i].s.x : jj == 1 ? k[i].s.y : jj == 2 ? k[i].s.z : k[i].s.w;
+                lo4[i] = qw[i] & 0x0F0F0F0Fu;
+                hi4[i] = (qw[i] >> 4) & 0x0F0F0F0Fu;
+            }
+#pragma unroll
+            for (uint32_t h = 0; h < 2; ++h) {
+                const uint32_t j = 2 * jj + h;
+                if (j >= nblk) break;
+                const uint32_t e = (tb0 + j) * 8 + l;
+                const float4 xv = xs[e];
+                const float sx8 = s8[e];
+#pragma unroll
+                for (int i = 0; i < NR; ++i) {
+                    const float qa = h ? ubyte2(lo4[i]) : ubyte0(lo4[i]);
+                    const float qb = h ? ubyte3(lo4[i]) : ubyte1(lo4[i]);
+                    const float qc = h ? ubyte2(hi4[i]) : ubyte0(hi4[i]);
+                    const float qd = h ? ubyte3(hi4[i]) : ubyte1(hi4[i]);
+                    // lo = fma(q[l], x[l], q[8+l]*x[8+l]); hi likewise for 16+l, 24+l
+                    const float lo = fma_rn(qa, xv.x, qb * xv.y);
+                    const float hi = fma_rn(qc, xv.z, qd * xv.w);
+                    const float c = (lo + hi) - sx8;
+                    const float d = half_bits_to_float(h ? (sw[i] >> 16) : (sw[i] & 0xFFFFu));
+                    t[i] = fma_rn(c, d, t[i]);
+                }
+            }
+        }
+    }
+
+    // The row's value from the lane chains (all 8 lanes end with it).
+    __device__ static float finish(float t) { return hsum8_lanes(t); }
+};
+
+// ---------------------------------------------------------------- Q8_0 --
+// Block = 32; chunk = 4 blocks. LDS per block: 8 lanes x float4.
+struct Q80 {
+    static constexpr uint32_t kType = FMX_TYPE_Q8_0;
+    static constexpr uint32_t kBlock = 32;
+    static constexpr uint32_t kPerChunk = 4;
+    static constexpr uint32_t kLdsFloatsPerBlock = 32;
+
+    __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb,
+                                 float *lds, uint32_t tid, uint32_t nthreads) {
+        float4 *xs = reinterpret_cast<float4 *>(lds);
+        for (uint32_t e = tid; e < nb * 8; e += nthreads) {
+            const uint32_t b = e >> 3, l = e & 7;
+            const float *xb = x + static_cast<uint64_t>(b0 + b) * 32;
+            xs[e] = make_float4(xb[l], xb[8 + l], xb[16 + l], xb[24 + l]);
+        }
+    }
+
+    struct Row {
+        const uint8_t *scales;
+        const uint8_t *quants;
+    };
+    __device__ static Row row(const uint8_t *packed, uint64_t scale_bytes, uint32_t blocks_padded,
+                              uint32_t chunks, uint32_t r, uint32_t l) {
+        Row w;
+        w.scales = packed + static_cast<uint64_t>(r) * blocks_padded * 2;
+        w.quants = packed + scale_bytes + (static_cast<uint64_t>(r) * chunks * 8 + l) * 16;
+        return w;
+    }
+
+    struct Chunk {
+        uint4 q;
+        uint2 s;
+    };
+    __device__ static Chunk load(const Row &w, uint32_t c) {
+        Chunk k;
+        k.q = ld16(w.quants + static_cast<uint64_t>(c) * 128);
+        k.s = *reinterpret_cast<const uint2 *>(w.scales + static_cast<uint64_t>(c) * 8);
+        return k;
+    }
+
+    __device__ static float sbyte(uint32_t w, int k) {
+        return static_cast<float>(static_cast<int32_t>(w << (24 - 8 * k)) >> 24);
+    }
+
+    template <int NR>
+    __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t /*nb_tile*/,
+                                uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
+        const float4 *xs = reinterpret_cast<const float4 *>(lds);
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            if (j >= nblk) break;
+            const float4 xv = xs[(tb0 + j) * 8 + l];
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const uint32_t w = j == 0 ? k[i].q.x : j == 1 ? k[i].q.y : j == 2 ? k[i].q.z : k[i].q.w;
+                const uint32_t sw = j < 2 ? k[i].s.x : k[i].s.y;
+                // acc over elements l, 8+l, 16+l, 24+l from zero, then t += acc*d (both FMA)
+                float acc = fma_rn(sbyte(w, 0), xv.x, 0.0f);
+                acc = fma_rn(sbyte(w, 1), xv.y, acc);
+                acc = fma_rn(sbyte(w, 2), xv.z, acc);
+                acc = fma_rn(sbyte(w, 3), xv.w, acc);
+                const float d = half_bits_to_float((j & 1) ? (sw >> 16) : (sw & 0xFFFFu));
+                t[i] = fma_rn(acc, d, t[i]);
+            }
+        }
+    }
+
+    __device__ static float finish(float t) { return hsum8_lanes(t); }
+};
+
+// ---------------------------------------------------------------- Q4_K --
+// Super-block = 256 elements = one chunk. LDS per super-block: [4 groups]
+// [8 lanes][8 floats: x[64g+8k+l], k<4, then x[64g+32+8k+l]] followed, after
+// the tile, by 8 floats of per-group sums (lo, hi) in the reference's order.
+struct Q4K {
+    static constexpr uint32_t kType = FMX_TYPE_Q4_K;
+    static constexpr uint32_t kBlock = 256;
+    static constexpr uint32_t kPerChunk = 1;
+    static constexpr uint32_t kLdsFloatsPerBlock = 264;
+
+    __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb,
+                                 float *lds, uint32_t tid, uint32_t nthreads) {
+        float4 *xs = reinterpret_cast<float4 *>(lds);
+        float *sums = lds + nb * 256;
+        for (uint32_t e = tid; e < nb * 32; e += nthreads) {
+            const uint32_t b = e >> 5, g = (e >> 3) & 3, l = e & 7;
+            const float *xg = x + static_cast<uint64_t>(b0 + b) * 256 + 64 * g;
+            xs[2 * e] = make_float4(xg[l], xg[8 + l], xg[16 + l], xg[24 + l]);
+            xs[2 * e + 1] = make_float4(xg[32 + l], xg[40 + l], xg[48 + l], xg[56 + l]);
+        }
+        for (uint32_t e = tid; e < nb * 4; e += nthreads) {
+            const float *xg = x + static_cast<uint64_t>(b0 + (e >> 2)) * 256 + 64 * (e & 3);
+            float lo[8], hi[8];
+            for (int l = 0; l < 8; ++l) {
+                lo[l] = (xg[l] + xg[8 + l]) + (xg[16 + l] + xg[24 + l]);
+                hi[l] = (xg[32 + l] + xg[40 + l]) + (xg[48 + l] + xg[56 + l]);
+            }
+            sums[2 * e] = ((lo[0] + lo[4]) + (lo[1] + lo[5])) + ((lo[2] + lo[6]) + (lo[3] + lo[7]));
+            sums[2 * e + 1] = ((hi[0] + hi[4]) + (hi[1] + hi[5])) + ((hi[2] + hi[6]) + (hi[3] + hi[7]));
+        }
+    }
+
+    struct Row {
+        const uint8_t *header;
+        const uint8_t *quants;
+    };
+    __device__ static Row row(const uint8_t *packed, uint64_t scale_bytes, uint32_t /*bp*/,
+                              uint32_t chunks, uint32_t r, uint32_t l) {
+        Row w;
+        w.header = packed + static_cast<uint64_t>(r) * chunks * 16;
+        w.quants = packed + scale_bytes + (static_cast<uint64_t>(r) * chunks * 8 + l) * 16;
+        return w;
+    }
+
+    struct Chunk {
+        uint4 q, h;
+    };
+    __device__ static Chunk load(const Row &w, uint32_t c) {
+        Chunk k;
+        k.q = ld16(w.quants + static_cast<uint64_t>(c) * 128);
+        k.h = ld16(w.header + static_cast<uint64_t>(c) * 16);
+        return k;
+    }
+
+    template <int NR>
+    __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t nb_tile,
+                                uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
+        if (nblk == 0) return;
+        const float4 *xs = reinterpret_cast<const float4 *>(lds);
+        const float *sums = lds + nb_tile * 256;
+#pragma unroll
+        for (uint32_t g = 0; g < 4; ++g) {
+            const uint32_t e = (tb0 * 4 + g) * 8 + l;
+            const float4 xl = xs[2 * e], xh = xs[2 * e + 1];
+            const float sum_lo = sums[(tb0 * 4 + g) * 2], sum_hi = sums[(tb0 * 4 + g) * 2 + 1];
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const uint32_t w = g == 0 ? k[i].q.x : g == 1 ? k[i].q.y : g == 2 ? k[i].q.z : k[i].q.w;
+                const uint32_t lo4 = w & 0x0F0F0F0Fu, hi4 = (w >> 4) & 0x0F0F0F0Fu;
+                float alo = fma_rn(ubyte0(lo4), xl.x, 0.0f);
+                alo = fma_rn(ubyte1(lo4), xl.y, alo);
+                alo = fma_rn(ubyte2(lo4), xl.z, alo);
+                alo = fma_rn(ubyte3(lo4), xl.w, alo);
+                float ahi = fma_rn(ubyte0(hi4), xh.x, 0.0f);
+                ahi = fma_rn(ubyte1(hi4), xh.y, ahi);
+                ahi = fma_rn(ubyte2(hi4), xh.z, ahi);
+                ahi = fma_rn(ubyte3(hi4), xh.w, ahi);
+                const float hlo = hsum8_lanes(alo), hhi = hsum8_lanes(ahi);
+                uint8_t hdr[16];
+                memcpy(hdr, &k[i].h, 16);
+                const float d = half_bits_to_float(hdr[0] | (hdr[1] << 8));
+                const float dmin = half_bits_to_float(hdr[2] | (hdr[3] << 8));
+                uint32_t sc1, m1, sc2, m2;
+                k4_scale_min(2 * g, hdr + 4, sc1, m1);
+                k4_scale_min(2 * g + 1, hdr + 4, sc2, m2);
+                const float dsc1 = d * static_cast<float>(sc1), dm1 = dmin * static_cast<float>(m1);
+                const float dsc2 = d * static_cast<float>(sc2), dm2 = dmin * static_cast<float>(m2);
+                // part = fma(d*sc, hsum(acc), -((dmin*m) * sum_x)); total += lo + hi
+                const float part_lo = fma_rn(dsc1, hlo, -(dm1 * sum_lo));
+                const float part_hi = fma_rn(dsc2, hhi, -(dm2 * sum_hi));
+                t[i] = t[i] + (part_lo + part_hi);
+            }
+        }
+    }
+
+    // The running total is already the row's value in every lane.
+    __device__ static float finish(float t) { return t; }
+};
+
+// ------------------------------------------------ chunked row processing --
+
+// Processes chunks [c0, c1) of NR rows against the LDS tile that starts at
+// block `tile_b0` (tile holds nb_tile blocks). PF chunks per row are kept in
+// flight in registers: chunk c + PF is requested before chunk c is consumed.
+template <class T, int NR, int PF>
+__device__ __forceinline__ void run_chunks_pf(const typename T::Row (&rows)[NR], uint32_t c0,
+                                              uint32_t c1, uint32_t blocks, uint32_t tile_b0,
+                                              uint32_t nb_tile, const float *lds, uint32_t l,
+                                              float (&t)[NR]) {
+    typename T::Chunk buf[PF][NR];
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+        if (c0 + p < c1) {
+#pragma unroll
+            for (int i = 0; i < NR; ++i) buf[p][i] = T::load(rows[i], c0 + p);
+        }
+    for (uint32_t c = c0; c < c1; c += PF) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p) {
+            const uint32_t cc = c + p;
+            if (cc >= c1) break;
+            typename T::Chunk cur[NR];
+#pragma unroll
+            for (int i = 0; i < NR; ++i) cur[i] = buf[p][i];
+            if (cc + PF < c1) {
+#pragma unroll
+                for (int i = 0; i < NR; ++i) buf[p][i] = T::load(rows[i], cc + PF);
+            }
+            const uint32_t b = cc * T::kPerChunk;
+            const uint32_t nblk = blocks - b < T::kPerChunk ? blocks - b : T::kPerChunk;
+            T::template step<NR>(cur, lds, nb_tile, b - tile_b0, nblk, l, t);
+        }
+    }
+}
+
+// Blocks per LDS tile: a whole number of chunks, at most `budget_floats` of LDS.
+template <class T>
+__host__ __device__ inline uint32_t tile_blocks_for(uint32_t blocks, uint32_t budget_floats) {
+    uint32_t tb = budget_floats / T::kLdsFloatsPerBlock;
+    tb = tb / T::kPerChunk * T::kPerChunk;
+    if (tb == 0) tb = T::kPerChunk;
+    const uint32_t whole = (blocks + T::kPerChunk - 1) / T::kPerChunk * T::kPerChunk;
+    return tb < whole ? tb : whole;
+}
+
+} // namespace fmx

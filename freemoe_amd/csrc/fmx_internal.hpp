@@ -1,0 +1,123 @@
+// fmx_internal.hpp — shared host and device helpers of libfmx (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstring>
+
+#include "fmx.h"
+
+namespace fmx {
+
+// ------------------------------------------------------------------ host --
+
+// Host-side fault state (fm::BackendFault semantics, backend.cpp:258-277).
+int current_fault();
+void consume_fault(int fault);
+// FMX_ERR_DEVICE_LOSS when a device loss is injected, else FMX_OK.
+int fault_gate();
+
+#define FMX_HIP_TRY(expr)                                                        \
+    do {                                                                         \
+        hipError_t fmx_e_ = (expr);                                              \
+        if (fmx_e_ != hipSuccess) return ::fmx::status_of_hip(fmx_e_);           \
+    } while (0)
+
+#define FMX_LAUNCH_CHECK()                                                       \
+    do {                                                                         \
+        hipError_t fmx_e_ = hipGetLastError();                                   \
+        if (fmx_e_ != hipSuccess) return ::fmx::status_of_hip(fmx_e_);           \
+    } while (0)
+
+int status_of_hip(hipError_t e);
+
+inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+inline uint32_t div_up(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+// Packed layout of one [rows x cols] matrix: two regions, scales then quants,
+// each 256-byte aligned. A "chunk" is what one lane loads per row per step
+// (16 bytes of quants); 8 lanes load a row's 128-byte chunk together.
+struct PackedGeometry {
+    uint32_t type_id = 0;
+    uint32_t rows = 0, cols = 0;
+    uint32_t blocks = 0;          // quant blocks (Q4_K: super-blocks) per row
+    uint32_t blocks_padded = 0;   // rounded up to whole chunks
+    uint32_t chunks = 0;          // per row
+    uint64_t scale_row_bytes = 0; // bytes of region A per row
+    uint64_t scale_bytes = 0;     // region A, aligned
+    uint64_t quant_bytes = 0;     // region B
+    uint64_t total = 0;
+};
+
+// Fills `g`; FMX_ERR_UNSUPPORTED_QUANTISATION / FMX_ERR_SHAPE_MISMATCH on bad input.
+int packed_geometry(uint32_t type_id, uint32_t rows, uint32_t cols, PackedGeometry *g);
+
+// Raw block geometry (gguf.cpp:58-106) for the four types.
+int raw_geometry(uint32_t type_id, uint32_t *block_size, uint32_t *block_bytes);
+
+// Device error word bits (fmx_moe_status).
+enum : uint32_t { STATUS_NONFINITE_SCORE = 1u, STATUS_BAD_EXPERT = 2u };
+
+// ---------------------------------------------------------------- device --
+
+// IEEE binary16 bits -> float. The hardware conversion is exact for every
+// half, subnormals included (tests check all 65536 encodings).
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+// Byte n of a dword as an exact float (v_cvt_f32_ubyte{0..3}).
+__device__ __forceinline__ float ubyte0(uint32_t v) {
+    float r;
+    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+__device__ __forceinline__ float ubyte1(uint32_t v) {
+    float r;
+    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+__device__ __forceinline__ float ubyte2(uint32_t v) {
+    float r;
+    asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+__device__ __forceinline__ float ubyte3(uint32_t v) {
+    float r;
+    asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+__device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+
+// Value held by lane (lane ^ mask), mask < 8, inside a wavefront.
+__device__ __forceinline__ float lane_xor(float v, int mask) {
+    return __shfl_xor(v, mask, 64);
+}
+
+// Horizontal sum of t_l over the 8 lanes l = lane & 7 in the tree of the
+// reference's _mm256 reduction: s_i = t_i + t_{i+4}; (s0 + s1) + (s2 + s3).
+// Addition is commutative, so every lane of the group ends with the same bits.
+__device__ __forceinline__ float hsum8_lanes(float t) {
+    const float s = t + lane_xor(t, 4);
+    const float a = s + lane_xor(s, 1);
+    return a + lane_xor(a, 2);
+}
+
+__device__ __forceinline__ uint4 ld16(const void *p) {
+    return *reinterpret_cast<const uint4 *>(p);
+}
+
+// 6-bit scale/min pair j of a Q4_K super-block (quant.cpp:63-71).
+__device__ __forceinline__ void k4_scale_min(int j, const uint8_t *q, uint32_t &sc, uint32_t &m) {
+    if (j < 4) {
+        sc = q[j] & 63u;
+        m = q[j + 4] & 63u;
+    } else {
+        sc = (q[j + 4] & 0x0Fu) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+} // namespace fmx

@@ -1,0 +1,104 @@
+// matvec.hip — y = W x for one matrix (Backend::matvec / gemv_quant).
+//
+// Block-type rows use the lane chains of chains.hpp; F32 rows use the
+// reference's gemv_avx2_row order (kernels.cpp:147-167): per row 16 chains
+// (chain c takes k = c mod 16; chains 0..7 are acc0, 8..15 acc1), an 8-element
+// tail into acc0, lane-wise acc0 + acc1, the 8-lane tree sum, then a scalar
+// FMA tail over the last in_dim mod 8 elements.
+#include "chains.hpp"
+#include "matvec.hpp"
+
+namespace fmx {
+
+namespace {
+
+constexpr uint32_t kThreads = 256;              // 4 wavefronts
+constexpr uint32_t kLdsBudgetFloats = 8 * 1024; // 32 KiB of x per tile
+
+template <class T, int NR>
+__global__ __launch_bounds__(kThreads) void matvec_kernel(
+    const uint8_t *__restrict__ packed, const float *__restrict__ x, float *__restrict__ y,
+    uint32_t rows, uint32_t blocks, uint32_t blocks_padded, uint32_t chunks, uint64_t scale_bytes,
+    uint32_t tile_blocks) {
+    extern __shared__ float lds[];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t l = tid & 7;
+    const uint32_t slot = tid >> 3; // 0..31
+    const uint32_t r0 = (blockIdx.x * (kThreads / 8) + slot) * NR;
+    typename T::Row rw[NR];
+    float t[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const uint32_t r = r0 + i < rows ? r0 + i : rows - 1; // clamp: loads stay in bounds
+        rw[i] = T::row(packed, scale_bytes, blocks_padded, chunks, r, l);
+        t[i] = 0.0f;
+    }
+    for (uint32_t tb = 0; tb < blocks; tb += tile_blocks) {
+        const uint32_t nb = blocks - tb < tile_blocks ? blocks - tb : tile_blocks;
+        __syncthreads();
+        T::stage(x, tb, nb, lds, tid, kThreads);
+        __syncthreads();
+        const uint32_t c0 = tb / T::kPerChunk;
+        const uint32_t c1 = (tb + nb + T::kPerChunk - 1) / T::kPerChunk;
+        run_chunks_pf<T, NR, 2>(rw, c0, c1, blocks, tb, nb, lds, l, t);
+    }
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const float v = T::finish(t[i]);
+        if (l == 0 && r0 + i < rows) y[r0 + i] = v;
+    }
+}
+
+// F32: 16 lanes per row (4 row slots per wavefront, 16 per workgroup).
+__global__ __launch_bounds__(kThreads) void matvec_f32_kernel(const float *__restrict__ w,
+                                                              const float *__restrict__ x,
+                                                              float *__restrict__ y,
+                                                              uint32_t rows, uint32_t n) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t c = tid & 15;
+    const uint32_t r = blockIdx.x * (kThreads / 16) + (tid >> 4);
+    const uint32_t rr = r < rows ? r : rows - 1;
+    const float *row = w + static_cast<uint64_t>(rr) * n;
+    const float total = f32_row_chains(row, x, n, c);
+    if (c == 0 && r < rows) y[r] = total;
+}
+
+template <class T, int NR>
+int launch_matvec(const PackedGeometry &g, const void *packed, const float *x, float *y,
+                  hipStream_t s) {
+    const uint32_t tb = tile_blocks_for<T>(g.blocks, kLdsBudgetFloats);
+    const size_t lds = static_cast<size_t>(tb) * T::kLdsFloatsPerBlock * sizeof(float);
+    const uint32_t rows_per_wg = (kThreads / 8) * NR;
+    hipLaunchKernelGGL((matvec_kernel<T, NR>), dim3(div_up(g.rows, rows_per_wg)), dim3(kThreads),
+                       lds, s, static_cast<const uint8_t *>(packed), x, y, g.rows, g.blocks,
+                       g.blocks_padded, g.chunks, g.scale_bytes, tb);
+    FMX_LAUNCH_CHECK();
+    return FMX_OK;
+}
+
+} // namespace
+
+} // namespace fmx
+
+using namespace fmx;
+
+extern "C" int fmx_matvec(uint32_t type_id, const void *packed, const float *x, float *y,
+                          uint32_t out_dim, uint32_t in_dim, void *stream) {
+    if (int rc = fault_gate()) return rc;
+    if (out_dim == 0 || in_dim == 0) return FMX_OK;
+    PackedGeometry g;
+    if (int rc = packed_geometry(type_id, out_dim, in_dim, &g)) return rc;
+    if (!packed || !x || !y) return FMX_ERR_INVALID_ARGUMENT;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    switch (type_id) {
+    case FMX_TYPE_F32:
+        hipLaunchKernelGGL(matvec_f32_kernel, dim3(div_up(out_dim, kThreads / 16)), dim3(kThreads), 0,
+                           s, static_cast<const float *>(packed), x, y, out_dim, in_dim);
+        FMX_LAUNCH_CHECK();
+        return FMX_OK;
+    case FMX_TYPE_Q4_0: return launch_matvec<Q40, 2>(g, packed, x, y, s);
+    case FMX_TYPE_Q8_0: return launch_matvec<Q80, 2>(g, packed, x, y, s);
+    case FMX_TYPE_Q4_K: return launch_matvec<Q4K, 1>(g, packed, x, y, s);
+    }
+    return FMX_ERR_UNSUPPORTED_QUANTISATION;
+}

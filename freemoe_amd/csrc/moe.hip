@@ -1,0 +1,458 @@
+// moe.hip — the MoE block of Engine::forward_token on gfx950.
+//
+//   route_kernel    RMSNorm (engine.cpp:723-740) -> router logits (F32, the
+//                   gemv_avx2_row order) -> logit bias (engine.cpp:1611-1616) ->
+//                   softmax (engine.cpp:378-393) -> stable top-k
+//                   (engine.cpp:395-411) -> weights (engine.cpp:1680-1702).
+//                   One workgroup per token.
+//   gate_up_kernel  gate and up rows of each routed expert, fused with SwiGLU
+//                   (engine.cpp:1738-1761; activation.hpp:33, 84).
+//   down_kernel     down rows of all routed experts of a token, the combine in
+//                   rank order (engine.cpp:1770) and the residual add
+//                   (engine.cpp:813-816, 1822).
+//
+// RMSNorm's sum of squares is a sequential double sum in the reference. Here it
+// is a parallel sum plus a certificate: every normalised value is checked to
+// lie farther from a float rounding boundary than the worst-case difference
+// between the two sums can move it; only when some value is that close does
+// one lane redo the sum in the reference's order. Either way h is the
+// reference's h bit for bit.
+#include "chains.hpp"
+#include "matvec.hpp"
+#include "moe.hpp"
+
+namespace fmx {
+
+namespace {
+
+constexpr uint32_t kRouteThreads = 256;
+constexpr uint32_t kThreads = 256;
+
+__device__ inline double wave_sum_double(double v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+// The float after f towards +infinity (f finite).
+__device__ inline float float_up(float f) {
+    if (f == 0.0f) return __uint_as_float(1u);
+    const uint32_t b = __float_as_uint(f);
+    return __uint_as_float((b >> 31) ? b - 1 : b + 1);
+}
+
+// True when float(yd) could change if yd moved by rel_tol of itself: the
+// rounding boundaries around f are the midpoints to its neighbours, exact in
+// double.
+__device__ inline bool rounding_unsafe(double yd, float f, double rel_tol) {
+    if (!__builtin_isfinite(f) || __builtin_isnan(yd)) return true;
+    if (yd == 0.0) return false;
+    const double tol = __builtin_fabs(yd) * rel_tol;
+    const double lo = (static_cast<double>(f) + static_cast<double>(-float_up(-f))) * 0.5;
+    const double hi = (static_cast<double>(f) + static_cast<double>(float_up(f))) * 0.5;
+    return (yd - lo) <= tol || (hi - yd) <= tol;
+}
+
+__device__ inline float normalised(float x, const float *w, uint32_t k, double scale,
+                                   double norm_bias) {
+    const float gain = w ? static_cast<float>(norm_bias + static_cast<double>(w[k])) : 1.0f;
+    return static_cast<float>(static_cast<double>(x) * scale * static_cast<double>(gain));
+}
+
+__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a, const float *__restrict__ x,
+                                                              float *__restrict__ h_out,
+                                                              float *__restrict__ logits_out,
+                                                              uint32_t *__restrict__ ids,
+                                                              float *__restrict__ weights,
+                                                              uint32_t *__restrict__ status) {
+    extern __shared__ double lds_d[];
+    __shared__ double wave_part[kRouteThreads / 64];
+    __shared__ double ss_s, sum_s;
+    __shared__ int unsafe_s, bad_s;
+    __shared__ float max_s;
+    const uint32_t H = a.hidden, E = a.experts, K = a.top_k;
+    const uint32_t tid = threadIdx.x, t = blockIdx.x;
+    double *exps = lds_d;                                   // [E]
+    float *xs = reinterpret_cast<float *>(lds_d + E);       // [H]
+    float *hs = xs + H;                                     // [H]
+    float *logit_s = hs + H;                                // [E]
+    float *prob_s = logit_s + E;                            // [E]
+    const float *xt = x + static_cast<uint64_t>(t) * H;
+
+    // ---- RMSNorm
+    double part = 0.0;
+    for (uint32_t k = tid; k < H; k += kRouteThreads) {
+        const float v = xt[k];
+        xs[k] = v;
+        part += static_cast<double>(v) * static_cast<double>(v);
+    }
+    part = wave_sum_double(part);
+    if ((tid & 63) == 0) wave_part[tid >> 6] = part;
+    if (tid == 0) {
+        unsafe_s = 0;
+        bad_s = 0;
+    }
+    __syncthreads();
+    if (tid == 0) ss_s = ((wave_part[0] + wave_part[1]) + wave_part[2]) + wave_part[3];
+    __syncthreads();
+    // |parallel sum - sequential sum| <= (H + 32) u ss; scale moves by half of
+    // that plus a few roundings (see header)
+    const double rel_tol = 0.6e-16 * static_cast<double>(H + 32) + 2e-15;
+    double scale = 1.0 / sqrt(ss_s / static_cast<double>(H) + a.rms_eps);
+    bool unsafe = false;
+    for (uint32_t k = tid; k < H; k += kRouteThreads) {
+        const float gain = a.norm_weight ? static_cast<float>(a.norm_bias + static_cast<double>(a.norm_weight[k])) : 1.0f;
+        const double yd = static_cast<double>(xs[k]) * scale * static_cast<double>(gain);
+        const float f = static_cast<float>(yd);
+        hs[k] = f;
+        unsafe |= rounding_unsafe(yd, f, rel_tol);
+    }
+    if (unsafe) atomicOr(&unsafe_s, 1);
+    __syncthreads();
+    if (unsafe_s) {
+        if (tid == 0) {
+            double ss = 0.0;
+            for (uint32_t k = 0; k < H; ++k) ss += static_cast<double>(xs[k]) * static_cast<double>(xs[k]);
+            ss_s = ss;
+        }
+        __syncthreads();
+        scale = 1.0 / sqrt(ss_s / static_cast<double>(H) + a.rms_eps);
+        for (uint32_t k = tid; k < H; k += kRouteThreads)
+            hs[k] = normalised(xs[k], a.norm_weight, k, scale, a.norm_bias);
+        __syncthreads();
+    }
+    if (h_out)
+        for (uint32_t k = tid; k < H; k += kRouteThreads) h_out[static_cast<uint64_t>(t) * H + k] = hs[k];
+
+    // ---- router logits: 16 lanes per expert row
+    for (uint32_t e0 = 0; e0 < E; e0 += kRouteThreads / 16) {
+        const uint32_t e = e0 + (tid >> 4);
+        const uint32_t er = e < E ? e : E - 1;
+        const float v = f32_row_chains(a.router + static_cast<uint64_t>(er) * H, hs, H, tid & 15);
+        if ((tid & 15) == 0 && e < E) logit_s[e] = a.router_bias ? v + a.router_bias[e] : v;
+    }
+    __syncthreads();
+
+    // ---- softmax: float max, double exp and sum, float quotient
+    if (tid == 0) {
+        float m = logit_s[0];
+        int bad = 0;
+        for (uint32_t e = 0; e < E; ++e) {
+            if (!__builtin_isfinite(logit_s[e])) bad = 1;
+            if (logit_s[e] > m) m = logit_s[e];
+        }
+        max_s = m;
+        bad_s = bad;
+    }
+    __syncthreads();
+    if (logits_out)
+        for (uint32_t e = tid; e < E; e += kRouteThreads) logits_out[static_cast<uint64_t>(t) * E + e] = logit_s[e];
+    if (bad_s) {
+        // The reference raises INTERNAL_ERROR here. Record it and emit a
+        // routing that keeps every later kernel in bounds.
+        if (tid == 0) atomicOr(status, STATUS_NONFINITE_SCORE);
+        for (uint32_t i = tid; i < K; i += kRouteThreads) {
+            ids[static_cast<uint64_t>(t) * K + i] = i < E ? i : 0;
+            weights[static_cast<uint64_t>(t) * K + i] = 0.0f;
+        }
+        return;
+    }
+    for (uint32_t e = tid; e < E; e += kRouteThreads)
+        exps[e] = exp(static_cast<double>(logit_s[e]) - static_cast<double>(max_s));
+    __syncthreads();
+    if (tid == 0) {
+        double s = 0.0;
+        for (uint32_t e = 0; e < E; ++e) s += exps[e];
+        sum_s = s;
+    }
+    __syncthreads();
+    for (uint32_t e = tid; e < E; e += kRouteThreads) prob_s[e] = static_cast<float>(exps[e] / sum_s);
+    __syncthreads();
+
+    // ---- top-k (ties to the lower index) and weights, one lane
+    if (tid == 0) {
+        uint32_t *it = ids + static_cast<uint64_t>(t) * K;
+        float *wt = weights + static_cast<uint64_t>(t) * K;
+        uint32_t chosen[64];
+        float total = 0.0f;
+        for (uint32_t r = 0; r < K; ++r) {
+            uint32_t best = E;
+            for (uint32_t e = 0; e < E; ++e) {
+                bool taken = false;
+                for (uint32_t q = 0; q < r; ++q) taken |= chosen[q] == e;
+                if (taken) continue;
+                if (best == E || prob_s[e] > prob_s[best]) best = e;
+            }
+            chosen[r] = best;
+        }
+        float wv[64];
+        for (uint32_t r = 0; r < K; ++r) {
+            wv[r] = prob_s[chosen[r]];
+            total += wv[r];
+        }
+        if (a.weights_norm) {
+            const double den = a.epsilon_additive ? static_cast<double>(total) + a.weights_epsilon
+                                                  : fmax(static_cast<double>(total), a.weights_epsilon);
+            for (uint32_t r = 0; r < K; ++r) wv[r] = static_cast<float>(static_cast<double>(wv[r]) / den);
+        }
+        for (uint32_t r = 0; r < K; ++r) {
+            it[r] = chosen[r];
+            wt[r] = static_cast<float>(static_cast<double>(wv[r]) * a.weights_scale);
+        }
+    }
+}
+
+// ------------------------------------------------------------ experts --
+
+__device__ inline float swiglu(float gate, float up) {
+    const double g = static_cast<double>(gate);
+    return static_cast<float>(g / (1.0 + exp(-g))) * up;
+}
+
+// Gate and up rows j of the expert at rank blockIdx.y, RJ rows per thread.
+template <class T, int RJ, int PF>
+__global__ __launch_bounds__(kThreads) void gate_up_kernel(ExpertArgs a, const float *__restrict__ h,
+                                                           const uint32_t *__restrict__ ids,
+                                                           float *__restrict__ act,
+                                                           uint32_t *__restrict__ status) {
+    extern __shared__ float lds[];
+    const uint32_t tid = threadIdx.x, l = tid & 7, slot = tid >> 3;
+    const uint32_t rank = blockIdx.y;
+    const uint32_t e = ids[rank];
+    if (e >= a.experts) {
+        if (tid == 0 && blockIdx.x == 0) atomicOr(status, STATUS_BAD_EXPERT);
+        return;
+    }
+    const uint8_t *gate = static_cast<const uint8_t *>(a.gate[e]);
+    const uint8_t *up = static_cast<const uint8_t *>(a.up[e]);
+    const uint32_t F = a.ffn;
+    const uint32_t j0 = (blockIdx.x * (kThreads / 8) + slot) * RJ;
+    typename T::Row rw[2 * RJ];
+    float t[2 * RJ];
+#pragma unroll
+    for (int m = 0; m < RJ; ++m) {
+        const uint32_t j = j0 + m < F ? j0 + m : F - 1;
+        rw[2 * m] = T::row(gate, a.gu.scale_bytes, a.gu.blocks_padded, a.gu.chunks, j, l);
+        rw[2 * m + 1] = T::row(up, a.gu.scale_bytes, a.gu.blocks_padded, a.gu.chunks, j, l);
+        t[2 * m] = 0.0f;
+        t[2 * m + 1] = 0.0f;
+    }
+    const uint32_t blocks = a.gu.blocks;
+    for (uint32_t tb = 0; tb < blocks; tb += a.gu_tile) {
+        const uint32_t nb = blocks - tb < a.gu_tile ? blocks - tb : a.gu_tile;
+        __syncthreads();
+        T::stage(h, tb, nb, lds, tid, kThreads);
+        __syncthreads();
+        run_chunks_pf<T, 2 * RJ, PF>(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk,
+                                     blocks, tb, nb, lds, l, t);
+    }
+#pragma unroll
+    for (int m = 0; m < RJ; ++m) {
+        const float g = T::finish(t[2 * m]);
+        const float u = T::finish(t[2 * m + 1]);
+        if (l == 0 && j0 + m < F) act[static_cast<uint64_t>(rank) * F + j0 + m] = swiglu(g, u);
+    }
+}
+
+// Down rows of every routed expert of one token, then the combine and the
+// residual. Slot s handles (rank s / jpw, row s % jpw); jpw = 32 / top_k.
+template <class T, int PF>
+__global__ __launch_bounds__(kThreads) void down_kernel(ExpertArgs a, const float *__restrict__ x,
+                                                        const float *__restrict__ act,
+                                                        const uint32_t *__restrict__ ids,
+                                                        const float *__restrict__ w,
+                                                        float *__restrict__ out,
+                                                        uint32_t *__restrict__ status) {
+    extern __shared__ float lds[];
+    __shared__ float dres[kThreads / 8];
+    const uint32_t tid = threadIdx.x, l = tid & 7, slot = tid >> 3;
+    const uint32_t K = a.top_k, H = a.hidden;
+    const uint32_t jpw = (kThreads / 8) / K;
+    const uint32_t rank = slot / jpw < K ? slot / jpw : K - 1;
+    const uint32_t jj = slot % jpw;
+    const uint32_t j = blockIdx.x * jpw + jj;
+    const uint32_t jr = j < H ? j : H - 1;
+    uint32_t e = ids[rank];
+    const bool bad = e >= a.experts;
+    if (bad) {
+        if (l == 0) atomicOr(status, STATUS_BAD_EXPERT);
+        e = 0;
+    }
+    typename T::Row rw[1];
+    rw[0] = T::row(static_cast<const uint8_t *>(a.down[e]), a.dn.scale_bytes, a.dn.blocks_padded,
+                   a.dn.chunks, jr, l);
+    float t[1] = {0.0f};
+    const uint32_t blocks = a.dn.blocks;
+    const uint32_t tile_floats = a.dn_tile * T::kLdsFloatsPerBlock;
+    for (uint32_t tb = 0; tb < blocks; tb += a.dn_tile) {
+        const uint32_t nb = blocks - tb < a.dn_tile ? blocks - tb : a.dn_tile;
+        __syncthreads();
+        for (uint32_t r = 0; r < K; ++r)
+            T::stage(act + static_cast<uint64_t>(r) * a.ffn, tb, nb, lds + r * tile_floats, tid, kThreads);
+        __syncthreads();
+        run_chunks_pf<T, 1, PF>(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk,
+                                blocks, tb, nb, lds + rank * tile_floats, l, t);
+    }
+    const float v = T::finish(t[0]);
+    if (l == 0 && slot < K * jpw) dres[slot] = bad ? 0.0f : v;
+    __syncthreads();
+    if (tid < jpw) {
+        const uint32_t jo = blockIdx.x * jpw + tid;
+        if (jo < H) {
+            float ffn = 0.0f;
+            for (uint32_t r = 0; r < K; ++r) ffn = ffn + w[r] * dres[r * jpw + tid];
+            out[jo] = x[jo] + ffn;
+        }
+    }
+}
+
+// F32 experts: 16 lanes per row, x read through the cache.
+__global__ __launch_bounds__(kThreads) void gate_up_f32_kernel(ExpertArgs a, const float *__restrict__ h,
+                                                               const uint32_t *__restrict__ ids,
+                                                               float *__restrict__ act,
+                                                               uint32_t *__restrict__ status) {
+    const uint32_t tid = threadIdx.x, c = tid & 15;
+    const uint32_t rank = blockIdx.y;
+    const uint32_t e = ids[rank];
+    if (e >= a.experts) {
+        if (tid == 0 && blockIdx.x == 0) atomicOr(status, STATUS_BAD_EXPERT);
+        return;
+    }
+    const uint32_t F = a.ffn, H = a.hidden;
+    const uint32_t j = blockIdx.x * (kThreads / 16) + (tid >> 4);
+    const uint32_t jr = j < F ? j : F - 1;
+    const float *gate = static_cast<const float *>(a.gate[e]) + static_cast<uint64_t>(jr) * H;
+    const float *up = static_cast<const float *>(a.up[e]) + static_cast<uint64_t>(jr) * H;
+    const float g = f32_row_chains(gate, h, H, c);
+    const float u = f32_row_chains(up, h, H, c);
+    if (c == 0 && j < F) act[static_cast<uint64_t>(rank) * F + j] = swiglu(g, u);
+}
+
+__global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const float *__restrict__ x,
+                                                            const float *__restrict__ act,
+                                                            const uint32_t *__restrict__ ids,
+                                                            const float *__restrict__ w,
+                                                            float *__restrict__ out,
+                                                            uint32_t *__restrict__ status) {
+    __shared__ float dres[kThreads / 16];
+    const uint32_t tid = threadIdx.x, c = tid & 15, slot = tid >> 4; // 16 slots
+    const uint32_t K = a.top_k, H = a.hidden, F = a.ffn;
+    const uint32_t jpw = (kThreads / 16) / K;
+    const uint32_t rank = slot / jpw < K ? slot / jpw : K - 1;
+    const uint32_t jj = slot % jpw;
+    const uint32_t j = blockIdx.x * jpw + jj;
+    const uint32_t jr = j < H ? j : H - 1;
+    uint32_t e = ids[rank];
+    const bool bad = e >= a.experts;
+    if (bad) {
+        if (c == 0) atomicOr(status, STATUS_BAD_EXPERT);
+        e = 0;
+    }
+    const float *row = static_cast<const float *>(a.down[e]) + static_cast<uint64_t>(jr) * F;
+    const float v = f32_row_chains(row, act + static_cast<uint64_t>(rank) * F, F, c);
+    if (c == 0 && slot < K * jpw) dres[slot] = bad ? 0.0f : v;
+    __syncthreads();
+    if (tid < jpw) {
+        const uint32_t jo = blockIdx.x * jpw + tid;
+        if (jo < H) {
+            float ffn = 0.0f;
+            for (uint32_t r = 0; r < K; ++r) ffn = ffn + w[r] * dres[r * jpw + tid];
+            out[jo] = x[jo] + ffn;
+        }
+    }
+}
+
+// ------------------------------------------------------------ launchers --
+
+template <class T>
+int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const uint32_t *ids,
+                     const float *w, float *act, float *out, uint32_t *status, hipStream_t s,
+                     hipEvent_t mid) {
+    constexpr int RJ = 1;
+    const size_t lds_gu = static_cast<size_t>(a.gu_tile) * T::kLdsFloatsPerBlock * sizeof(float);
+    hipLaunchKernelGGL((gate_up_kernel<T, RJ, 2>), dim3(div_up(a.ffn, (kThreads / 8) * RJ), a.top_k),
+                       dim3(kThreads), lds_gu, s, a, h, ids, act, status);
+    FMX_LAUNCH_CHECK();
+    if (mid) FMX_HIP_TRY(hipEventRecord(mid, s));
+    const uint32_t jpw = (kThreads / 8) / a.top_k;
+    const size_t lds_dn = static_cast<size_t>(a.dn_tile) * T::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
+    hipLaunchKernelGGL((down_kernel<T, 4>), dim3(div_up(a.hidden, jpw)), dim3(kThreads), lds_dn, s, a, x,
+                       act, ids, w, out, status);
+    FMX_LAUNCH_CHECK();
+    return FMX_OK;
+}
+
+} // namespace
+
+size_t route_lds_bytes(uint32_t hidden, uint32_t experts) {
+    return static_cast<size_t>(experts) * sizeof(double) + (2ull * hidden + 2ull * experts) * sizeof(float);
+}
+
+int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
+                 uint32_t *ids, float *weights, uint32_t *status, hipStream_t s) {
+    hipLaunchKernelGGL(route_kernel, dim3(tokens), dim3(kRouteThreads), route_lds_bytes(a.hidden, a.experts),
+                       s, a, x, h, logits, ids, weights, status);
+    FMX_LAUNCH_CHECK();
+    return FMX_OK;
+}
+
+int prepare_expert_args(const fmx_moe_layer *L, ExpertArgs *a) {
+    ExpertArgs e;
+    e.hidden = L->hidden;
+    e.ffn = L->ffn;
+    e.experts = L->experts;
+    e.top_k = L->top_k;
+    e.type_gu = L->gate_type;
+    e.type_dn = L->down_type;
+    e.gate = L->gate;
+    e.up = L->up;
+    e.down = L->down;
+    if (L->up_type != L->gate_type) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    if (int rc = packed_geometry(L->gate_type, L->ffn, L->hidden, &e.gu)) return rc;
+    if (int rc = packed_geometry(L->down_type, L->hidden, L->ffn, &e.dn)) return rc;
+    // LDS tiles: gate/up stage one x tile; down stages one tile per rank
+    constexpr uint32_t kGuBudget = 6 * 1024, kDnBudget = 10 * 1024;
+    switch (L->gate_type) {
+    case FMX_TYPE_Q4_0: e.gu_tile = tile_blocks_for<Q40>(e.gu.blocks, kGuBudget); break;
+    case FMX_TYPE_Q8_0: e.gu_tile = tile_blocks_for<Q80>(e.gu.blocks, kGuBudget); break;
+    case FMX_TYPE_Q4_K: e.gu_tile = tile_blocks_for<Q4K>(e.gu.blocks, kGuBudget); break;
+    default: e.gu_tile = 0; break;
+    }
+    const uint32_t dn_budget = kDnBudget / L->top_k;
+    switch (L->down_type) {
+    case FMX_TYPE_Q4_0: e.dn_tile = tile_blocks_for<Q40>(e.dn.blocks, dn_budget); break;
+    case FMX_TYPE_Q8_0: e.dn_tile = tile_blocks_for<Q80>(e.dn.blocks, dn_budget); break;
+    case FMX_TYPE_Q4_K: e.dn_tile = tile_blocks_for<Q4K>(e.dn.blocks, dn_budget); break;
+    default: e.dn_tile = 0; break;
+    }
+    *a = e;
+    return FMX_OK;
+}
+
+int launch_experts(const ExpertArgs &a, const float *x, const float *h, const uint32_t *ids,
+                   const float *w, float *act, float *out, uint32_t *status, hipStream_t s,
+                   hipEvent_t mid) {
+    if (a.type_gu == FMX_TYPE_F32) {
+        if (a.top_k > kThreads / 16 || a.type_dn != FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+        hipLaunchKernelGGL(gate_up_f32_kernel, dim3(div_up(a.ffn, kThreads / 16), a.top_k), dim3(kThreads), 0, s,
+                           a, h, ids, act, status);
+        FMX_LAUNCH_CHECK();
+        if (mid) FMX_HIP_TRY(hipEventRecord(mid, s));
+    }
+    if (a.type_gu == FMX_TYPE_F32 && a.type_dn == FMX_TYPE_F32) {
+        const uint32_t jpw = (kThreads / 16) / a.top_k;
+        hipLaunchKernelGGL(down_f32_kernel, dim3(div_up(a.hidden, jpw)), dim3(kThreads), 0, s, a, x, act, ids,
+                           w, out, status);
+        FMX_LAUNCH_CHECK();
+        return FMX_OK;
+    }
+    if (a.type_gu != a.type_dn) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    switch (a.type_gu) {
+    case FMX_TYPE_Q4_0: return launch_experts_q<Q40>(a, x, h, ids, w, act, out, status, s, mid);
+    case FMX_TYPE_Q8_0: return launch_experts_q<Q80>(a, x, h, ids, w, act, out, status, s, mid);
+    case FMX_TYPE_Q4_K: return launch_experts_q<Q4K>(a, x, h, ids, w, act, out, status, s, mid);
+    }
+    return FMX_ERR_UNSUPPORTED_QUANTISATION;
+}
+
+} // namespace fmx

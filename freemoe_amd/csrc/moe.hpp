@@ -1,0 +1,42 @@
+// moe.hpp — argument blocks and launchers shared by the MoE entry points.
+#pragma once
+
+#include "fmx_internal.hpp"
+
+namespace fmx {
+
+// Routing arguments (device pointers); F32 router only.
+struct RouteArgs {
+    uint32_t hidden, experts, top_k;
+    const float *norm_weight;
+    double rms_eps, norm_bias;
+    const float *router;
+    const float *router_bias;
+    int32_t weights_norm, epsilon_additive;
+    double weights_epsilon, weights_scale;
+};
+
+// Expert projections of one layer: packed geometry of gate/up ([ffn x hidden])
+// and down ([hidden x ffn]) plus the LDS tile sizes (in blocks) of each pass.
+struct ExpertArgs {
+    uint32_t hidden, ffn, experts, top_k;
+    uint32_t type_gu, type_dn;
+    const void *const *gate;
+    const void *const *up;
+    const void *const *down;
+    PackedGeometry gu, dn;
+    uint32_t gu_tile, dn_tile;
+};
+
+size_t route_lds_bytes(uint32_t hidden, uint32_t experts);
+int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
+                 uint32_t *ids, float *weights, uint32_t *status, hipStream_t s);
+int prepare_expert_args(const fmx_moe_layer *L, ExpertArgs *a);
+// Decode experts for one token: gate/up + SwiGLU into act[top_k x ffn], then
+// down + combine + residual into out[hidden].
+// `mid`, when given, is recorded between the gate/up and the down launch.
+int launch_experts(const ExpertArgs &a, const float *x, const float *h, const uint32_t *ids,
+                   const float *w, float *act, float *out, uint32_t *status, hipStream_t s,
+                   hipEvent_t mid = nullptr);
+
+} // namespace fmx

@@ -1,0 +1,122 @@
+"""Seeded synthetic MoE layers and inputs in raw GGUF block layout.
+
+Shapes are the benchmark and test workloads of this path:
+
+  tiny           hidden 64, ffn 128, 4 experts, top-2, F32 weights ~N(0, 0.02)
+                 (the freemoe-tiny-v1 MoE block shape)
+  mixtral-q4_0   hidden 4096, ffn 14336, 8 experts, top-2, Q4_0 experts,
+                 decode at batch 1 (1000 tokens, one at a time)
+  mixtral-q8_0   same layer with Q8_0 experts, prefill of 512 tokens
+  finegrained    hidden 2048, ffn 768, 128 experts, top-8, Q4_K experts,
+                 2048 tokens, Zipf(s=1.2) router bias
+
+Weights: block scales d = f16(|N(0, 0.01)|) (Q4_K: d and dmin); Q4_0 nibbles
+and Q4_K nibbles / 6-bit scale codes uniform; Q8_0 quants uniform in
+-127..127. The F32 router is N(0, 1/hidden) so logits are ~N(0, 1); RMSNorm
+gains are 1 + N(0, 0.02). Inputs x ~ N(0, 1).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+F32, Q4_0, Q8_0, Q4_K = 0, 2, 8, 12
+GEOMETRY = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144)}
+TYPE_NAMES = {F32: "f32", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k"}
+
+
+def row_bytes(type_id: int, cols: int) -> int:
+    bs, bb = GEOMETRY[type_id]
+    if cols % bs:
+        raise ValueError(f"{cols} columns is not a whole number of {TYPE_NAMES[type_id]} blocks")
+    return cols // bs * bb
+
+
+def _half_scales(rng: np.random.Generator, n: int, sigma: float) -> np.ndarray:
+    return np.abs(rng.standard_normal(n) * sigma).astype(np.float16).view(np.uint8).reshape(n, 2)
+
+
+def matrix(type_id: int, rng: np.random.Generator, rows: int, cols: int, sigma: float = 0.01,
+           f32_sigma: float = 0.02) -> np.ndarray:
+    """A [rows x cols] weight matrix as raw GGUF bytes, shape (rows, row_bytes)."""
+    if type_id == F32:
+        return (rng.standard_normal((rows, cols), dtype=np.float32) * np.float32(f32_sigma)).view(np.uint8)
+    bs, bb = GEOMETRY[type_id]
+    nb = rows * (cols // bs)
+    if type_id == Q8_0:
+        w = np.empty((nb, bb), np.uint8)
+        w[:, 2:] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
+    else:
+        w = np.frombuffer(rng.bytes(nb * bb), np.uint8).reshape(nb, bb).copy()
+    w[:, 0:2] = _half_scales(rng, nb, sigma)
+    if type_id == Q4_K:
+        w[:, 2:4] = _half_scales(rng, nb, sigma)
+    return w.reshape(rows, -1)
+
+
+@dataclass
+class LayerWeights:
+    hidden: int
+    ffn: int
+    experts: int
+    top_k: int
+    gate_type: int
+    norm_weight: np.ndarray
+    router: np.ndarray                 # F32 [experts x hidden]
+    gate: list                         # per expert raw [ffn x row_bytes(hidden)]
+    up: list
+    down: list                         # per expert raw [hidden x row_bytes(ffn)]
+    router_bias: np.ndarray | None = None
+    rms_eps: float = float(np.float32(1e-5))
+    weights_norm: bool = True
+    seed: int = 0
+    notes: dict = field(default_factory=dict)
+
+    @property
+    def up_type(self):
+        return self.gate_type
+
+    @property
+    def down_type(self):
+        return self.gate_type
+
+
+def make_layer(hidden: int, ffn: int, experts: int, top_k: int, type_id: int, seed: int,
+               zipf_s: float | None = None) -> LayerWeights:
+    rng = np.random.default_rng(seed)
+    norm = (1.0 + rng.standard_normal(hidden) * 0.02).astype(np.float32)
+    router = (rng.standard_normal((experts, hidden)) / np.sqrt(hidden)).astype(np.float32)
+    bias = None
+    notes = {}
+    if zipf_s is not None:
+        ranks = rng.permutation(experts) + 1
+        bias = (-zipf_s * np.log(ranks)).astype(np.float32)
+        notes["router_bias"] = f"-{zipf_s}*ln(rank), ranks a seeded permutation of 1..{experts}"
+    gate, up, down = [], [], []
+    for _ in range(experts):
+        gate.append(matrix(type_id, rng, ffn, hidden))
+        up.append(matrix(type_id, rng, ffn, hidden))
+        down.append(matrix(type_id, rng, hidden, ffn))
+    return LayerWeights(hidden, ffn, experts, top_k, type_id, norm, router, gate, up, down, bias,
+                        seed=seed, notes=notes)
+
+
+def inputs(hidden: int, tokens: int, seed: int) -> np.ndarray:
+    return np.random.default_rng(seed).standard_normal((tokens, hidden), dtype=np.float32)
+
+
+WORKLOADS = {
+    "tiny": dict(hidden=64, ffn=128, experts=4, top_k=2, type_id=F32, tokens=64),
+    "mixtral-q4_0": dict(hidden=4096, ffn=14336, experts=8, top_k=2, type_id=Q4_0, tokens=1000),
+    "mixtral-q8_0": dict(hidden=4096, ffn=14336, experts=8, top_k=2, type_id=Q8_0, tokens=512),
+    "finegrained": dict(hidden=2048, ffn=768, experts=128, top_k=8, type_id=Q4_K, tokens=2048, zipf_s=1.2),
+}
+
+
+def workload(name: str, seed: int = 1234):
+    """(LayerWeights, x[tokens x hidden]) of a named workload."""
+    w = dict(WORKLOADS[name])
+    tokens = w.pop("tokens")
+    layer = make_layer(seed=seed, **w)
+    return layer, inputs(layer.hidden, tokens, seed + 1)

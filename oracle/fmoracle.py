@@ -1,0 +1,247 @@
+"""ctypes binding of the CPU oracle (libfmoracle.so) and of oracle/_ref/libfmref.so.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, as the checker. Nothing in freemoe_amd/ imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_double, c_float, c_int, c_uint16, c_uint32, c_uint64, c_void_p
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_PATH = HERE / "libfmoracle.so"
+REF_PATH = HERE / "_ref" / "libfmref.so"
+
+ISA_SCALAR, ISA_AVX2 = 0, 1
+TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K = 0, 2, 8, 12
+GEOMETRY = {TYPE_F32: (1, 4), TYPE_Q4_0: (32, 18), TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144)}
+
+
+class OracleError(RuntimeError):
+    def __init__(self, status: int, where: str):
+        self.status = status
+        super().__init__(f"{where}: status {status}")
+
+
+class Layer(ctypes.Structure):
+    _fields_ = [("hidden", c_uint32), ("ffn", c_uint32), ("experts", c_uint32), ("top_k", c_uint32),
+                ("norm_weight", c_void_p), ("rms_eps", c_double), ("norm_bias", c_double),
+                ("router_type", c_uint32), ("router", c_void_p), ("router_bias", c_void_p),
+                ("weights_norm", c_int), ("epsilon_additive", c_int), ("weights_epsilon", c_double),
+                ("weights_scale", c_double), ("gate_type", c_uint32), ("up_type", c_uint32),
+                ("down_type", c_uint32), ("gate", c_void_p), ("up", c_void_p), ("down", c_void_p)]
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(c_void_p)
+
+
+_oracle = None
+_ref = None
+
+
+def oracle() -> ctypes.CDLL:
+    global _oracle
+    if _oracle is None:
+        lib = ctypes.CDLL(str(ORACLE_PATH))
+        lib.fmo_fp16_to_f32.restype = c_float
+        lib.fmo_fp16_to_f32.argtypes = [c_uint16]
+        for name in ["fmo_dequantize_block", "fmo_dequantize_region", "fmo_gemv", "fmo_rmsnorm",
+                     "fmo_softmax", "fmo_topk", "fmo_route", "fmo_moe_layer", "fmo_moe_layer_batch",
+                     "fmo_moe_bucket", "fmo_quant_geometry"]:
+            getattr(lib, name).restype = c_int
+        lib.fmo_dequantize_region.argtypes = [c_uint32, c_void_p, c_void_p, c_uint64]
+        lib.fmo_gemv.argtypes = [c_int, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]
+        lib.fmo_rmsnorm.argtypes = [c_void_p, c_void_p, c_uint32, c_double, c_double, c_void_p]
+        lib.fmo_softmax.argtypes = [c_void_p, c_uint32, c_void_p]
+        lib.fmo_topk.argtypes = [c_void_p, c_uint32, c_uint32, c_void_p]
+        lib.fmo_route.argtypes = [c_int, POINTER(Layer), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                  c_void_p]
+        lib.fmo_moe_layer.argtypes = [c_int, POINTER(Layer), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                      c_void_p]
+        lib.fmo_moe_layer_batch.argtypes = [c_int, POINTER(Layer), c_void_p, c_void_p, c_void_p, c_void_p,
+                                            c_uint32]
+        lib.fmo_moe_bucket.argtypes = [c_void_p, c_uint32, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p]
+        _oracle = lib
+    return _oracle
+
+
+def ref_available() -> bool:
+    return REF_PATH.exists()
+
+
+def ref() -> ctypes.CDLL:
+    """The reference's own kernels (built from the FreeMoe sources by oracle/Makefile)."""
+    global _ref
+    if _ref is None:
+        lib = ctypes.CDLL(str(REF_PATH))
+        lib.fmr_fp16_to_f32.restype = c_float
+        lib.fmr_fp16_to_f32.argtypes = [c_uint16]
+        lib.fmr_dequantize_block.argtypes = [c_uint32, c_void_p, c_void_p]
+        lib.fmr_gemv.argtypes = [c_int, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]
+        lib.fmr_moe_layer_batch.argtypes = [c_int, c_uint32, POINTER(Layer), c_void_p, c_void_p, c_void_p,
+                                            c_void_p, c_uint32]
+        lib.fmr_resolved_threads.restype = c_uint32
+        lib.fmr_resolved_threads.argtypes = [c_uint32]
+        _ref = lib
+    return _ref
+
+
+def check(rc: int, where: str) -> None:
+    if rc != 0:
+        raise OracleError(rc, where)
+
+
+# ----------------------------------------------------------------- kernels --
+
+def fp16_to_f32(h: int) -> float:
+    return oracle().fmo_fp16_to_f32(h)
+
+
+def dequantize(type_id: int, raw: np.ndarray, count: int) -> np.ndarray:
+    out = np.empty(count, np.float32)
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    check(oracle().fmo_dequantize_region(type_id, _p(raw), _p(out), count), "fmo_dequantize_region")
+    return out
+
+
+def gemv(type_id: int, w: np.ndarray, x: np.ndarray, out_dim: int, in_dim: int, isa: int = ISA_AVX2) -> np.ndarray:
+    y = np.empty(out_dim, np.float32)
+    w = np.ascontiguousarray(w)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    check(oracle().fmo_gemv(isa, type_id, _p(w), _p(x), _p(y), out_dim, in_dim), "fmo_gemv")
+    return y
+
+
+def ref_gemv(type_id: int, w: np.ndarray, x: np.ndarray, out_dim: int, in_dim: int, isa: int = ISA_AVX2,
+             threads: int = 1) -> np.ndarray:
+    y = np.empty(out_dim, np.float32)
+    w = np.ascontiguousarray(w)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    check(ref().fmr_gemv(isa, threads, type_id, _p(w), _p(x), _p(y), out_dim, in_dim), "fmr_gemv")
+    return y
+
+
+def rmsnorm(x: np.ndarray, w, eps: float, norm_bias: float = 0.0) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    w = None if w is None else np.ascontiguousarray(w, np.float32)
+    check(oracle().fmo_rmsnorm(_p(x), _p(w), x.size, eps, norm_bias, _p(y)), "fmo_rmsnorm")
+    return y
+
+
+def softmax(v: np.ndarray) -> np.ndarray:
+    v = np.ascontiguousarray(v, np.float32)
+    out = np.empty_like(v)
+    check(oracle().fmo_softmax(_p(v), v.size, _p(out)), "fmo_softmax")
+    return out
+
+
+def topk(scores: np.ndarray, k: int) -> np.ndarray:
+    s = np.ascontiguousarray(scores, np.float32)
+    ids = np.empty(max(k, 1), np.uint32)
+    check(oracle().fmo_topk(_p(s), s.size, k, _p(ids)), "fmo_topk")
+    return ids[:k]
+
+
+def bucket(ids: np.ndarray, experts: int):
+    ids = np.ascontiguousarray(ids, np.uint32)
+    tokens, k = ids.shape
+    offsets = np.empty(experts + 1, np.uint32)
+    tl = np.empty(max(tokens * k, 1), np.uint32)
+    rl = np.empty(max(tokens * k, 1), np.uint32)
+    check(oracle().fmo_moe_bucket(_p(ids), tokens, k, experts, _p(offsets), _p(tl), _p(rl)), "fmo_moe_bucket")
+    return offsets, tl[:tokens * k], rl[:tokens * k]
+
+
+# ------------------------------------------------------------------- layer --
+
+class HostLayer:
+    """A MoE layer held in host memory in raw GGUF block layout."""
+
+    def __init__(self, *, hidden, ffn, experts, top_k, norm_weight, rms_eps, router, gate, up, down,
+                 gate_type, up_type=None, down_type=None, router_type=TYPE_F32, router_bias=None,
+                 norm_bias=0.0, weights_norm=True, epsilon_additive=False, weights_epsilon=6.103515625e-5,
+                 weights_scale=1.0):
+        self.hidden, self.ffn, self.experts, self.top_k = hidden, ffn, experts, top_k
+        self.norm_weight = None if norm_weight is None else np.ascontiguousarray(norm_weight, np.float32)
+        self.rms_eps, self.norm_bias = rms_eps, norm_bias
+        self.router_type = router_type
+        self.router = np.ascontiguousarray(router)
+        self.router_bias = None if router_bias is None else np.ascontiguousarray(router_bias, np.float32)
+        self.weights_norm, self.epsilon_additive = weights_norm, epsilon_additive
+        self.weights_epsilon, self.weights_scale = weights_epsilon, weights_scale
+        self.gate_type = gate_type
+        self.up_type = gate_type if up_type is None else up_type
+        self.down_type = gate_type if down_type is None else down_type
+        self.gate = [np.ascontiguousarray(g) for g in gate]
+        self.up = [np.ascontiguousarray(u) for u in up]
+        self.down = [np.ascontiguousarray(d) for d in down]
+        self._ptrs = [(ctypes.c_void_p * experts)(*[g.ctypes.data for g in arr]) for arr in (self.gate, self.up, self.down)]
+
+    def struct(self) -> Layer:
+        return Layer(self.hidden, self.ffn, self.experts, self.top_k, _p(self.norm_weight), self.rms_eps,
+                     self.norm_bias, self.router_type, _p(self.router), _p(self.router_bias),
+                     int(self.weights_norm), int(self.epsilon_additive), self.weights_epsilon, self.weights_scale,
+                     self.gate_type, self.up_type, self.down_type,
+                     ctypes.cast(self._ptrs[0], c_void_p), ctypes.cast(self._ptrs[1], c_void_p),
+                     ctypes.cast(self._ptrs[2], c_void_p))
+
+    def route(self, x: np.ndarray, isa: int = ISA_AVX2):
+        x = np.ascontiguousarray(x, np.float32)
+        h = np.empty(self.hidden, np.float32)
+        logits = np.empty(self.experts, np.float32)
+        probs = np.empty(self.experts, np.float32)
+        ids = np.empty(self.top_k, np.uint32)
+        w = np.empty(self.top_k, np.float32)
+        L = self.struct()
+        check(oracle().fmo_route(isa, ctypes.byref(L), _p(x), _p(h), _p(logits), _p(probs), _p(ids), _p(w)),
+              "fmo_route")
+        return h, logits, probs, ids, w
+
+    def forward(self, x: np.ndarray, isa: int = ISA_AVX2):
+        """One token: (out, ids, weights, h, act[top_k x ffn])."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(self.hidden, np.float32)
+        ids = np.empty(self.top_k, np.uint32)
+        w = np.empty(self.top_k, np.float32)
+        h = np.empty(self.hidden, np.float32)
+        act = np.empty((self.top_k, self.ffn), np.float32)
+        L = self.struct()
+        check(oracle().fmo_moe_layer(isa, ctypes.byref(L), _p(x), _p(out), _p(ids), _p(w), _p(h), _p(act)),
+              "fmo_moe_layer")
+        return out, ids, w, h, act
+
+    def forward_batch(self, x: np.ndarray, isa: int = ISA_AVX2):
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.hidden)
+        t = x.shape[0]
+        out = np.empty_like(x)
+        ids = np.empty((t, self.top_k), np.uint32)
+        w = np.empty((t, self.top_k), np.float32)
+        L = self.struct()
+        check(oracle().fmo_moe_layer_batch(isa, ctypes.byref(L), _p(x), _p(out), _p(ids), _p(w), t),
+              "fmo_moe_layer_batch")
+        return out, ids, w
+
+    def ref_forward_batch(self, x: np.ndarray, isa: int = ISA_AVX2, threads: int = 0):
+        """The same layer through the reference's own kernels (libfmref)."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.hidden)
+        t = x.shape[0]
+        out = np.empty_like(x)
+        ids = np.empty((t, self.top_k), np.uint32)
+        w = np.empty((t, self.top_k), np.float32)
+        L = self.struct()
+        check(ref().fmr_moe_layer_batch(isa, threads, ctypes.byref(L), _p(x), _p(out), _p(ids), _p(w), t),
+              "fmr_moe_layer_batch")
+        return out, ids, w
+
+
+def host_layer(lw) -> HostLayer:
+    """HostLayer from freemoe_amd.workloads.LayerWeights (same arrays, no copies)."""
+    return HostLayer(hidden=lw.hidden, ffn=lw.ffn, experts=lw.experts, top_k=lw.top_k,
+                     norm_weight=lw.norm_weight, rms_eps=lw.rms_eps, router=lw.router.view(np.uint8),
+                     router_bias=lw.router_bias, gate=lw.gate, up=lw.up, down=lw.down,
+                     gate_type=lw.gate_type, weights_norm=lw.weights_norm)
