@@ -43,21 +43,43 @@ def algorithmic_bytes(H, F, E, K, row_bytes_h, row_bytes_f):
     return gate_up, down, route
 
 
-def cpu_baseline(lw, x, target_s=12.0, max_tokens=256):
+def cpu_baseline(lw, x, target_s=15.0, max_tokens=256):
+    """The reference's own kernels on the host, one token at a time, until
+    target_s seconds or max_tokens tokens have run.
+
+    Two threads: the reference's WorkerPool (kernels.cpp:414-459) publishes
+    `pending = ranges - 1` into every worker's slot, each worker decrements only
+    its own slot, and the caller waits for worker 0's slot to reach zero, so a
+    split into more than two ranges never completes. Two threads (one range
+    each for the caller and worker 0) is the largest count that finishes; it is
+    also the thread count of the reference's own 2-vCPU test machine."""
     sys.path.insert(0, str(ROOT / "oracle"))
+    import numpy as np
     import fmoracle as fo
     hl = fo.host_layer(lw)
-    threads = int(fo.ref().fmr_resolved_threads(0))
+    threads = 2
+    outs, idss, ws = [], [], []
+    hl.ref_forward_batch(x[:1], fo.ISA_AVX2, threads=threads)  # wakes the worker pool
     t0 = time.perf_counter()
-    out, ids, w = hl.ref_forward_batch(x[:4], fo.ISA_AVX2, threads=0)
-    per_tok = (time.perf_counter() - t0) / 4
-    n = int(max(8, min(max_tokens, target_s / max(per_tok, 1e-6))))
-    t0 = time.perf_counter()
-    out, ids, w = hl.ref_forward_batch(x[:n], fo.ISA_AVX2, threads=0)
+    last = t0
+    n = 0
+    while n < min(max_tokens, len(x)):
+        o, i, w = hl.ref_forward_batch(x[n:n + 1], fo.ISA_AVX2, threads=threads)
+        outs.append(o)
+        idss.append(i)
+        ws.append(w)
+        n += 1
+        now = time.perf_counter()
+        if now - last > 5.0:
+            print(f"[bench] cpu baseline: {n} tokens in {now - t0:.1f}s", file=sys.stderr, flush=True)
+            last = now
+        if now - t0 > target_s:
+            break
     dt = time.perf_counter() - t0
-    return {"value": n / dt, "unit": "tokens/s", "cores": threads, "kind": "reference",
-            "sample": f"first {n} of the 1000 tokens, reference gemv/gemv_quant (KernelIsa::Auto = AVX2, "
-                      f"WorkerPool {threads} threads) composed in the engine's MoE order"}, (out, ids, w, n)
+    return {"value": round(n / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "reference",
+            "sample": f"first {n} of the 1000 tokens, one at a time, through the reference's gemv/gemv_quant "
+                      f"(KernelIsa::Auto = AVX2+FMA, WorkerPool {threads} threads) in the engine's MoE order"}, \
+        (np.concatenate(outs), np.concatenate(idss), np.concatenate(ws), n)
 
 
 def main() -> int:
@@ -67,6 +89,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--tokens", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-bytes", type=int, default=0,
+                    help="also run one plain device-to-device copy of this many bytes (a known-traffic "
+                         "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -102,6 +127,13 @@ def main() -> int:
     dl.ensure_workspace(T)
     torch.cuda.synchronize()
 
+    if args.copy_bytes:
+        src = torch.ones(args.copy_bytes // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     for _ in range(args.warmup):
         dl.decode(xd, out, ids, wts)
     torch.cuda.synchronize()
@@ -121,6 +153,7 @@ def main() -> int:
     print(f"[bench] timed {args.steps} steps: {ms_per_step:.3f} ms/step", file=sys.stderr, flush=True)
 
     # per-kernel durations with HIP events on the launch stream
+    print("[bench] per-kernel event timing", file=sys.stderr, flush=True)
     kernel_ms = (ctypes.c_double * 3)()
     ws = dl.workspace
     fmx.call("fmx_moe_decode_timed", ctypes.byref(dl.desc), xd.data_ptr(), out.data_ptr(), T, ids.data_ptr(),
@@ -130,6 +163,13 @@ def main() -> int:
     rb_f = fmx.raw_row_bytes(lw.down_type, F)
     gu_bytes, dn_bytes, route_bytes = algorithmic_bytes(H, F, E, K, rb_h, rb_f)
     achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    traffic = None
+    try:
+        measured = json.loads((ROOT / "profiles" / "traffic.json").read_text())
+        traffic = measured.get(WORKLOAD, {}).get(f"gate_up_kernel<{wl.TYPE_NAMES[lw.gate_type].upper()}>",
+                                                  {}).get("bytes")
+    except (OSError, ValueError):
+        pass
 
     result = {
         "metric": METRIC,
@@ -149,7 +189,7 @@ def main() -> int:
                    "tokens_per_step": T, "seed": seed},
         "roofline": {"bound": "hbm", "kernel": "gate_up_kernel<Q4_0>", "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": None, "bytes_per_launch": gu_bytes, "mean_us": round(gu_us, 3)},
+                     "traffic": traffic, "bytes_per_launch": gu_bytes, "mean_us": round(gu_us, 3)},
         "kernels_us_per_token": {"route": round(route_us, 3), "gate_up": round(gu_us, 3),
                                  "down": round(dn_us, 3),
                                  "down_GBs": round(dn_bytes / (dn_us * 1e-6) / 1e9, 1)},
@@ -161,6 +201,7 @@ def main() -> int:
 
     if not args.no_cpu_baseline:
         try:
+            print("[bench] cpu baseline", file=sys.stderr, flush=True)
             base, (rout, rids, rw, n) = cpu_baseline(lw, x)
             result["cpu_baseline"] = base
             go = out[:n].cpu().numpy()
