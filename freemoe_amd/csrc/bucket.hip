@@ -26,7 +26,7 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     const uint32_t *__restrict__ ids, uint32_t tokens, uint32_t K, uint32_t E,
     uint32_t *__restrict__ offsets, uint32_t *__restrict__ token_list,
     uint32_t *__restrict__ rank_list, uint32_t *__restrict__ slot_of, uint32_t *__restrict__ status) {
-    extern __shared__ uint32_t sm[];
+    extern __shared__ __align__(16) uint32_t sm[];
     uint32_t *count = sm;                  // [E]
     uint32_t *base = count + E;            // [E]
     uint32_t *mask = base + E;             // [E][kWords]

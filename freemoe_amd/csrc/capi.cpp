@@ -24,7 +24,7 @@ struct Fence {
 
 // Workspace layout of the MoE entry points (all offsets 256-byte aligned):
 //   [0, 256)     error word (uint32)
-//   h            tokens x hidden floats (decode: one token)
+//   h            hidden floats (decode: one token)
 //   act          top_k x ffn floats (decode)
 struct DecodeWorkspace {
     uint64_t h = 0, act = 0, total = 0;
@@ -38,14 +38,18 @@ DecodeWorkspace decode_workspace(const fmx_moe_layer *L) {
     return w;
 }
 
+// Zeroes the error word with a kernel, not a memset, so a caller may capture
+// the sequence in a HIP graph.
 __global__ void clear_word_kernel(uint32_t *word) { *word = 0; }
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int validate_layer(const fmx_moe_layer *L) {
     if (!L) return FMX_ERR_INVALID_ARGUMENT;
     if (L->hidden == 0 || L->ffn == 0 || L->experts == 0 || L->top_k == 0) return FMX_ERR_INVALID_ARGUMENT;
     if (L->top_k > L->experts) return FMX_ERR_INVALID_ARGUMENT;      // engine.cpp:408
-    if (L->top_k > 32 || L->experts > 1024) return FMX_ERR_INVALID_ARGUMENT;
-    if (L->hidden > 16384) return FMX_ERR_SHAPE_MISMATCH;             // route kernel LDS
+    if (L->top_k > 32 || L->experts > 256) return FMX_ERR_INVALID_ARGUMENT;
+    if (L->hidden > 16384 || L->hidden % 4) return FMX_ERR_SHAPE_MISMATCH; // routing stages x as float4
     if (!L->router || !L->gate || !L->up || !L->down) return FMX_ERR_INVALID_ARGUMENT;
     if (L->router_type != FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
     return FMX_OK;
@@ -290,6 +294,7 @@ int fmx_moe_route(const fmx_moe_layer *L, const float *x, uint32_t tokens, float
     if (int rc = validate_layer(L)) return rc;
     if (tokens == 0) return FMX_OK;
     if (!x || !ids || !weights || !workspace || workspace_bytes < kStatusBytes) return FMX_ERR_INVALID_ARGUMENT;
+    if (!aligned16(x)) return FMX_ERR_INVALID_ARGUMENT;
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint32_t *status = static_cast<uint32_t *>(workspace);
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
@@ -303,6 +308,7 @@ int fmx_moe_decode(const fmx_moe_layer *L, const float *x, float *out, uint32_t 
     if (int rc = validate_layer(L)) return rc;
     if (tokens == 0) return FMX_OK;
     if (!x || !out || !ids || !weights || !workspace) return FMX_ERR_INVALID_ARGUMENT;
+    if (!aligned16(x) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
     const DecodeWorkspace ws = decode_workspace(L);
     if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
     ExpertArgs ea;
@@ -312,13 +318,14 @@ int fmx_moe_decode(const fmx_moe_layer *L, const float *x, float *out, uint32_t 
     uint8_t *base = static_cast<uint8_t *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(base);
     float *h = reinterpret_cast<float *>(base + ws.h);
-    float *act = reinterpret_cast<float *>(base + ws.act);
+    DecodeScratch sc;
+    sc.act = reinterpret_cast<float *>(base + ws.act);
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
     FMX_LAUNCH_CHECK();
     const uint64_t H = L->hidden, K = L->top_k;
     for (uint32_t t = 0; t < tokens; ++t) {
-        if (int rc = launch_route(ra, x + t * H, 1, h, nullptr, ids + t * K, weights + t * K, status, s)) return rc;
-        if (int rc = launch_experts(ea, x + t * H, h, ids + t * K, weights + t * K, act, out + t * H, status, s))
+        if (int rc = launch_route_decode(ra, x + t * H, h, ids + t * K, weights + t * K, status, s)) return rc;
+        if (int rc = launch_experts(ea, x + t * H, h, ids + t * K, weights + t * K, sc, out + t * H, status, s))
             return rc;
     }
     return FMX_OK;
@@ -339,10 +346,12 @@ int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uin
     if (int rc = prepare_expert_args(L, &ea)) return rc;
     const RouteArgs ra = route_args(L);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (!aligned16(x) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
     uint8_t *base = static_cast<uint8_t *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(base);
     float *h = reinterpret_cast<float *>(base + ws.h);
-    float *act = reinterpret_cast<float *>(base + ws.act);
+    DecodeScratch sc;
+    sc.act = reinterpret_cast<float *>(base + ws.act);
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
     FMX_LAUNCH_CHECK();
     // events in batches: [token][route start, route end = experts start, gate/up end, down end]
@@ -357,10 +366,10 @@ int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uin
         for (uint32_t i = 0; i < n && rc == FMX_OK; ++i) {
             const uint64_t t = t0 + i;
             (void)hipEventRecord(ev[i][0], s);
-            rc = launch_route(ra, x + t * H, 1, h, nullptr, ids + t * K, weights + t * K, status, s);
+            rc = launch_route_decode(ra, x + t * H, h, ids + t * K, weights + t * K, status, s);
             (void)hipEventRecord(ev[i][1], s);
             if (rc == FMX_OK)
-                rc = launch_experts(ea, x + t * H, h, ids + t * K, weights + t * K, act, out + t * H, status, s,
+                rc = launch_experts(ea, x + t * H, h, ids + t * K, weights + t * K, sc, out + t * H, status, s,
                                     ev[i][2]);
             (void)hipEventRecord(ev[i][3], s);
         }

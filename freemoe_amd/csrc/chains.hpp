@@ -16,6 +16,40 @@
 
 namespace fmx {
 
+// ------------------------------------------------------------- staging --
+// Copies elements [e0, e0 + n) of x (n a multiple of 4, x + e0 16-byte
+// aligned) into LDS in a lane-major order: element i goes to float
+// slot(i) * 4 + (i % 32) / 8, where a slot (16 bytes) holds the four elements
+// of a 32-element run that lane i % 8 consumes. All of a thread's global
+// loads (up to 8 float4) are in flight together; consecutive elements land in
+// consecutive lanes' slots, kLaneSlots slots apart.
+template <uint32_t kLaneSlots, class Slot>
+__device__ __forceinline__ void scatter_lanes(const float *__restrict__ x, uint32_t e0, uint32_t n, float *lds,
+                                              uint32_t tid, uint32_t nthreads, Slot slot) {
+    const float4 *src = reinterpret_cast<const float4 *>(x + e0);
+    const uint32_t n4 = n / 4;
+    for (uint32_t i0 = tid; i0 < n4; i0 += 8 * nthreads) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t i = i0 + u * nthreads;
+            v[u] = src[i < n4 ? i : n4 - 1];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t i = i0 + u * nthreads;
+            if (i < n4) {
+                const uint32_t e = 4 * i;
+                float *d = lds + slot(e) * 4 + ((e & 31) >> 3);
+                d[0] = v[u].x;
+                d[4 * kLaneSlots] = v[u].y;
+                d[8 * kLaneSlots] = v[u].z;
+                d[12 * kLaneSlots] = v[u].w;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- Q4_0 --
 // Block = 32 elements; chunk = 8 blocks (one 16-byte lane load per row).
 // LDS per block: 8 lanes x float4 x-values, then 8 floats of 8*sum(x).
@@ -25,18 +59,20 @@ struct Q40 {
     static constexpr uint32_t kPerChunk = 8;
     static constexpr uint32_t kLdsFloatsPerBlock = 40;
 
-    // Stage blocks [b0, b0 + nb) of x into lds (xs: nb*32 floats, s8: nb*8).
+    // Stage blocks [b0, b0 + nb) of x into lds (xs: nb*32 floats, s8: nb*8):
+    // xs[b][l] = (x[l], x[8+l], x[16+l], x[24+l]) of block b, then per (b, l)
+    // 8 * ((x[l] + x[8+l]) + (x[16+l] + x[24+l])) (the scaling is exact). The
+    // caller's barrier after stage() publishes the sums.
     __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb,
                                  float *lds, uint32_t tid, uint32_t nthreads) {
-        float4 *xs = reinterpret_cast<float4 *>(lds);
+        scatter_lanes<1>(x, b0 * 32, nb * 32, lds, tid, nthreads,
+                      [](uint32_t e) { return (e >> 5) * 8 + (e & 7); });
+        __syncthreads();
+        const float4 *xs = reinterpret_cast<const float4 *>(lds);
         float *s8 = lds + nb * 32;
         for (uint32_t e = tid; e < nb * 8; e += nthreads) {
-            const uint32_t b = e >> 3, l = e & 7;
-            const float *xb = x + static_cast<uint64_t>(b0 + b) * 32;
-            const float x0 = xb[l], x1 = xb[8 + l], x2 = xb[16 + l], x3 = xb[24 + l];
-            xs[e] = make_float4(x0, x1, x2, x3);
-            // 8 * ((x[l] + x[8+l]) + (x[16+l] + x[24+l])): the scaling is exact
-            s8[e] = 8.0f * ((x0 + x1) + (x2 + x3));
+            const float4 v = xs[e];
+            s8[e] = 8.0f * ((v.x + v.y) + (v.z + v.w));
         }
     }
 
@@ -65,29 +101,36 @@ struct Q40 {
     }
 
     // Blocks j < nblk of chunk `k` (block index within the LDS tile: tb0 + j).
-    template <int NR>
+    // FULL: all kPerChunk blocks are present, so the LDS reads of the whole
+    // chunk are issued before the arithmetic.
+    template <int NR, bool FULL = false>
     __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t nb_tile,
                                 uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
-        const float4 *xs = reinterpret_cast<const float4 *>(lds);
-        const float *s8 = lds + nb_tile * 32;
+        const float4 *xs = reinterpret_cast<const float4 *>(lds) + tb0 * 8 + l;
+        const float *s8 = lds + nb_tile * 32 + tb0 * 8 + l;
+        float4 xv[8];
+        float sx8[8];
+#pragma unroll
+        for (uint32_t j = 0; j < 8; ++j) {
+            const uint32_t jr = FULL || j < nblk ? j : 0;
+            xv[j] = xs[jr * 8];
+            sx8[j] = s8[jr * 8];
+        }
 #pragma unroll
         for (uint32_t jj = 0; jj < 4; ++jj) {
             // dword jj holds blocks 2jj and 2jj+1: bytes (A, B, A', B')
-            uint32_t qw[NR], lo4[NR], hi4[NR], sw[NR];
+            uint32_t lo4[NR], hi4[NR], sw[NR];
 #pragma unroll
             for (int i = 0; i < NR; ++i) {
-                qw[i] = jj == 0 ? k[i].q.x : jj == 1 ? k[i].q.y : jj == 2 ? k[i].q.z : k[i].q.w;
+                const uint32_t qw = jj == 0 ? k[i].q.x : jj == 1 ? k[i].q.y : jj == 2 ? k[i].q.z : k[i].q.w;
                 sw[i] = jj == 0 ? k[i].s.x : jj == 1 ? k[i].s.y : jj == 2 ? k[i].s.z : k[i].s.w;
-                lo4[i] = qw[i] & 0x0F0F0F0Fu;
-                hi4[i] = (qw[i] >> 4) & 0x0F0F0F0Fu;
+                lo4[i] = qw & 0x0F0F0F0Fu;
+                hi4[i] = (qw >> 4) & 0x0F0F0F0Fu;
             }
 #pragma unroll
             for (uint32_t h = 0; h < 2; ++h) {
                 const uint32_t j = 2 * jj + h;
-                if (j >= nblk) break;
-                const uint32_t e = (tb0 + j) * 8 + l;
-                const float4 xv = xs[e];
-                const float sx8 = s8[e];
+                if (!FULL && j >= nblk) break;
 #pragma unroll
                 for (int i = 0; i < NR; ++i) {
                     const float qa = h ? ubyte2(lo4[i]) : ubyte0(lo4[i]);
@@ -95,9 +138,9 @@ struct Q40 {
                     const float qc = h ? ubyte2(hi4[i]) : ubyte0(hi4[i]);
                     const float qd = h ? ubyte3(hi4[i]) : ubyte1(hi4[i]);
                     // lo = fma(q[l], x[l], q[8+l]*x[8+l]); hi likewise for 16+l, 24+l
-                    const float lo = fma_rn(qa, xv.x, qb * xv.y);
-                    const float hi = fma_rn(qc, xv.z, qd * xv.w);
-                    const float c = (lo + hi) - sx8;
+                    const float lo = fma_rn(qa, xv[j].x, qb * xv[j].y);
+                    const float hi = fma_rn(qc, xv[j].z, qd * xv[j].w);
+                    const float c = (lo + hi) - sx8[j];
                     const float d = half_bits_to_float(h ? (sw[i] >> 16) : (sw[i] & 0xFFFFu));
                     t[i] = fma_rn(c, d, t[i]);
                 }
@@ -117,14 +160,12 @@ struct Q80 {
     static constexpr uint32_t kPerChunk = 4;
     static constexpr uint32_t kLdsFloatsPerBlock = 32;
 
+    // xs[b][l] = (x[l], x[8+l], x[16+l], x[24+l]) of block b.
     __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb,
                                  float *lds, uint32_t tid, uint32_t nthreads) {
-        float4 *xs = reinterpret_cast<float4 *>(lds);
-        for (uint32_t e = tid; e < nb * 8; e += nthreads) {
-            const uint32_t b = e >> 3, l = e & 7;
-            const float *xb = x + static_cast<uint64_t>(b0 + b) * 32;
-            xs[e] = make_float4(xb[l], xb[8 + l], xb[16 + l], xb[24 + l]);
-        }
+        scatter_lanes<1>(x, b0 * 32, nb * 32, lds, tid, nthreads,
+                      [](uint32_t e) { return (e >> 5) * 8 + (e & 7); });
+        __syncthreads();
     }
 
     struct Row {
@@ -146,7 +187,7 @@ struct Q80 {
     __device__ static Chunk load(const Row &w, uint32_t c) {
         Chunk k;
         k.q = ld16(w.quants + static_cast<uint64_t>(c) * 128);
-        k.s = *reinterpret_cast<const uint2 *>(w.scales + static_cast<uint64_t>(c) * 8);
+        k.s = ld8(w.scales + static_cast<uint64_t>(c) * 8);
         return k;
     }
 
@@ -154,23 +195,25 @@ struct Q80 {
         return static_cast<float>(static_cast<int32_t>(w << (24 - 8 * k)) >> 24);
     }
 
-    template <int NR>
+    template <int NR, bool FULL = false>
     __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t /*nb_tile*/,
                                 uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
-        const float4 *xs = reinterpret_cast<const float4 *>(lds);
+        const float4 *xs = reinterpret_cast<const float4 *>(lds) + tb0 * 8 + l;
+        float4 xv[4];
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) xv[j] = xs[(FULL || j < nblk ? j : 0) * 8];
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
-            if (j >= nblk) break;
-            const float4 xv = xs[(tb0 + j) * 8 + l];
+            if (!FULL && j >= nblk) break;
 #pragma unroll
             for (int i = 0; i < NR; ++i) {
                 const uint32_t w = j == 0 ? k[i].q.x : j == 1 ? k[i].q.y : j == 2 ? k[i].q.z : k[i].q.w;
                 const uint32_t sw = j < 2 ? k[i].s.x : k[i].s.y;
                 // acc over elements l, 8+l, 16+l, 24+l from zero, then t += acc*d (both FMA)
-                float acc = fma_rn(sbyte(w, 0), xv.x, 0.0f);
-                acc = fma_rn(sbyte(w, 1), xv.y, acc);
-                acc = fma_rn(sbyte(w, 2), xv.z, acc);
-                acc = fma_rn(sbyte(w, 3), xv.w, acc);
+                float acc = fma_rn(sbyte(w, 0), xv[j].x, 0.0f);
+                acc = fma_rn(sbyte(w, 1), xv[j].y, acc);
+                acc = fma_rn(sbyte(w, 2), xv[j].z, acc);
+                acc = fma_rn(sbyte(w, 3), xv[j].w, acc);
                 const float d = half_bits_to_float((j & 1) ? (sw >> 16) : (sw & 0xFFFFu));
                 t[i] = fma_rn(acc, d, t[i]);
             }
@@ -190,25 +233,29 @@ struct Q4K {
     static constexpr uint32_t kPerChunk = 1;
     static constexpr uint32_t kLdsFloatsPerBlock = 264;
 
+    // Per super-block and group g: slots (g, l, half) hold x[64g + 32 half + 8k + l],
+    // k = 0..3; then per (super-block, g) the low and high 32-element sums in
+    // the reference's order (per-lane sums of four, then the 8-lane tree). The
+    // caller's barrier after stage() publishes the sums.
     __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb,
                                  float *lds, uint32_t tid, uint32_t nthreads) {
-        float4 *xs = reinterpret_cast<float4 *>(lds);
+        // element e of the tile: super-block e/256, group (e%256)/64, half (e%64)/32
+        scatter_lanes<2>(x, b0 * 256, nb * 256, lds, tid, nthreads, [](uint32_t e) {
+            return (((e >> 6) * 8 + (e & 7)) * 2) + ((e >> 5) & 1);
+        });
+        __syncthreads();
+        const float4 *xs = reinterpret_cast<const float4 *>(lds);
         float *sums = lds + nb * 256;
-        for (uint32_t e = tid; e < nb * 32; e += nthreads) {
-            const uint32_t b = e >> 5, g = (e >> 3) & 3, l = e & 7;
-            const float *xg = x + static_cast<uint64_t>(b0 + b) * 256 + 64 * g;
-            xs[2 * e] = make_float4(xg[l], xg[8 + l], xg[16 + l], xg[24 + l]);
-            xs[2 * e + 1] = make_float4(xg[32 + l], xg[40 + l], xg[48 + l], xg[56 + l]);
-        }
-        for (uint32_t e = tid; e < nb * 4; e += nthreads) {
-            const float *xg = x + static_cast<uint64_t>(b0 + (e >> 2)) * 256 + 64 * (e & 3);
-            float lo[8], hi[8];
+        for (uint32_t e = tid; e < nb * 8; e += nthreads) {
+            // e = (super-block, group) * 2 + half
+            const uint32_t sg = e >> 1, half = e & 1;
+            float v[8];
+#pragma unroll
             for (int l = 0; l < 8; ++l) {
-                lo[l] = (xg[l] + xg[8 + l]) + (xg[16 + l] + xg[24 + l]);
-                hi[l] = (xg[32 + l] + xg[40 + l]) + (xg[48 + l] + xg[56 + l]);
+                const float4 q = xs[(sg * 8 + l) * 2 + half];
+                v[l] = (q.x + q.y) + (q.z + q.w);
             }
-            sums[2 * e] = ((lo[0] + lo[4]) + (lo[1] + lo[5])) + ((lo[2] + lo[6]) + (lo[3] + lo[7]));
-            sums[2 * e + 1] = ((hi[0] + hi[4]) + (hi[1] + hi[5])) + ((hi[2] + hi[6]) + (hi[3] + hi[7]));
+            sums[e] = ((v[0] + v[4]) + (v[1] + v[5])) + ((v[2] + v[6]) + (v[3] + v[7]));
         }
     }
 
@@ -234,10 +281,10 @@ struct Q4K {
         return k;
     }
 
-    template <int NR>
+    template <int NR, bool FULL = false>
     __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t nb_tile,
                                 uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
-        if (nblk == 0) return;
+        if (!FULL && nblk == 0) return;
         const float4 *xs = reinterpret_cast<const float4 *>(lds);
         const float *sums = lds + nb_tile * 256;
 #pragma unroll
@@ -315,13 +362,64 @@ __device__ __forceinline__ void run_chunks_pf(const typename T::Row (&rows)[NR],
     }
 }
 
-// Blocks per LDS tile: a whole number of chunks, at most `budget_floats` of LDS.
+// A row stream with PF chunks per row in flight across LDS tiles: prime()
+// requests chunks 0..PF-1 (before the first tile is staged, so the weight
+// loads overlap the staging); run() consumes chunks [c0, c1) of the current
+// tile and keeps requesting chunk c + PF up to the row's last chunk, so the
+// loads of the next tile are already in flight when its staging starts.
+// The chunks live in a ring of kSlots = PF + 1 register slots: the load for
+// chunk c + PF goes into the slot chunk c - 1 just left, before chunk c is
+// consumed, with every slot index a compile-time constant. Every tile must
+// start at a multiple of kSlots chunks.
+template <class T, int NR, int PF>
+struct ChunkStream {
+    static constexpr int kSlots = PF + 1;
+    typename T::Chunk buf[kSlots][NR];
+
+    __device__ __forceinline__ void prime(const typename T::Row (&rows)[NR], uint32_t c_end) {
+#pragma unroll
+        for (int p = 0; p < PF; ++p)
+            if (static_cast<uint32_t>(p) < c_end) {
+#pragma unroll
+                for (int i = 0; i < NR; ++i) buf[p][i] = T::load(rows[i], p);
+            }
+    }
+
+    __device__ __forceinline__ void run(const typename T::Row (&rows)[NR], uint32_t c0, uint32_t c1,
+                                        uint32_t c_end, uint32_t blocks, uint32_t tile_b0,
+                                        uint32_t nb_tile, const float *lds, uint32_t l, float (&t)[NR]) {
+        const uint32_t full_end = blocks / T::kPerChunk; // chunks [0, full_end) hold kPerChunk blocks
+        for (uint32_t c = c0; c < c1; c += kSlots) {
+#pragma unroll
+            for (int p = 0; p < kSlots; ++p) {
+                const uint32_t cc = c + p;
+                if (cc >= c1) break;
+                if (cc + PF < c_end) {
+#pragma unroll
+                    for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(rows[i], cc + PF);
+                }
+                const uint32_t b = cc * T::kPerChunk;
+                if (cc < full_end) {
+                    T::template step<NR, true>(buf[p], lds, nb_tile, b - tile_b0, T::kPerChunk, l, t);
+                } else {
+                    T::template step<NR, false>(buf[p], lds, nb_tile, b - tile_b0, blocks - b, l, t);
+                }
+            }
+        }
+    }
+};
+
+// Blocks per LDS tile: the whole row when it fits in `budget_floats` of LDS,
+// else a whole number of `align`-chunk groups (at least one group).
 template <class T>
-__host__ __device__ inline uint32_t tile_blocks_for(uint32_t blocks, uint32_t budget_floats) {
-    uint32_t tb = budget_floats / T::kLdsFloatsPerBlock;
-    tb = tb / T::kPerChunk * T::kPerChunk;
-    if (tb == 0) tb = T::kPerChunk;
+__host__ __device__ inline uint32_t tile_blocks_for(uint32_t blocks, uint32_t budget_floats,
+                                                    uint32_t align = 1) {
     const uint32_t whole = (blocks + T::kPerChunk - 1) / T::kPerChunk * T::kPerChunk;
+    if (whole * T::kLdsFloatsPerBlock <= budget_floats) return whole;
+    const uint32_t unit = T::kPerChunk * align;
+    uint32_t tb = budget_floats / T::kLdsFloatsPerBlock;
+    tb = tb / unit * unit;
+    if (tb == 0) tb = unit;
     return tb < whole ? tb : whole;
 }
 

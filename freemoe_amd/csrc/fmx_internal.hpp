@@ -32,8 +32,8 @@ int fault_gate();
 
 int status_of_hip(hipError_t e);
 
-inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
-inline uint32_t div_up(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+__host__ __device__ inline uint32_t div_up(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
 // Packed layout of one [rows x cols] matrix: two regions, scales then quants,
 // each 256-byte aligned. A "chunk" is what one lane loads per row per step
@@ -105,8 +105,24 @@ __device__ __forceinline__ float hsum8_lanes(float t) {
     return a + lane_xor(a, 2);
 }
 
+// Global-memory loads through an address-space-1 pointer. Expert slots are
+// reached through a table of generic pointers, which the compiler would
+// otherwise read with FLAT instructions; FLAT loads count against the LDS
+// wait counter too, so every wait for an LDS read would also drain the
+// weight prefetch.
+typedef unsigned int fmx_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int fmx_u32x2 __attribute__((ext_vector_type(2)));
+typedef const __attribute__((address_space(1))) fmx_u32x4 fmx_global_u32x4;
+typedef const __attribute__((address_space(1))) fmx_u32x2 fmx_global_u32x2;
+
 __device__ __forceinline__ uint4 ld16(const void *p) {
-    return *reinterpret_cast<const uint4 *>(p);
+    const fmx_u32x4 v = *(fmx_global_u32x4 *)(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint2 ld8(const void *p) {
+    const fmx_u32x2 v = *(fmx_global_u32x2 *)(p);
+    return make_uint2(v.x, v.y);
 }
 
 // 6-bit scale/min pair j of a Q4_K super-block (quant.cpp:63-71).

@@ -20,7 +20,7 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
     const uint8_t *__restrict__ packed, const float *__restrict__ x, float *__restrict__ y,
     uint32_t rows, uint32_t blocks, uint32_t blocks_padded, uint32_t chunks, uint64_t scale_bytes,
     uint32_t tile_blocks) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     const uint32_t tid = threadIdx.x;
     const uint32_t l = tid & 7;
     const uint32_t slot = tid >> 3; // 0..31
@@ -89,6 +89,8 @@ extern "C" int fmx_matvec(uint32_t type_id, const void *packed, const float *x, 
     PackedGeometry g;
     if (int rc = packed_geometry(type_id, out_dim, in_dim, &g)) return rc;
     if (!packed || !x || !y) return FMX_ERR_INVALID_ARGUMENT;
+    // block-type kernels stage x with 16-byte loads
+    if (type_id != FMX_TYPE_F32 && (reinterpret_cast<uintptr_t>(x) & 15u)) return FMX_ERR_INVALID_ARGUMENT;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (type_id) {
     case FMX_TYPE_F32:

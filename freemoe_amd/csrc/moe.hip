@@ -4,12 +4,17 @@
 //                   gemv_avx2_row order) -> logit bias (engine.cpp:1611-1616) ->
 //                   softmax (engine.cpp:378-393) -> stable top-k
 //                   (engine.cpp:395-411) -> weights (engine.cpp:1680-1702).
-//                   One workgroup per token.
+//                   One workgroup per token: 256 threads per token for batches,
+//                   1024 threads with the router rows staged in LDS for decode.
 //   gate_up_kernel  gate and up rows of each routed expert, fused with SwiGLU
 //                   (engine.cpp:1738-1761; activation.hpp:33, 84).
 //   down_kernel     down rows of all routed experts of a token, the combine in
 //                   rank order (engine.cpp:1770) and the residual add
 //                   (engine.cpp:813-816, 1822).
+//
+// gfx950 gives a workgroup up to 160 KiB of LDS; the decode kernels stage the
+// whole router, the whole of h, and every routed expert's activations at once
+// so that no pass waits twice on HBM latency.
 //
 // RMSNorm's sum of squares is a sequential double sum in the reference. Here it
 // is a parallel sum plus a certificate: every normalised value is checked to
@@ -21,11 +26,19 @@
 #include "matvec.hpp"
 #include "moe.hpp"
 
+#include <mutex>
+#include <vector>
+
 namespace fmx {
 
 namespace {
 
-constexpr uint32_t kRouteThreads = 256;
+constexpr uint32_t kRouteThreads = 256;      // batched routing: one workgroup per token
+constexpr uint32_t kDecodeRouteThreads = 1024;
+constexpr uint32_t kMaxHidden = 16384;         // hidden sizes the routing kernels accept
+// Dynamic LDS these kernels request at most: a gfx950 workgroup may hold
+// 160 KiB, of which 1 KiB is left for the kernels' static LDS.
+constexpr size_t kMaxLds = 159 * 1024;
 constexpr uint32_t kThreads = 256;
 
 __device__ inline double wave_sum_double(double v) {
@@ -59,81 +72,83 @@ __device__ inline float normalised(float x, const float *w, uint32_t k, double s
     return static_cast<float>(static_cast<double>(x) * scale * static_cast<double>(gain));
 }
 
-__global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a, const float *__restrict__ x,
-                                                              float *__restrict__ h_out,
-                                                              float *__restrict__ logits_out,
-                                                              uint32_t *__restrict__ ids,
-                                                              float *__restrict__ weights,
-                                                              uint32_t *__restrict__ status) {
-    extern __shared__ double lds_d[];
-    __shared__ double wave_part[kRouteThreads / 64];
-    __shared__ double ss_s, sum_s;
-    __shared__ int unsafe_s, bad_s;
-    __shared__ float max_s;
-    const uint32_t H = a.hidden, E = a.experts, K = a.top_k;
-    const uint32_t tid = threadIdx.x, t = blockIdx.x;
-    double *exps = lds_d;                                   // [E]
-    float *xs = reinterpret_cast<float *>(lds_d + E);       // [H]
-    float *hs = xs + H;                                     // [H]
-    float *logit_s = hs + H;                                // [E]
-    float *prob_s = logit_s + E;                            // [E]
-    const float *xt = x + static_cast<uint64_t>(t) * H;
-
-    // ---- RMSNorm
+// Writes RMSNorm(x) into hs (LDS, H floats); NT threads, x held in registers
+// (H <= kMaxHidden). The norm gains are requested with x. Every thread of the
+// workgroup calls it; ends with a barrier.
+template <uint32_t NT>
+__device__ void rmsnorm_lds(const RouteArgs &a, const float *__restrict__ x, float *hs) {
+    constexpr uint32_t kPer = kMaxHidden / NT;
+    __shared__ double wave_part[NT / 64];
+    __shared__ double ss_s;
+    __shared__ int unsafe_s;
+    const uint32_t H = a.hidden, tid = threadIdx.x;
+    float xv[kPer];
     double part = 0.0;
-    for (uint32_t k = tid; k < H; k += kRouteThreads) {
-        const float v = xt[k];
-        xs[k] = v;
-        part += static_cast<double>(v) * static_cast<double>(v);
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+        const uint32_t k = tid + i * NT;
+        xv[i] = k < H ? x[k] : 0.0f;
+        if (k < H) hs[k] = a.norm_weight ? a.norm_weight[k] : 1.0f;
     }
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) part += static_cast<double>(xv[i]) * static_cast<double>(xv[i]);
     part = wave_sum_double(part);
     if ((tid & 63) == 0) wave_part[tid >> 6] = part;
-    if (tid == 0) {
-        unsafe_s = 0;
-        bad_s = 0;
-    }
+    if (tid == 0) unsafe_s = 0;
     __syncthreads();
-    if (tid == 0) ss_s = ((wave_part[0] + wave_part[1]) + wave_part[2]) + wave_part[3];
+    if (tid == 0) {
+        double ss = wave_part[0];
+        for (uint32_t w = 1; w < NT / 64; ++w) ss += wave_part[w];
+        ss_s = ss;
+    }
     __syncthreads();
     // |parallel sum - sequential sum| <= (H + 32) u ss; scale moves by half of
     // that plus a few roundings (see header)
     const double rel_tol = 0.6e-16 * static_cast<double>(H + 32) + 2e-15;
     double scale = 1.0 / sqrt(ss_s / static_cast<double>(H) + a.rms_eps);
     bool unsafe = false;
-    for (uint32_t k = tid; k < H; k += kRouteThreads) {
-        const float gain = a.norm_weight ? static_cast<float>(a.norm_bias + static_cast<double>(a.norm_weight[k])) : 1.0f;
-        const double yd = static_cast<double>(xs[k]) * scale * static_cast<double>(gain);
-        const float f = static_cast<float>(yd);
-        hs[k] = f;
-        unsafe |= rounding_unsafe(yd, f, rel_tol);
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+        const uint32_t k = tid + i * NT;
+        if (k < H) {
+            const float gain = a.norm_weight ? static_cast<float>(a.norm_bias + static_cast<double>(hs[k])) : 1.0f;
+            const double yd = static_cast<double>(xv[i]) * scale * static_cast<double>(gain);
+            const float f = static_cast<float>(yd);
+            hs[k] = f;
+            unsafe |= rounding_unsafe(yd, f, rel_tol);
+        }
     }
     if (unsafe) atomicOr(&unsafe_s, 1);
     __syncthreads();
     if (unsafe_s) {
         if (tid == 0) {
             double ss = 0.0;
-            for (uint32_t k = 0; k < H; ++k) ss += static_cast<double>(xs[k]) * static_cast<double>(xs[k]);
+            for (uint32_t k = 0; k < H; ++k) ss += static_cast<double>(x[k]) * static_cast<double>(x[k]);
             ss_s = ss;
         }
         __syncthreads();
         scale = 1.0 / sqrt(ss_s / static_cast<double>(H) + a.rms_eps);
-        for (uint32_t k = tid; k < H; k += kRouteThreads)
-            hs[k] = normalised(xs[k], a.norm_weight, k, scale, a.norm_bias);
+#pragma unroll
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t k = tid + i * NT;
+            if (k < H) hs[k] = normalised(xv[i], a.norm_weight, k, scale, a.norm_bias);
+        }
         __syncthreads();
     }
-    if (h_out)
-        for (uint32_t k = tid; k < H; k += kRouteThreads) h_out[static_cast<uint64_t>(t) * H + k] = hs[k];
+}
 
-    // ---- router logits: 16 lanes per expert row
-    for (uint32_t e0 = 0; e0 < E; e0 += kRouteThreads / 16) {
-        const uint32_t e = e0 + (tid >> 4);
-        const uint32_t er = e < E ? e : E - 1;
-        const float v = f32_row_chains(a.router + static_cast<uint64_t>(er) * H, hs, H, tid & 15);
-        if ((tid & 15) == 0 && e < E) logit_s[e] = a.router_bias ? v + a.router_bias[e] : v;
-    }
-    __syncthreads();
-
-    // ---- softmax: float max, double exp and sum, float quotient
+// Softmax (float max, double exp and sum, float quotient), stable top-k on
+// the probabilities (ties to the lower index) and the routing weights, from
+// the E logits in logit_s (LDS). exps (E doubles) and prob_s (E floats) are
+// LDS scratch. NT threads; every thread of the workgroup calls it.
+template <uint32_t NT>
+__device__ void finish_routing(const RouteArgs &a, const float *logit_s, double *exps, float *prob_s,
+                               uint32_t *__restrict__ ids, float *__restrict__ weights,
+                               uint32_t *__restrict__ status) {
+    __shared__ float max_s;
+    __shared__ int bad_s;
+    __shared__ double sum_s;
+    const uint32_t E = a.experts, K = a.top_k, tid = threadIdx.x;
     if (tid == 0) {
         float m = logit_s[0];
         int bad = 0;
@@ -145,20 +160,17 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a, const
         bad_s = bad;
     }
     __syncthreads();
-    if (logits_out)
-        for (uint32_t e = tid; e < E; e += kRouteThreads) logits_out[static_cast<uint64_t>(t) * E + e] = logit_s[e];
     if (bad_s) {
         // The reference raises INTERNAL_ERROR here. Record it and emit a
         // routing that keeps every later kernel in bounds.
         if (tid == 0) atomicOr(status, STATUS_NONFINITE_SCORE);
-        for (uint32_t i = tid; i < K; i += kRouteThreads) {
-            ids[static_cast<uint64_t>(t) * K + i] = i < E ? i : 0;
-            weights[static_cast<uint64_t>(t) * K + i] = 0.0f;
+        for (uint32_t i = tid; i < K; i += NT) {
+            ids[i] = i < E ? i : 0;
+            weights[i] = 0.0f;
         }
         return;
     }
-    for (uint32_t e = tid; e < E; e += kRouteThreads)
-        exps[e] = exp(static_cast<double>(logit_s[e]) - static_cast<double>(max_s));
+    for (uint32_t e = tid; e < E; e += NT) exps[e] = exp(static_cast<double>(logit_s[e]) - static_cast<double>(max_s));
     __syncthreads();
     if (tid == 0) {
         double s = 0.0;
@@ -166,14 +178,11 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a, const
         sum_s = s;
     }
     __syncthreads();
-    for (uint32_t e = tid; e < E; e += kRouteThreads) prob_s[e] = static_cast<float>(exps[e] / sum_s);
+    for (uint32_t e = tid; e < E; e += NT) prob_s[e] = static_cast<float>(exps[e] / sum_s);
     __syncthreads();
-
-    // ---- top-k (ties to the lower index) and weights, one lane
     if (tid == 0) {
-        uint32_t *it = ids + static_cast<uint64_t>(t) * K;
-        float *wt = weights + static_cast<uint64_t>(t) * K;
-        uint32_t chosen[64];
+        uint32_t chosen[32];
+        float wv[32];
         float total = 0.0f;
         for (uint32_t r = 0; r < K; ++r) {
             uint32_t best = E;
@@ -185,7 +194,6 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a, const
             }
             chosen[r] = best;
         }
-        float wv[64];
         for (uint32_t r = 0; r < K; ++r) {
             wv[r] = prob_s[chosen[r]];
             total += wv[r];
@@ -196,10 +204,75 @@ __global__ __launch_bounds__(kRouteThreads) void route_kernel(RouteArgs a, const
             for (uint32_t r = 0; r < K; ++r) wv[r] = static_cast<float>(static_cast<double>(wv[r]) / den);
         }
         for (uint32_t r = 0; r < K; ++r) {
-            it[r] = chosen[r];
-            wt[r] = static_cast<float>(static_cast<double>(wv[r]) * a.weights_scale);
+            ids[r] = chosen[r];
+            weights[r] = static_cast<float>(static_cast<double>(wv[r]) * a.weights_scale);
         }
     }
+}
+
+// Routing, one workgroup of NT threads per token. rows_lds = 0: the 16 chain
+// lanes of a router row read it from global memory (batched prefill: many
+// tokens in flight hide the latency). rows_lds > 0: the router is staged into
+// LDS rows_lds rows at a time with every thread's loads in flight together,
+// and the chains read LDS (decode: one token, latency exposed).
+template <uint32_t NT>
+__global__ __launch_bounds__(NT) void route_kernel(RouteArgs a, uint32_t rows_lds, const float *__restrict__ x,
+                                                   float *__restrict__ h_out, float *__restrict__ logits_out,
+                                                   uint32_t *__restrict__ ids, float *__restrict__ weights,
+                                                   uint32_t *__restrict__ status) {
+    extern __shared__ __align__(16) double lds_d[];
+    const uint32_t H = a.hidden, E = a.experts, K = a.top_k;
+    const uint32_t tid = threadIdx.x, t = blockIdx.x;
+    double *exps = lds_d;                                   // [E]
+    float *hs = reinterpret_cast<float *>(lds_d + E);       // [H]
+    float *logit_s = hs + H;                                // [E]
+    float *prob_s = logit_s + E;                            // [E]
+    float *rows = reinterpret_cast<float *>(reinterpret_cast<char *>(lds_d) +
+                                            align_up(E * sizeof(double) + (H + 2 * E) * sizeof(float), 16));
+    const uint32_t c = tid & 15, grp = tid >> 4;
+
+    if (rows_lds == 0) {
+        rmsnorm_lds<NT>(a, x + static_cast<uint64_t>(t) * H, hs);
+        for (uint32_t e0 = 0; e0 < E; e0 += NT / 16) {
+            const uint32_t e = e0 + grp;
+            const uint32_t er = e < E ? e : E - 1;
+            const float v = f32_row_chains(a.router + static_cast<uint64_t>(er) * H, hs, H, c);
+            if (c == 0 && e < E) logit_s[e] = a.router_bias ? v + a.router_bias[e] : v;
+        }
+    } else {
+        for (uint32_t e0 = 0; e0 < E; e0 += rows_lds) {
+            const uint32_t nr = E - e0 < rows_lds ? E - e0 : rows_lds;
+            if (e0 > 0) __syncthreads(); // the previous rows' chains are done
+            const float4 *src = reinterpret_cast<const float4 *>(a.router + static_cast<uint64_t>(e0) * H);
+            float4 *dst = reinterpret_cast<float4 *>(rows);
+            const uint32_t n4 = nr * H / 4;
+            for (uint32_t i0 = tid; i0 < n4; i0 += 8 * NT) {
+                float4 v[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t i = i0 + u * NT;
+                    v[u] = src[i < n4 ? i : n4 - 1];
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (i0 + u * NT < n4) dst[i0 + u * NT] = v[u];
+            }
+            if (e0 == 0) rmsnorm_lds<NT>(a, x + static_cast<uint64_t>(t) * H, hs); // ends with a barrier
+            else __syncthreads();
+            for (uint32_t r = grp; r < nr; r += NT / 16) {
+                const float v = f32_row_chains(rows + static_cast<uint64_t>(r) * H, hs, H, c);
+                const uint32_t e = e0 + r;
+                if (c == 0) logit_s[e] = a.router_bias ? v + a.router_bias[e] : v;
+            }
+        }
+    }
+    __syncthreads();
+    if (h_out)
+        for (uint32_t k = tid; k < H; k += NT) h_out[static_cast<uint64_t>(t) * H + k] = hs[k];
+    if (logits_out)
+        for (uint32_t e = tid; e < E; e += NT) logits_out[static_cast<uint64_t>(t) * E + e] = logit_s[e];
+    finish_routing<NT>(a, logit_s, exps, prob_s, ids + static_cast<uint64_t>(t) * K,
+                       weights + static_cast<uint64_t>(t) * K, status);
 }
 
 // ------------------------------------------------------------ experts --
@@ -209,13 +282,14 @@ __device__ inline float swiglu(float gate, float up) {
     return static_cast<float>(g / (1.0 + exp(-g))) * up;
 }
 
-// Gate and up rows j of the expert at rank blockIdx.y, RJ rows per thread.
+// Gate and up rows j of the expert at rank blockIdx.y, RJ rows per thread:
+// the first PF chunks of every row are requested before h is staged.
 template <class T, int RJ, int PF>
 __global__ __launch_bounds__(kThreads) void gate_up_kernel(ExpertArgs a, const float *__restrict__ h,
                                                            const uint32_t *__restrict__ ids,
                                                            float *__restrict__ act,
                                                            uint32_t *__restrict__ status) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     const uint32_t tid = threadIdx.x, l = tid & 7, slot = tid >> 3;
     const uint32_t rank = blockIdx.y;
     const uint32_t e = ids[rank];
@@ -238,13 +312,16 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(ExpertArgs a, const f
         t[2 * m + 1] = 0.0f;
     }
     const uint32_t blocks = a.gu.blocks;
+    const uint32_t c_end = (blocks + T::kPerChunk - 1) / T::kPerChunk;
+    ChunkStream<T, 2 * RJ, PF> cs;
+    cs.prime(rw, c_end);
     for (uint32_t tb = 0; tb < blocks; tb += a.gu_tile) {
         const uint32_t nb = blocks - tb < a.gu_tile ? blocks - tb : a.gu_tile;
         __syncthreads();
         T::stage(h, tb, nb, lds, tid, kThreads);
         __syncthreads();
-        run_chunks_pf<T, 2 * RJ, PF>(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk,
-                                     blocks, tb, nb, lds, l, t);
+        cs.run(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, c_end, blocks, tb, nb, lds, l,
+               t);
     }
 #pragma unroll
     for (int m = 0; m < RJ; ++m) {
@@ -254,8 +331,11 @@ __global__ __launch_bounds__(kThreads) void gate_up_kernel(ExpertArgs a, const f
     }
 }
 
-// Down rows of every routed expert of one token, then the combine and the
-// residual. Slot s handles (rank s / jpw, row s % jpw); jpw = 32 / top_k.
+// Down rows of every routed expert of one token, then the combine in rank
+// order (ffn = 0 + w_0 d_0 + w_1 d_1 ..., engine.cpp:1517, 1770) and the
+// residual (engine.cpp:813-816, 1822). Row slot s handles rank s / jpw, row
+// s % jpw of this workgroup's jpw rows (jpw = 32 / top_k); every rank's
+// activations are staged together, so one workgroup finishes its rows alone.
 template <class T, int PF>
 __global__ __launch_bounds__(kThreads) void down_kernel(ExpertArgs a, const float *__restrict__ x,
                                                         const float *__restrict__ act,
@@ -263,14 +343,13 @@ __global__ __launch_bounds__(kThreads) void down_kernel(ExpertArgs a, const floa
                                                         const float *__restrict__ w,
                                                         float *__restrict__ out,
                                                         uint32_t *__restrict__ status) {
-    extern __shared__ float lds[];
+    extern __shared__ __align__(16) float lds[];
     __shared__ float dres[kThreads / 8];
     const uint32_t tid = threadIdx.x, l = tid & 7, slot = tid >> 3;
     const uint32_t K = a.top_k, H = a.hidden;
     const uint32_t jpw = (kThreads / 8) / K;
     const uint32_t rank = slot / jpw < K ? slot / jpw : K - 1;
-    const uint32_t jj = slot % jpw;
-    const uint32_t j = blockIdx.x * jpw + jj;
+    const uint32_t j = blockIdx.x * jpw + slot % jpw;
     const uint32_t jr = j < H ? j : H - 1;
     uint32_t e = ids[rank];
     const bool bad = e >= a.experts;
@@ -279,22 +358,25 @@ __global__ __launch_bounds__(kThreads) void down_kernel(ExpertArgs a, const floa
         e = 0;
     }
     typename T::Row rw[1];
-    rw[0] = T::row(static_cast<const uint8_t *>(a.down[e]), a.dn.scale_bytes, a.dn.blocks_padded,
-                   a.dn.chunks, jr, l);
+    rw[0] = T::row(static_cast<const uint8_t *>(a.down[e]), a.dn.scale_bytes, a.dn.blocks_padded, a.dn.chunks,
+                   jr, l);
     float t[1] = {0.0f};
     const uint32_t blocks = a.dn.blocks;
+    const uint32_t c_end = (blocks + T::kPerChunk - 1) / T::kPerChunk;
     const uint32_t tile_floats = a.dn_tile * T::kLdsFloatsPerBlock;
+    ChunkStream<T, 1, PF> cs;
+    cs.prime(rw, c_end);
     for (uint32_t tb = 0; tb < blocks; tb += a.dn_tile) {
         const uint32_t nb = blocks - tb < a.dn_tile ? blocks - tb : a.dn_tile;
         __syncthreads();
         for (uint32_t r = 0; r < K; ++r)
             T::stage(act + static_cast<uint64_t>(r) * a.ffn, tb, nb, lds + r * tile_floats, tid, kThreads);
         __syncthreads();
-        run_chunks_pf<T, 1, PF>(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk,
-                                blocks, tb, nb, lds + rank * tile_floats, l, t);
+        cs.run(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, c_end, blocks, tb, nb,
+               lds + rank * tile_floats, l, t);
     }
     const float v = T::finish(t[0]);
-    if (l == 0 && slot < K * jpw) dres[slot] = bad ? 0.0f : v;
+    if (l == 0) dres[slot] = bad ? 0.0f : v;
     __syncthreads();
     if (tid < jpw) {
         const uint32_t jo = blockIdx.x * jpw + tid;
@@ -364,34 +446,82 @@ __global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const 
 
 // ------------------------------------------------------------ launchers --
 
+// Prefetch depth (chunks in flight per row) of each pass.
+constexpr int kGateUpPF = 4;
+constexpr int kDownPF = 8;
+
+// Raises the dynamic LDS limit of kernel `fn` (64 KiB by default) to `bytes`
+// when a launch needs more; the limit only grows, and each kernel's is kept.
+int allow_lds(const void *fn, size_t bytes) {
+    if (bytes <= 64 * 1024) return FMX_OK;
+    static std::mutex mu;
+    static std::vector<std::pair<const void *, size_t>> limits;
+    std::lock_guard<std::mutex> lock(mu);
+    for (auto &f : limits)
+        if (f.first == fn) {
+            if (f.second >= bytes) return FMX_OK;
+            FMX_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
+            f.second = bytes;
+            return FMX_OK;
+        }
+    FMX_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
+    limits.emplace_back(fn, bytes);
+    return FMX_OK;
+}
+
 template <class T>
 int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const uint32_t *ids,
-                     const float *w, float *act, float *out, uint32_t *status, hipStream_t s,
+                     const float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
                      hipEvent_t mid) {
     constexpr int RJ = 1;
     const size_t lds_gu = static_cast<size_t>(a.gu_tile) * T::kLdsFloatsPerBlock * sizeof(float);
-    hipLaunchKernelGGL((gate_up_kernel<T, RJ, 2>), dim3(div_up(a.ffn, (kThreads / 8) * RJ), a.top_k),
-                       dim3(kThreads), lds_gu, s, a, h, ids, act, status);
+    const size_t lds_dn = static_cast<size_t>(a.dn_tile) * T::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
+    if (lds_gu > kMaxLds || lds_dn > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
+    auto gu = gate_up_kernel<T, RJ, kGateUpPF>;
+    auto dn = down_kernel<T, kDownPF>;
+    if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds_gu)) return rc;
+    if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds_dn)) return rc;
+    hipLaunchKernelGGL(gu, dim3(div_up(a.ffn, (kThreads / 8) * RJ), a.top_k), dim3(kThreads), lds_gu, s, a, h, ids,
+                       ws.act, status);
     FMX_LAUNCH_CHECK();
     if (mid) FMX_HIP_TRY(hipEventRecord(mid, s));
     const uint32_t jpw = (kThreads / 8) / a.top_k;
-    const size_t lds_dn = static_cast<size_t>(a.dn_tile) * T::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
-    hipLaunchKernelGGL((down_kernel<T, 4>), dim3(div_up(a.hidden, jpw)), dim3(kThreads), lds_dn, s, a, x,
-                       act, ids, w, out, status);
+    hipLaunchKernelGGL(dn, dim3(div_up(a.hidden, jpw)), dim3(kThreads), lds_dn, s, a, x, ws.act, ids, w, out,
+                       status);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
 
 } // namespace
 
-size_t route_lds_bytes(uint32_t hidden, uint32_t experts) {
-    return static_cast<size_t>(experts) * sizeof(double) + (2ull * hidden + 2ull * experts) * sizeof(float);
+size_t route_lds_bytes(uint32_t hidden, uint32_t experts, uint32_t rows_lds) {
+    const size_t base = static_cast<size_t>(experts) * sizeof(double) + (hidden + 2ull * experts) * sizeof(float);
+    return align_up(base, 16) + static_cast<size_t>(rows_lds) * hidden * sizeof(float);
 }
 
 int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                  uint32_t *ids, float *weights, uint32_t *status, hipStream_t s) {
-    hipLaunchKernelGGL(route_kernel, dim3(tokens), dim3(kRouteThreads), route_lds_bytes(a.hidden, a.experts),
-                       s, a, x, h, logits, ids, weights, status);
+    if (a.hidden > kMaxHidden) return FMX_ERR_SHAPE_MISMATCH;
+    const size_t lds = route_lds_bytes(a.hidden, a.experts, 0);
+    if (lds > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
+    auto k = route_kernel<kRouteThreads>;
+    if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+    hipLaunchKernelGGL(k, dim3(tokens), dim3(kRouteThreads), lds, s, a, 0u, x, h, logits, ids, weights, status);
+    FMX_LAUNCH_CHECK();
+    return FMX_OK;
+}
+
+int launch_route_decode(const RouteArgs &a, const float *x, float *h, uint32_t *ids, float *weights,
+                        uint32_t *status, hipStream_t s) {
+    if (a.hidden > kMaxHidden || a.hidden % 4) return FMX_ERR_SHAPE_MISMATCH;
+    const size_t base = route_lds_bytes(a.hidden, a.experts, 0);
+    if (base + a.hidden * sizeof(float) > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
+    uint32_t rows = static_cast<uint32_t>((kMaxLds - base) / (a.hidden * sizeof(float)));
+    rows = rows < a.experts ? rows : a.experts;
+    const size_t lds = route_lds_bytes(a.hidden, a.experts, rows);
+    auto k = route_kernel<kDecodeRouteThreads>;
+    if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+    hipLaunchKernelGGL(k, dim3(1), dim3(kDecodeRouteThreads), lds, s, a, rows, x, h, nullptr, ids, weights, status);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
@@ -410,19 +540,21 @@ int prepare_expert_args(const fmx_moe_layer *L, ExpertArgs *a) {
     if (L->up_type != L->gate_type) return FMX_ERR_UNSUPPORTED_QUANTISATION;
     if (int rc = packed_geometry(L->gate_type, L->ffn, L->hidden, &e.gu)) return rc;
     if (int rc = packed_geometry(L->down_type, L->hidden, L->ffn, &e.dn)) return rc;
-    // LDS tiles: gate/up stage one x tile; down stages one tile per rank
-    constexpr uint32_t kGuBudget = 6 * 1024, kDnBudget = 10 * 1024;
+    // LDS tiles (blocks): gate/up stages one tile of h, down one tile of every
+    // rank's activations; a tile is the whole row when it fits, else a whole
+    // multiple of the pass's chunk ring (prefetch depth + 1)
+    constexpr uint32_t kGuBudget = 32 * 1024;                      // floats
+    const uint32_t dn_budget = static_cast<uint32_t>(kMaxLds / 4 - 1024) / L->top_k;
     switch (L->gate_type) {
-    case FMX_TYPE_Q4_0: e.gu_tile = tile_blocks_for<Q40>(e.gu.blocks, kGuBudget); break;
-    case FMX_TYPE_Q8_0: e.gu_tile = tile_blocks_for<Q80>(e.gu.blocks, kGuBudget); break;
-    case FMX_TYPE_Q4_K: e.gu_tile = tile_blocks_for<Q4K>(e.gu.blocks, kGuBudget); break;
+    case FMX_TYPE_Q4_0: e.gu_tile = tile_blocks_for<Q40>(e.gu.blocks, kGuBudget, kGateUpPF + 1); break;
+    case FMX_TYPE_Q8_0: e.gu_tile = tile_blocks_for<Q80>(e.gu.blocks, kGuBudget, kGateUpPF + 1); break;
+    case FMX_TYPE_Q4_K: e.gu_tile = tile_blocks_for<Q4K>(e.gu.blocks, kGuBudget, kGateUpPF + 1); break;
     default: e.gu_tile = 0; break;
     }
-    const uint32_t dn_budget = kDnBudget / L->top_k;
     switch (L->down_type) {
-    case FMX_TYPE_Q4_0: e.dn_tile = tile_blocks_for<Q40>(e.dn.blocks, dn_budget); break;
-    case FMX_TYPE_Q8_0: e.dn_tile = tile_blocks_for<Q80>(e.dn.blocks, dn_budget); break;
-    case FMX_TYPE_Q4_K: e.dn_tile = tile_blocks_for<Q4K>(e.dn.blocks, dn_budget); break;
+    case FMX_TYPE_Q4_0: e.dn_tile = tile_blocks_for<Q40>(e.dn.blocks, dn_budget, kDownPF + 1); break;
+    case FMX_TYPE_Q8_0: e.dn_tile = tile_blocks_for<Q80>(e.dn.blocks, dn_budget, kDownPF + 1); break;
+    case FMX_TYPE_Q4_K: e.dn_tile = tile_blocks_for<Q4K>(e.dn.blocks, dn_budget, kDownPF + 1); break;
     default: e.dn_tile = 0; break;
     }
     *a = e;
@@ -430,8 +562,9 @@ int prepare_expert_args(const fmx_moe_layer *L, ExpertArgs *a) {
 }
 
 int launch_experts(const ExpertArgs &a, const float *x, const float *h, const uint32_t *ids,
-                   const float *w, float *act, float *out, uint32_t *status, hipStream_t s,
+                   const float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
                    hipEvent_t mid) {
+    float *act = ws.act;
     if (a.type_gu == FMX_TYPE_F32) {
         if (a.top_k > kThreads / 16 || a.type_dn != FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
         hipLaunchKernelGGL(gate_up_f32_kernel, dim3(div_up(a.ffn, kThreads / 16), a.top_k), dim3(kThreads), 0, s,
@@ -448,9 +581,9 @@ int launch_experts(const ExpertArgs &a, const float *x, const float *h, const ui
     }
     if (a.type_gu != a.type_dn) return FMX_ERR_UNSUPPORTED_QUANTISATION;
     switch (a.type_gu) {
-    case FMX_TYPE_Q4_0: return launch_experts_q<Q40>(a, x, h, ids, w, act, out, status, s, mid);
-    case FMX_TYPE_Q8_0: return launch_experts_q<Q80>(a, x, h, ids, w, act, out, status, s, mid);
-    case FMX_TYPE_Q4_K: return launch_experts_q<Q4K>(a, x, h, ids, w, act, out, status, s, mid);
+    case FMX_TYPE_Q4_0: return launch_experts_q<Q40>(a, x, h, ids, w, ws, out, status, s, mid);
+    case FMX_TYPE_Q8_0: return launch_experts_q<Q80>(a, x, h, ids, w, ws, out, status, s, mid);
+    case FMX_TYPE_Q4_K: return launch_experts_q<Q4K>(a, x, h, ids, w, ws, out, status, s, mid);
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }
