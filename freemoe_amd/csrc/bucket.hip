@@ -25,7 +25,8 @@ constexpr uint32_t kWords = kBucketThreads / 32; // bitmask words per expert
 __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     const uint32_t *__restrict__ ids, uint32_t tokens, uint32_t K, uint32_t E,
     uint32_t *__restrict__ offsets, uint32_t *__restrict__ token_list,
-    uint32_t *__restrict__ rank_list, uint32_t *__restrict__ slot_of, uint32_t *__restrict__ status) {
+    uint32_t *__restrict__ rank_list, uint32_t *__restrict__ slot_of, uint32_t *__restrict__ status,
+    uint32_t *__restrict__ tiles, uint32_t tile_rows) {
     extern __shared__ __align__(16) uint32_t sm[];
     uint32_t *count = sm;                  // [E]
     uint32_t *base = count + E;            // [E]
@@ -43,18 +44,31 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     }
     __syncthreads();
     if (bad) {
-        if (tid == 0) atomicOr(status, STATUS_BAD_EXPERT);
+        if (tid == 0) {
+            atomicOr(status, STATUS_BAD_EXPERT);
+            if (tiles) tiles[0] = 0; // nothing downstream runs on these lists
+        }
         return;
     }
-    // exclusive prefix sum over experts (E <= kBucketThreads), one lane
+    // exclusive prefix sum over experts (E <= kBucketThreads), one lane;
+    // with `tiles`, also the list of row tiles (expert, first row, rows) of
+    // at most tile_rows rows each, experts ascending: tiles[0] = count, then
+    // 3 words per tile
     if (tid == 0) {
-        uint32_t run = 0;
+        uint32_t run = 0, nt = 0;
         for (uint32_t e = 0; e < E; ++e) {
             base[e] = run;
             offsets[e] = run;
+            if (tiles)
+                for (uint32_t r = 0; r < count[e]; r += tile_rows, ++nt) {
+                    tiles[1 + 3 * nt] = e;
+                    tiles[2 + 3 * nt] = run + r;
+                    tiles[3 + 3 * nt] = count[e] - r < tile_rows ? count[e] - r : tile_rows;
+                }
             run += count[e];
         }
         offsets[E] = run;
+        if (tiles) tiles[0] = nt;
     }
     __syncthreads();
     for (uint32_t t0 = 0; t0 < tokens; t0 += kBucketThreads) {
@@ -98,9 +112,10 @@ size_t bucket_lds_bytes(uint32_t experts) {
 
 int launch_bucket(const uint32_t *ids, uint32_t tokens, uint32_t K, uint32_t E, uint32_t *offsets,
                   uint32_t *token_list, uint32_t *rank_list, uint32_t *slot_of, uint32_t *status,
-                  hipStream_t s) {
+                  hipStream_t s, uint32_t *tiles, uint32_t tile_rows) {
+    if (tiles && tile_rows == 0) return FMX_ERR_INVALID_ARGUMENT;
     hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(kBucketThreads), bucket_lds_bytes(E), s, ids, tokens, K,
-                       E, offsets, token_list, rank_list, slot_of, status);
+                       E, offsets, token_list, rank_list, slot_of, status, tiles, tile_rows);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }

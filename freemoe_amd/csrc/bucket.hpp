@@ -9,8 +9,14 @@ namespace fmx {
 constexpr uint32_t kBucketMaxExperts = 256;
 
 size_t bucket_lds_bytes(uint32_t experts);
+// tiles (optional): [1 + 3 * max_tiles] words, max_tiles = E + tokens*K / tile_rows;
+// receives the row tiles of at most tile_rows rows of every non-empty expert.
 int launch_bucket(const uint32_t *ids, uint32_t tokens, uint32_t K, uint32_t E, uint32_t *offsets,
                   uint32_t *token_list, uint32_t *rank_list, uint32_t *slot_of, uint32_t *status,
-                  hipStream_t s);
+                  hipStream_t s, uint32_t *tiles = nullptr, uint32_t tile_rows = 0);
+
+inline uint32_t bucket_max_tiles(uint32_t tokens, uint32_t K, uint32_t E, uint32_t tile_rows) {
+    return E + static_cast<uint32_t>((static_cast<uint64_t>(tokens) * K) / tile_rows);
+}
 
 } // namespace fmx

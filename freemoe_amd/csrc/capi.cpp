@@ -3,6 +3,7 @@
 #include "bucket.hpp"
 #include "fmx_internal.hpp"
 #include "moe.hpp"
+#include "prefill.hpp"
 
 #include <atomic>
 #include <chrono>
@@ -35,6 +36,39 @@ DecodeWorkspace decode_workspace(const fmx_moe_layer *L) {
     w.h = kStatusBytes;
     w.act = w.h + align_up(static_cast<uint64_t>(L->hidden) * 4, 256);
     w.total = w.act + align_up(static_cast<uint64_t>(L->top_k) * L->ffn * 4, 256);
+    return w;
+}
+
+// Prefill workspace (all offsets 256-byte aligned), pairs = tokens * top_k:
+//   [0, 256) error word | h [tokens x hidden] f32 | offsets [experts + 1] |
+//   token_list, rank_list, slot_of [pairs] | row tiles [1 + 3 * max_tiles] |
+//   x [pairs x hidden] bf16 | act [pairs x ffn] bf16 | dn [pairs x hidden] f32 |
+//   the decode scratch (act of one token) for shapes the GEMMs do not tile
+struct PrefillWorkspace {
+    uint64_t h = 0, offsets = 0, token_list = 0, rank_list = 0, slot_of = 0, tiles = 0, x = 0, act = 0, dn = 0,
+             dec_act = 0, total = 0;
+    uint32_t pairs = 0, max_tiles = 0;
+};
+
+PrefillWorkspace prefill_workspace(const fmx_moe_layer *L, uint32_t tokens) {
+    PrefillWorkspace w;
+    const uint64_t H = L->hidden, F = L->ffn, E = L->experts;
+    w.pairs = tokens * L->top_k;
+    w.max_tiles = bucket_max_tiles(tokens, L->top_k, L->experts, kPrefillTileRows);
+    const uint64_t P = w.pairs;
+    uint64_t o = kStatusBytes;
+    auto take = [&o](uint64_t bytes) { const uint64_t at = o; o += align_up(bytes, 256); return at; };
+    w.h = take(static_cast<uint64_t>(tokens) * H * 4);
+    w.offsets = take((E + 1) * 4);
+    w.token_list = take(P * 4);
+    w.rank_list = take(P * 4);
+    w.slot_of = take(P * 4);
+    w.tiles = take((1 + 3ull * w.max_tiles) * 4);
+    w.x = take(P * H * 2);
+    w.act = take(P * F * 2);
+    w.dn = take(P * H * 4);
+    w.dec_act = take(static_cast<uint64_t>(L->top_k) * F * 4);
+    w.total = o;
     return w;
 }
 
@@ -388,6 +422,61 @@ int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uin
     for (auto &row : ev)
         for (auto &e : row) (void)hipEventDestroy(e);
     return rc;
+}
+
+uint64_t fmx_moe_prefill_workspace_bytes(const fmx_moe_layer *L, uint32_t tokens) {
+    if (validate_layer(L) || tokens == 0) return 0;
+    return prefill_workspace(L, tokens).total;
+}
+
+int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
+                    float *weights, void *workspace, uint64_t workspace_bytes, void *stream) {
+    if (int rc = fault_gate()) return rc;
+    if (int rc = validate_layer(L)) return rc;
+    if (tokens == 0) return FMX_OK;
+    if (!x || !out || !ids || !weights || !workspace) return FMX_ERR_INVALID_ARGUMENT;
+    if (!aligned16(x) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
+    const PrefillWorkspace ws = prefill_workspace(L, tokens);
+    if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
+    ExpertArgs ea;
+    if (int rc = prepare_expert_args(L, &ea)) return rc;
+    const RouteArgs ra = route_args(L);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint8_t *base = static_cast<uint8_t *>(workspace);
+    uint32_t *status = reinterpret_cast<uint32_t *>(base);
+    float *h = reinterpret_cast<float *>(base + ws.h);
+    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
+    FMX_LAUNCH_CHECK();
+    if (int rc = launch_route(ra, x, tokens, h, nullptr, ids, weights, status, s)) return rc;
+    const uint64_t H = L->hidden, K = L->top_k;
+    if (!prefill_gemm_supported(ea)) {
+        // shapes the grouped GEMMs do not tile (and F32 experts): the decode
+        // expert kernels, one token at a time, on the routing just computed
+        DecodeScratch sc;
+        sc.act = reinterpret_cast<float *>(base + ws.dec_act);
+        for (uint32_t t = 0; t < tokens; ++t)
+            if (int rc = launch_experts(ea, x + t * H, h + t * H, ids + t * K, weights + t * K, sc, out + t * H,
+                                        status, s))
+                return rc;
+        return FMX_OK;
+    }
+    uint32_t *slot_of = reinterpret_cast<uint32_t *>(base + ws.slot_of);
+    PrefillBuffers b;
+    b.h = h;
+    b.token_list = reinterpret_cast<uint32_t *>(base + ws.token_list);
+    b.tiles = reinterpret_cast<uint32_t *>(base + ws.tiles);
+    b.tokens = tokens;
+    b.pairs = ws.pairs;
+    b.x = reinterpret_cast<__bf16 *>(base + ws.x);
+    b.act = reinterpret_cast<__bf16 *>(base + ws.act);
+    b.dn = reinterpret_cast<float *>(base + ws.dn);
+    if (int rc = launch_bucket(ids, tokens, L->top_k, L->experts, reinterpret_cast<uint32_t *>(base + ws.offsets),
+                               reinterpret_cast<uint32_t *>(base + ws.token_list),
+                               reinterpret_cast<uint32_t *>(base + ws.rank_list), slot_of, status, s,
+                               reinterpret_cast<uint32_t *>(base + ws.tiles), kPrefillTileRows))
+        return rc;
+    if (int rc = launch_prefill_experts(ea, b, ws.max_tiles, s)) return rc;
+    return launch_combine(x, b.dn, slot_of, weights, L->hidden, L->top_k, tokens, out, s);
 }
 
 int fmx_moe_status(void *workspace, void *stream) {

@@ -32,6 +32,10 @@ int fault_gate();
 
 int status_of_hip(hipError_t e);
 
+// Raises kernel `fn`'s dynamic LDS limit to `bytes` when above the 64 KiB
+// default (gfx950 workgroups may use up to 160 KiB).
+int allow_lds(const void *fn, size_t bytes);
+
 __host__ __device__ inline uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 __host__ __device__ inline uint32_t div_up(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 

@@ -450,25 +450,6 @@ __global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const 
 constexpr int kGateUpPF = 4;
 constexpr int kDownPF = 8;
 
-// Raises the dynamic LDS limit of kernel `fn` (64 KiB by default) to `bytes`
-// when a launch needs more; the limit only grows, and each kernel's is kept.
-int allow_lds(const void *fn, size_t bytes) {
-    if (bytes <= 64 * 1024) return FMX_OK;
-    static std::mutex mu;
-    static std::vector<std::pair<const void *, size_t>> limits;
-    std::lock_guard<std::mutex> lock(mu);
-    for (auto &f : limits)
-        if (f.first == fn) {
-            if (f.second >= bytes) return FMX_OK;
-            FMX_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
-            f.second = bytes;
-            return FMX_OK;
-        }
-    FMX_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
-    limits.emplace_back(fn, bytes);
-    return FMX_OK;
-}
-
 template <class T>
 int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const uint32_t *ids,
                      const float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
@@ -493,6 +474,25 @@ int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const 
 }
 
 } // namespace
+
+// Raises the dynamic LDS limit of kernel `fn` (64 KiB by default) to `bytes`
+// when a launch needs more; the limit only grows, and each kernel's is kept.
+int allow_lds(const void *fn, size_t bytes) {
+    if (bytes <= 64 * 1024) return FMX_OK;
+    static std::mutex mu;
+    static std::vector<std::pair<const void *, size_t>> limits;
+    std::lock_guard<std::mutex> lock(mu);
+    for (auto &f : limits)
+        if (f.first == fn) {
+            if (f.second >= bytes) return FMX_OK;
+            FMX_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
+            f.second = bytes;
+            return FMX_OK;
+        }
+    FMX_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
+    limits.emplace_back(fn, bytes);
+    return FMX_OK;
+}
 
 size_t route_lds_bytes(uint32_t hidden, uint32_t experts, uint32_t rows_lds) {
     const size_t base = static_cast<size_t>(experts) * sizeof(double) + (hidden + 2ull * experts) * sizeof(float);

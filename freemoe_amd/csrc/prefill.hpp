@@ -1,0 +1,33 @@
+// prefill.hpp — the batched (prefill) MoE path: grouped GEMMs on bf16 MFMA.
+#pragma once
+
+#include "moe.hpp"
+
+namespace fmx {
+
+// Device buffers of one prefill call (in the caller's workspace).
+struct PrefillBuffers {
+    const float *h;              // [tokens x hidden] RMSNorm output
+    const uint32_t *token_list;  // [pairs] token of each bucketed (token, expert) pair
+    const uint32_t *tiles;       // row tiles of the bucketing (count, then expert / first row / rows)
+    uint32_t tokens;
+    uint32_t pairs;              // tokens * top_k
+    __bf16 *x;                   // [pairs x hidden] gathered h in the gate/up packed K order
+    __bf16 *act;                 // [pairs x ffn] SwiGLU output in the down packed K order
+    float *dn;                   // [pairs x hidden] down projections
+};
+
+// Token-expert pairs per row tile of the grouped GEMMs (8 wavefronts x 32).
+constexpr uint32_t kPrefillTileRows = 256;
+
+// The grouped GEMMs need block-type experts with hidden and ffn multiples of
+// the K step (128), of the types' chunk sizes and of the N tiles (hidden % 128,
+// ffn % 64).
+bool prefill_gemm_supported(const ExpertArgs &a);
+// gather -> gate/up GEMM + SwiGLU -> down GEMM, over `max_tiles` row tiles.
+int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s);
+// out[t] = x[t] + sum over ranks (rank order) of w * dn[slot_of[t, r]].
+int launch_combine(const float *x, const float *dn, const uint32_t *slot_of, const float *w, uint32_t hidden,
+                   uint32_t K, uint32_t tokens, float *out, hipStream_t s);
+
+} // namespace fmx

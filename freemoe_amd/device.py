@@ -48,6 +48,7 @@ class DeviceLayer:
             fmx.ptr(self.router_bias), int(lw.weights_norm), 0, 6.103515625e-5, 1.0, lw.gate_type, lw.up_type,
             lw.down_type, self.slots[0].data_ptr(), self.slots[1].data_ptr(), self.slots[2].data_ptr())
         self.workspace = None
+        self.prefill_workspace = None
 
     def weight_bytes_per_expert(self) -> int:
         return sum(fmx.raw_row_bytes(t, c) * r for t, r, c in (
@@ -84,6 +85,26 @@ class DeviceLayer:
         fmx.call("fmx_moe_decode", ctypes.byref(self.desc), x.data_ptr(), out.data_ptr(), t, ids.data_ptr(),
                  wts.data_ptr(), ws.data_ptr(), ws.numel(), fmx.stream_handle(stream))
         return out, ids, wts
+
+    def prefill(self, x: torch.Tensor, out=None, ids=None, wts=None, stream=None):
+        """The whole layer over all rows of x at once (grouped GEMMs)."""
+        t = x.shape[0]
+        K = self.w.top_k
+        out = torch.empty_like(x) if out is None else out
+        ids = torch.empty((t, K), dtype=torch.int32, device=self.device) if ids is None else ids
+        wts = torch.empty((t, K), dtype=torch.float32, device=self.device) if wts is None else wts
+        need = fmx.lib().fmx_moe_prefill_workspace_bytes(ctypes.byref(self.desc), t)
+        if need == 0:
+            raise fmx.FmxError(1, "fmx_moe_prefill_workspace_bytes")
+        if self.prefill_workspace is None or self.prefill_workspace.numel() < need:
+            self.prefill_workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)
+        ws = self.prefill_workspace
+        fmx.call("fmx_moe_prefill", ctypes.byref(self.desc), x.data_ptr(), out.data_ptr(), t, ids.data_ptr(),
+                 wts.data_ptr(), ws.data_ptr(), ws.numel(), fmx.stream_handle(stream))
+        return out, ids, wts
+
+    def prefill_status(self, stream=None) -> int:
+        return fmx.lib().fmx_moe_status(self.prefill_workspace.data_ptr(), fmx.stream_handle(stream))
 
     def status(self, stream=None) -> int:
         ws = self.ensure_workspace(1)

@@ -185,6 +185,20 @@ int fmx_moe_decode_timed(const fmx_moe_layer *layer, const float *x, float *out,
                          uint32_t *ids, float *weights, void *workspace, uint64_t workspace_bytes,
                          void *stream, double *kernel_ms);
 
+/* Prefill: the whole layer for `tokens` rows of x ([tokens x hidden]) at once.
+ * Routing is bit-identical to fmx_moe_route (ids / weights [tokens x top_k]);
+ * the experts run as grouped GEMMs on bf16 MFMA over per-expert token lists
+ * (fmx_moe_bucket's order), with each expert's packed blocks dequantised into
+ * LDS; outputs match the reference within 2e-2 relative (bf16 operands, f32
+ * accumulation). The reference has no batched MoE path: it runs its decode
+ * step once per prompt token (engine.cpp:1870, 2395-2399); this replaces that
+ * loop. Shapes the GEMMs do not tile (and F32 experts) run the decode expert
+ * kernels token by token instead, on the GPU. */
+uint64_t fmx_moe_prefill_workspace_bytes(const fmx_moe_layer *layer, uint32_t tokens);
+int fmx_moe_prefill(const fmx_moe_layer *layer, const float *x, float *out, uint32_t tokens,
+                    uint32_t *ids, float *weights, void *workspace, uint64_t workspace_bytes,
+                    void *stream);
+
 /* Device error word written by the routing kernels (non-finite score or an
  * expert id out of range): reads and clears it, blocking on `stream`. */
 int fmx_moe_status(void *workspace, void *stream);
