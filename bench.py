@@ -82,6 +82,86 @@ def cpu_baseline(lw, x, target_s=15.0, max_tokens=256):
         (np.concatenate(outs), np.concatenate(idss), np.concatenate(ws), n)
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+PREFILL_WORKLOAD = "mixtral-q8_0"
+
+
+def prefill_leg(dev, seed=1234, reps=10, cpu=True):
+    """The Mixtral-shaped layer with Q8_0 experts over a 512-token prefill:
+    whole-layer time (routing, bucketing, both grouped GEMMs, combine) from
+    HIP events on the launch stream, against bf16 MFMA peak and HBM peak."""
+    import numpy as np
+    import torch
+    from freemoe_amd import fmx
+    from freemoe_amd import workloads as wl
+    from freemoe_amd.device import DeviceLayer
+
+    spec = wl.WORKLOADS[PREFILL_WORKLOAD]
+    H, F, E, K, T = spec["hidden"], spec["ffn"], spec["experts"], spec["top_k"], spec["tokens"]
+    t_gen = time.perf_counter()
+    lw = wl.make_layer(H, F, E, K, spec["type_id"], seed)
+    x = wl.inputs(H, T, seed + 1)
+    print(f"[bench] prefill weights in {time.perf_counter() - t_gen:.1f}s", file=sys.stderr, flush=True)
+    dl = DeviceLayer(lw, dev)
+    xd = torch.from_numpy(x).to(dev)
+    out = torch.empty_like(xd)
+    ids = torch.empty((T, K), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, K), dtype=torch.float32, device=dev)
+    for _ in range(2):
+        dl.prefill(xd, out, ids, wts)
+    torch.cuda.synchronize()
+    if dl.prefill_status() != 0:
+        raise RuntimeError("device reported a routing error in prefill")
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        dl.prefill(xd, out, ids, wts)
+    stop.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / reps
+    pairs = T * K
+    flops = 6.0 * pairs * H * F
+    counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E)
+    wbytes = int((counts > 0).sum()) * dl.weight_bytes_per_expert()
+    act_bytes = T * H * 4 * 2 + pairs * (H + F) * 2 * 2 + pairs * H * 4 * 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    gbs = (wbytes + act_bytes) / (ms * 1e-3) / 1e9
+    res = {"workload": "Mixtral-shaped MoE layer prefill, 512 tokens, Q8_0 experts", "tokens": T, "hidden": H,
+           "ffn": F, "experts": E, "top_k": K, "ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+           "expert_token_counts": counts.tolist(),
+           "roofline": {"bound": "mfma", "kernel": "whole layer (route, bucket, gather, gate/up GEMM, down GEMM, "
+                                                   "combine)", "achieved": round(tflops, 1),
+                        "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flops": flops,
+                        "hbm_achieved_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "hbm_bytes": wbytes + act_bytes}}
+    if cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import fmoracle as fo
+        hl = fo.host_layer(lw)
+        n, t0 = 0, time.perf_counter()
+        outs = []
+        while n < T and time.perf_counter() - t0 < 10.0:
+            o, _, _ = hl.ref_forward_batch(x[n:n + 1], fo.ISA_AVX2, threads=2)
+            outs.append(o)
+            n += 1
+        dt = time.perf_counter() - t0
+        ref = np.concatenate(outs).astype(np.float64) - x[:n]
+        got = out[:n].cpu().numpy().astype(np.float64) - x[:n]
+        err = got - ref
+        res["cpu_baseline"] = {"value": round(n / dt, 3), "unit": "tokens/s", "cores": 2, "kind": "reference",
+                               "sample": f"first {n} of the 512 tokens, one at a time (the reference has no batched "
+                                         "MoE path), reference gemv_quant at 2 WorkerPool threads"}
+        res["parity"] = {"tokens": n, "ids_equal": None,
+                         "ffn_rel_norm": float(np.linalg.norm(err) / np.linalg.norm(ref)),
+                         "ffn_rel_max": float(np.abs(err).max() / np.abs(ref).max()), "tolerance": 2e-2}
+        want_ids = hl.forward_batch(x[:n])[1]
+        res["parity"]["ids_equal"] = bool(np.array_equal(ids[:n].cpu().numpy().astype(np.uint32), want_ids))
+    del dl
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -89,6 +169,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--tokens", type=int, default=1000)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token Q8_0 prefill leg")
+    ap.add_argument("--prefill-only", action="store_true", help="run only the prefill leg (for profiling)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="also run one plain device-to-device copy of this many bytes (a known-traffic "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -110,6 +192,11 @@ def main() -> int:
     dev = torch.device("cuda:0")
     info = fmx.DeviceInfo()
     fmx.call("fmx_device_info_get", 0, ctypes.byref(info))
+
+    if args.prefill_only:
+        res = prefill_leg(dev, reps=args.steps, cpu=not args.no_cpu_baseline)
+        print(json.dumps({"prefill": res}))
+        return 0
 
     spec = wl.WORKLOADS[WORKLOAD]
     H, F, E, K, T = spec["hidden"], spec["ffn"], spec["experts"], spec["top_k"], args.tokens
@@ -211,6 +298,14 @@ def main() -> int:
                                 "bitwise_fraction": float(np.mean(go.view(np.uint32) == rout.view(np.uint32)))}
         except Exception as e:  # the baseline is reported, never the target
             result["cpu_baseline"] = {"value": None, "error": f"{type(e).__name__}: {e}"}
+    if not args.no_prefill:
+        del dl
+        torch.cuda.empty_cache()
+        print("[bench] prefill leg", file=sys.stderr, flush=True)
+        try:
+            result["prefill"] = prefill_leg(dev, cpu=not args.no_cpu_baseline)
+        except Exception as e:  # reported, never silently dropped
+            result["prefill"] = {"error": f"{type(e).__name__}: {e}"}
     print(json.dumps(result))
     return 0
 

@@ -499,9 +499,29 @@ size_t route_lds_bytes(uint32_t hidden, uint32_t experts, uint32_t rows_lds) {
     return align_up(base, 16) + static_cast<size_t>(rows_lds) * hidden * sizeof(float);
 }
 
+// Router rows that fit in LDS next to the routing state (0: none fit).
+uint32_t route_rows_in_lds(const RouteArgs &a) {
+    const size_t base = route_lds_bytes(a.hidden, a.experts, 0);
+    if (a.hidden % 4 || base + a.hidden * sizeof(float) > kMaxLds) return 0;
+    const uint32_t rows = static_cast<uint32_t>((kMaxLds - base) / (a.hidden * sizeof(float)));
+    return rows < a.experts ? rows : a.experts;
+}
+
+// One 1024-thread workgroup per token with the router staged in LDS; when
+// not even one router row fits, 256 threads per token reading it from memory.
 int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                  uint32_t *ids, float *weights, uint32_t *status, hipStream_t s) {
     if (a.hidden > kMaxHidden) return FMX_ERR_SHAPE_MISMATCH;
+    const uint32_t rows = route_rows_in_lds(a);
+    if (rows > 0) {
+        const size_t lds = route_lds_bytes(a.hidden, a.experts, rows);
+        auto k = route_kernel<kDecodeRouteThreads>;
+        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+        hipLaunchKernelGGL(k, dim3(tokens), dim3(kDecodeRouteThreads), lds, s, a, rows, x, h, logits, ids, weights,
+                           status);
+        FMX_LAUNCH_CHECK();
+        return FMX_OK;
+    }
     const size_t lds = route_lds_bytes(a.hidden, a.experts, 0);
     if (lds > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
     auto k = route_kernel<kRouteThreads>;
@@ -513,17 +533,7 @@ int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, 
 
 int launch_route_decode(const RouteArgs &a, const float *x, float *h, uint32_t *ids, float *weights,
                         uint32_t *status, hipStream_t s) {
-    if (a.hidden > kMaxHidden || a.hidden % 4) return FMX_ERR_SHAPE_MISMATCH;
-    const size_t base = route_lds_bytes(a.hidden, a.experts, 0);
-    if (base + a.hidden * sizeof(float) > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
-    uint32_t rows = static_cast<uint32_t>((kMaxLds - base) / (a.hidden * sizeof(float)));
-    rows = rows < a.experts ? rows : a.experts;
-    const size_t lds = route_lds_bytes(a.hidden, a.experts, rows);
-    auto k = route_kernel<kDecodeRouteThreads>;
-    if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
-    hipLaunchKernelGGL(k, dim3(1), dim3(kDecodeRouteThreads), lds, s, a, rows, x, h, nullptr, ids, weights, status);
-    FMX_LAUNCH_CHECK();
-    return FMX_OK;
+    return launch_route(a, x, 1, h, nullptr, ids, weights, status, s);
 }
 
 int prepare_expert_args(const fmx_moe_layer *L, ExpertArgs *a) {

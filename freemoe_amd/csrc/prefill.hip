@@ -18,12 +18,14 @@
 // one packed slot serves both decode and prefill, and every weight byte is
 // read from HBM in 16-byte runs straight into the dequantiser.
 //
-// Tiles. A workgroup (8 wavefronts) owns one row tile of one expert (up to 256
-// token-expert pairs, 32 per wavefront) and 128 weight rows (gate/up: 64 gate
-// rows and the same 64 up rows, so SwiGLU pairs meet in one lane). It walks K
-// in steps of 128 packed positions: the weight slices of step s+1 are in
-// flight while step s is dequantised into one of two LDS buffers and fed to
-// v_mfma_f32_32x32x16_bf16 with the activations read straight from memory.
+// Tiles. A workgroup (8 wavefronts) owns one row tile of one expert (up to 128
+// token-expert pairs) and 128 weight rows (gate/up: 64 gate rows and the same
+// 64 up rows, arranged so SwiGLU pairs meet in one lane); wavefront w computes
+// rows 32 (w / 2) .. +32 against weight rows 64 (w % 2) .. +64. It walks K in
+// steps of 128 packed positions with three steps of weight slices and
+// activation rows in flight: each step is dequantised (weights) and copied
+// (activations) into one of two LDS buffer pairs and fed from LDS to
+// v_mfma_f32_32x32x16_bf16.
 #include "bucket.hpp"
 #include "fmx_internal.hpp"
 #include "moe.hpp"
@@ -39,8 +41,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr uint32_t kGemmThreads = 512;            // 8 wavefronts
 constexpr uint32_t kTileN = 128;                  // weight rows per workgroup
 constexpr uint32_t kStepK = 128;                  // packed K positions per step
-constexpr uint32_t kWStride = kStepK + 8;         // bf16 per LDS weight row (16-byte pad)
-constexpr uint32_t kWBufElems = kTileN * kWStride;
+constexpr uint32_t kWBufElems = kTileN * kStepK;  // one LDS weight tile (bf16)
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     const __bf16 x = static_cast<__bf16>(a), y = static_cast<__bf16>(b);
@@ -80,10 +81,10 @@ struct GQ80 {
         for (int j = 0; j < 4; ++j) {
             const float d = half_bits_to_float(j & 2 ? ((j & 1) ? v.d.y >> 16 : v.d.y & 0xFFFFu)
                                                      : ((j & 1) ? v.d.x >> 16 : v.d.x & 0xFFFFu));
-            const float q0 = static_cast<float>(static_cast<int32_t>(w[j] << 24) >> 24);
-            const float q1 = static_cast<float>(static_cast<int32_t>(w[j] << 16) >> 24);
-            const float q2 = static_cast<float>(static_cast<int32_t>(w[j] << 8) >> 24);
-            const float q3 = static_cast<float>(static_cast<int32_t>(w[j]) >> 24);
+            const float q0 = static_cast<float>(static_cast<int8_t>(w[j]));
+            const float q1 = static_cast<float>(static_cast<int8_t>(w[j] >> 8));
+            const float q2 = static_cast<float>(static_cast<int8_t>(w[j] >> 16));
+            const float q3 = static_cast<float>(static_cast<int8_t>(w[j] >> 24));
             out[2 * j] = pack_bf16x2(d * q0, d * q1);
             out[2 * j + 1] = pack_bf16x2(d * q2, d * q3);
         }
@@ -185,12 +186,32 @@ struct GQ4K {
     }
 };
 
-// Weight rows of a tile: the LDS row lr (0..127) reads matrix `w0` row
-// base0 + lr for lr < split, else matrix `w1` row base1 + lr - split.
+// Weight rows of a tile. Gated (gate/up): LDS row block b = lr / 32 holds
+// gate rows (b even) or up rows (b odd) n0 + 32 (b / 2) + lr % 32, so each
+// wavefront's two 32-row blocks are the gate and up rows of the same ffn
+// rows. Plain (down): LDS row lr is matrix row n0 + lr.
 struct TileRows {
-    const uint8_t *w0, *w1;
-    uint32_t base0, base1, split;
+    const uint8_t *gate_or_w, *up;
+    uint32_t n0;
+    bool gated;
+    __device__ void at(uint32_t lr, const uint8_t *&w, uint32_t &r) const {
+        if (gated) {
+            const uint32_t b = lr >> 5;
+            w = (b & 1) ? up : gate_or_w;
+            r = n0 + 32 * (b >> 1) + (lr & 31);
+        } else {
+            w = gate_or_w;
+            r = n0 + lr;
+        }
+    }
 };
+
+// LDS tiles (weights and activations): 128 rows x 128 bf16 (256 bytes), the
+// 16-byte granule g of row r stored at granule g ^ (r & 15), so the 16 rows an
+// MFMA operand read or a store touches at once fall in 16 distinct bank groups.
+__device__ __forceinline__ uint32_t tile_offset(uint32_t row, uint32_t granule) {
+    return row * kStepK + ((granule ^ (row & 15)) << 3);
+}
 
 // One K step of the weight tile: thread t loads slices of LDS row t / 4.
 template <class T>
@@ -198,10 +219,8 @@ struct WeightStep {
     static constexpr uint32_t kPerThread = T::kSlices * kTileN / kGemmThreads; // 2 (Q8_0) or 1 (Q4)
     typename T::Slice s[kPerThread];
 
-    __device__ void load(const TileRows &tr, const PackedGeometry &g, uint32_t step, uint32_t tid) {
-        const uint32_t lr = tid >> 2;
-        const uint8_t *w = lr < tr.split ? tr.w0 : tr.w1;
-        const uint32_t r = lr < tr.split ? tr.base0 + lr : tr.base1 + lr - tr.split;
+    // w / r: the matrix and row of this thread's LDS row (tid / 4).
+    __device__ void load(const uint8_t *w, uint32_t r, const PackedGeometry &g, uint32_t step, uint32_t tid) {
         const uint32_t c = step * kStepK / T::kChunkK;
         const uint32_t s0 = (step * kStepK % T::kChunkK) / (T::kChunkK / 8); // first slice of the step
 #pragma unroll
@@ -215,55 +234,83 @@ struct WeightStep {
         for (uint32_t i = 0; i < kPerThread; ++i) {
             uint32_t v[T::kValsPerSlice / 2];
             T::dequant(s[i], v);
-            const uint32_t p0 = ((tid & 3) * kPerThread + i) * T::kValsPerSlice;
-            uint4 *dst = reinterpret_cast<uint4 *>(wbuf + lr * kWStride + p0);
+            const uint32_t g0 = ((tid & 3) * kPerThread + i) * (T::kValsPerSlice / 8);
 #pragma unroll
             for (uint32_t q = 0; q < T::kValsPerSlice / 8; ++q)
-                dst[q] = make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+                *reinterpret_cast<uint4 *>(wbuf + tile_offset(lr, g0 + q)) =
+                    make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
         }
     }
 };
 
-// Activation fragments of one K step for this lane: row `xrow`, positions
-// k0 + 16 kk + 8 (lane / 32) .. +8, kk = 0..7.
+// One K step of the activation tile: thread t copies 64 bytes (positions
+// 32 (t % 4) .. +32) of tile row t / 4, i.e. matrix row `xrow`.
 struct XStep {
-    bf16x8 f[kStepK / 16];
-    __device__ void load(const __bf16 *x, uint64_t ld, uint32_t xrow, uint32_t k0, uint32_t lane) {
-        const __bf16 *base = x + static_cast<uint64_t>(xrow) * ld + k0 + 8 * (lane >> 5);
+    uint4 v[4];
+    __device__ void load(const __bf16 *x, uint64_t ld, uint32_t xrow, uint32_t step, uint32_t tid) {
+        const __bf16 *src = x + static_cast<uint64_t>(xrow) * ld + step * kStepK + 32 * (tid & 3);
 #pragma unroll
-        for (uint32_t kk = 0; kk < kStepK / 16; ++kk) {
-            const uint4 v = ld16(base + 16 * kk);
-            f[kk] = __builtin_bit_cast(bf16x8, v);
-        }
+        for (int q = 0; q < 4; ++q) v[q] = ld16(src + 8 * q);
+    }
+    __device__ void store(__bf16 *xbuf, uint32_t tid) const {
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) *reinterpret_cast<uint4 *>(xbuf + tile_offset(tid >> 2, 4 * (tid & 3) + q)) = v[q];
     }
 };
 
-// The shared main loop: acc[nb] (32 x 32 blocks nb = 0..3 over the tile's 128
-// weight rows) += X[rows of this wavefront] . W^T over `steps` K steps.
+// K steps whose loads are in flight ahead of the step being consumed. The
+// loads of a step are issued together and consumed together, in issue order,
+// so a wait for one step never waits on a later one. Every step issues its
+// loads unconditionally (past the last step they re-read the last step, which
+// the caches still hold), so the compiler's wait counts stay exact.
+constexpr uint32_t kLead = 4;
+
+// The shared main loop over `steps` K steps. Per step: wait for that step's
+// weight slices and activation rows, dequantise / copy them into one of two
+// LDS buffer pairs, request step + kLead, barrier, then wavefront w multiplies
+// tile rows 32 (w / 2) .. +32 against weight row blocks 2 (w % 2), +1:
+// acc[j] += X . W^T, operands read from LDS.
 template <class T>
 __device__ void gemm_tile(const TileRows &tr, const PackedGeometry &g, const __bf16 *x, uint64_t ldx,
-                          uint32_t xrow, bool active, uint32_t steps, __bf16 *wlds, f32x16 (&acc)[4]) {
-    const uint32_t tid = threadIdx.x, lane = tid & 63;
-    WeightStep<T> ws;
-    XStep xs[2];
-    ws.load(tr, g, 0, tid);
-    if (active) xs[0].load(x, ldx, xrow, 0, lane);
-    for (uint32_t st = 0; st < steps; ++st) {
-        __bf16 *wbuf = wlds + (st & 1) * kWBufElems;
-        ws.store(wbuf, tid);
-        if (st + 1 < steps) ws.load(tr, g, st + 1, tid);
-        __syncthreads();
-        if (active) {
-            XStep &cur = xs[st & 1];
-            if (st + 1 < steps) xs[(st + 1) & 1].load(x, ldx, xrow, (st + 1) * kStepK, lane);
+                          uint32_t xrow, bool active, uint32_t steps, __bf16 *lds, f32x16 (&acc)[2]) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, mb = tid >> 7, nb0 = 2 * ((tid >> 6) & 1);
+    const uint8_t *wrow;
+    uint32_t rrow;
+    tr.at(tid >> 2, wrow, rrow);
+    WeightStep<T> ws[kLead];
+    XStep xs[kLead];
+    const uint32_t last = steps - 1;
 #pragma unroll
-            for (uint32_t kk = 0; kk < kStepK / 16; ++kk) {
+    for (uint32_t p = 0; p < kLead; ++p) {
+        ws[p].load(wrow, rrow, g, p < last ? p : last, tid);
+        xs[p].load(x, ldx, xrow, p < last ? p : last, tid);
+    }
+    for (uint32_t st0 = 0; st0 < steps; st0 += kLead) {
 #pragma unroll
-                for (uint32_t nb = 0; nb < 4; ++nb) {
-                    const uint4 bv = *reinterpret_cast<const uint4 *>(
-                        wbuf + (32 * nb + (lane & 31)) * kWStride + 16 * kk + 8 * (lane >> 5));
-                    acc[nb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(cur.f[kk], __builtin_bit_cast(bf16x8, bv),
-                                                                     acc[nb], 0, 0, 0);
+        for (uint32_t u = 0; u < kLead; ++u) {
+            const uint32_t st = st0 + u;
+            if (st >= steps) break;
+            __bf16 *wbuf = lds + (st & 1) * 2 * kWBufElems;
+            __bf16 *xbuf = wbuf + kWBufElems;
+            ws[u].store(wbuf, tid);
+            xs[u].store(xbuf, tid);
+            const uint32_t nxt = st + kLead < last ? st + kLead : last;
+            ws[u].load(wrow, rrow, g, nxt, tid);
+            xs[u].load(x, ldx, xrow, nxt, tid);
+            __syncthreads();
+            if (active) {
+                const uint32_t arow = 32 * mb + (lane & 31);
+#pragma unroll
+                for (uint32_t kk = 0; kk < kStepK / 16; ++kk) {
+                    const uint32_t gr = 2 * kk + (lane >> 5);
+                    const bf16x8 av = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(xbuf + tile_offset(arow, gr)));
+#pragma unroll
+                    for (uint32_t j = 0; j < 2; ++j) {
+                        const uint32_t brow = 32 * (nb0 + j) + (lane & 31);
+                        const uint4 bv = *reinterpret_cast<const uint4 *>(wbuf + tile_offset(brow, gr));
+                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bv), acc[j], 0,
+                                                                        0, 0);
+                    }
                 }
             }
         }
@@ -278,7 +325,7 @@ __device__ inline bool row_tile(const uint32_t *tiles, uint32_t mt, uint32_t exp
     e = tiles[1 + 3 * mt];
     row0 = tiles[2 + 3 * mt];
     rows = tiles[3 + 3 * mt];
-    return e < experts && rows > 0 && rows <= 32 * (kGemmThreads / 64) && row0 <= pairs && rows <= pairs - row0;
+    return e < experts && rows > 0 && rows <= kPrefillTileRows && row0 <= pairs && rows <= pairs - row0;
 }
 
 // ------------------------------------------------------------------ kernels --
@@ -302,76 +349,76 @@ __global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ h
     *reinterpret_cast<uint4 *>(x + static_cast<uint64_t>(s) * hidden + p0) = make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// Gate and up of 64 ffn rows (tile nt) for one row tile, SwiGLU, and the
-// activations written as bf16 in the down projection's packed K order.
-// grid: (ffn / 64, max row tiles).
+// Gate and up of 64 ffn rows for one row tile, SwiGLU, and the activations
+// written as bf16 in the down projection's packed K order.
+// grid: (max row tiles, ffn / 64): row tiles of one ffn slice run together,
+// so tiles of one expert share the slice's weights through the caches.
 template <class T, class TD>
 __global__ __launch_bounds__(kGemmThreads) void gate_up_gemm_kernel(ExpertArgs a, const uint32_t *__restrict__ tiles,
                                                                      uint32_t pairs, const __bf16 *__restrict__ x,
                                                                      __bf16 *__restrict__ act) {
-    extern __shared__ __align__(16) __bf16 wlds[];
+    extern __shared__ __align__(16) __bf16 tiles_lds[];
     uint32_t e, row0, rows;
-    if (!row_tile(tiles, blockIdx.y, a.experts, pairs, e, row0, rows)) return;
+    if (!row_tile(tiles, blockIdx.x, a.experts, pairs, e, row0, rows)) return;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t n0 = blockIdx.x * 64;
-    TileRows tr{static_cast<const uint8_t *>(a.gate[e]), static_cast<const uint8_t *>(a.up[e]), n0, n0, 64};
-    const uint32_t m_local = 32 * wave + (lane & 31);
-    const bool active = 32 * wave < rows;
-    const uint32_t xrow = row0 + (m_local < rows ? m_local : rows - 1);
-    f32x16 acc[4];
+    const uint32_t n0 = blockIdx.y * 64;
+    const TileRows tr{static_cast<const uint8_t *>(a.gate[e]), static_cast<const uint8_t *>(a.up[e]), n0, true};
+    const uint32_t mb = wave >> 1;
+    const bool active = 32 * mb < rows;
+    const uint32_t xr = tid >> 2; // the tile row this thread copies
+    const uint32_t xrow = row0 + (xr < rows ? xr : rows - 1);
+    f32x16 acc[2];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
-    gemm_tile<T>(tr, a.gu, x, a.hidden, xrow, active, a.hidden / kStepK, wlds, acc);
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+    gemm_tile<T>(tr, a.gu, x, a.hidden, xrow, active, a.hidden / kStepK, tiles_lds, acc);
     if (!active) return;
     const uint32_t F = a.ffn;
+    // acc[0] = gate, acc[1] = up of ffn row n0 + 32 (wave % 2) + lane % 32
+    const uint32_t n = n0 + 32 * (wave & 1) + (lane & 31);
+    const uint32_t col = n / TD::kChunkK * TD::kChunkK + TD::pos(n % TD::kChunkK);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const uint32_t m = 32 * wave + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const uint32_t m = 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m >= rows) continue;
-        __bf16 *dst = act + static_cast<uint64_t>(row0 + m) * F;
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            const uint32_t n = n0 + 32 * nb + (lane & 31);
-            const float gv = acc[nb][r], uv = acc[nb + 2][r];
-            const float sv = gv / (1.0f + expf(-gv)) * uv;
-            dst[n / TD::kChunkK * TD::kChunkK + TD::pos(n % TD::kChunkK)] = static_cast<__bf16>(sv);
-        }
+        const float gv = acc[0][r], uv = acc[1][r];
+        act[static_cast<uint64_t>(row0 + m) * F + col] = static_cast<__bf16>(gv / (1.0f + expf(-gv)) * uv);
     }
 }
 
 // Down rows [128 nt, +128) for one row tile into D [pairs x hidden] f32.
-// grid: (hidden / 128, max row tiles).
+// grid: (max row tiles, hidden / 128).
 template <class T>
 __global__ __launch_bounds__(kGemmThreads) void down_gemm_kernel(ExpertArgs a, const uint32_t *__restrict__ tiles,
                                                                   uint32_t pairs, const __bf16 *__restrict__ act,
                                                                   float *__restrict__ dn) {
-    extern __shared__ __align__(16) __bf16 wlds[];
+    extern __shared__ __align__(16) __bf16 tiles_lds[];
     uint32_t e, row0, rows;
-    if (!row_tile(tiles, blockIdx.y, a.experts, pairs, e, row0, rows)) return;
+    if (!row_tile(tiles, blockIdx.x, a.experts, pairs, e, row0, rows)) return;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t n0 = blockIdx.x * kTileN;
-    const uint8_t *w = static_cast<const uint8_t *>(a.down[e]);
-    TileRows tr{w, w, n0, n0, kTileN};
-    const uint32_t m_local = 32 * wave + (lane & 31);
-    const bool active = 32 * wave < rows;
-    const uint32_t xrow = row0 + (m_local < rows ? m_local : rows - 1);
-    f32x16 acc[4];
+    const uint32_t n0 = blockIdx.y * kTileN;
+    const TileRows tr{static_cast<const uint8_t *>(a.down[e]), nullptr, n0, false};
+    const uint32_t mb = wave >> 1;
+    const bool active = 32 * mb < rows;
+    const uint32_t xr = tid >> 2; // the tile row this thread copies
+    const uint32_t xrow = row0 + (xr < rows ? xr : rows - 1);
+    f32x16 acc[2];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[nb][r] = 0.0f;
-    gemm_tile<T>(tr, a.dn, act, a.ffn, xrow, active, a.ffn / kStepK, wlds, acc);
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+    gemm_tile<T>(tr, a.dn, act, a.ffn, xrow, active, a.ffn / kStepK, tiles_lds, acc);
     if (!active) return;
     const uint32_t H = a.hidden;
+    const uint32_t nb0 = 2 * (wave & 1);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-        const uint32_t m = 32 * wave + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const uint32_t m = 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m >= rows) continue;
         float *dst = dn + static_cast<uint64_t>(row0 + m) * H + n0 + (lane & 31);
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) dst[32 * nb] = acc[nb][r];
+        for (int j = 0; j < 2; ++j) dst[32 * (nb0 + j)] = acc[j][r];
     }
 }
 
@@ -404,17 +451,17 @@ int launch_gather(const float *h, uint32_t hidden, uint32_t tokens, const uint32
 
 template <class T, class TD>
 int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s) {
-    const size_t lds = 2ull * kWBufElems * sizeof(__bf16);
+    const size_t lds = 4ull * kWBufElems * sizeof(__bf16); // two (weights, activations) tile pairs
     auto gu = gate_up_gemm_kernel<T, TD>;
     auto dn = down_gemm_kernel<TD>;
     if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds)) return rc;
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds)) return rc;
     if (b.pairs == 0) return FMX_OK;
     if (int rc = launch_gather<T>(b.h, a.hidden, b.tokens, b.token_list, b.pairs, b.x, s)) return rc;
-    hipLaunchKernelGGL(gu, dim3(a.ffn / 64, max_tiles), dim3(kGemmThreads), lds, s, a, b.tiles, b.pairs, b.x,
+    hipLaunchKernelGGL(gu, dim3(max_tiles, a.ffn / 64), dim3(kGemmThreads), lds, s, a, b.tiles, b.pairs, b.x,
                        b.act);
     FMX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(dn, dim3(a.hidden / kTileN, max_tiles), dim3(kGemmThreads), lds, s, a, b.tiles, b.pairs,
+    hipLaunchKernelGGL(dn, dim3(max_tiles, a.hidden / kTileN), dim3(kGemmThreads), lds, s, a, b.tiles, b.pairs,
                        b.act, b.dn);
     FMX_LAUNCH_CHECK();
     return FMX_OK;

@@ -17,8 +17,8 @@ struct PrefillBuffers {
     float *dn;                   // [pairs x hidden] down projections
 };
 
-// Token-expert pairs per row tile of the grouped GEMMs (8 wavefronts x 32).
-constexpr uint32_t kPrefillTileRows = 256;
+// Token-expert pairs per row tile of the grouped GEMMs (4 blocks of 32).
+constexpr uint32_t kPrefillTileRows = 128;
 
 // The grouped GEMMs need block-type experts with hidden and ffn multiples of
 // the K step (128), of the types' chunk sizes and of the N tiles (hidden % 128,
