@@ -108,41 +108,47 @@ struct Q40 {
                                 uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
         const float4 *xs = reinterpret_cast<const float4 *>(lds) + tb0 * 8 + l;
         const float *s8 = lds + nb_tile * 32 + tb0 * 8 + l;
-        float4 xv[8];
-        float sx8[8];
+        // two halves of four blocks: each half's LDS reads are issued before its
+        // arithmetic (bounded register use)
 #pragma unroll
-        for (uint32_t j = 0; j < 8; ++j) {
-            const uint32_t jr = FULL || j < nblk ? j : 0;
-            xv[j] = xs[jr * 8];
-            sx8[j] = s8[jr * 8];
-        }
+        for (uint32_t half = 0; half < 2; ++half) {
+            float4 xv[4];
+            float sx8[4];
 #pragma unroll
-        for (uint32_t jj = 0; jj < 4; ++jj) {
-            // dword jj holds blocks 2jj and 2jj+1: bytes (A, B, A', B')
-            uint32_t lo4[NR], hi4[NR], sw[NR];
-#pragma unroll
-            for (int i = 0; i < NR; ++i) {
-                const uint32_t qw = jj == 0 ? k[i].q.x : jj == 1 ? k[i].q.y : jj == 2 ? k[i].q.z : k[i].q.w;
-                sw[i] = jj == 0 ? k[i].s.x : jj == 1 ? k[i].s.y : jj == 2 ? k[i].s.z : k[i].s.w;
-                lo4[i] = qw & 0x0F0F0F0Fu;
-                hi4[i] = (qw >> 4) & 0x0F0F0F0Fu;
+            for (uint32_t q = 0; q < 4; ++q) {
+                const uint32_t j = 4 * half + q;
+                const uint32_t jr = FULL || j < nblk ? j : 0;
+                xv[q] = xs[jr * 8];
+                sx8[q] = s8[jr * 8];
             }
 #pragma unroll
-            for (uint32_t h = 0; h < 2; ++h) {
-                const uint32_t j = 2 * jj + h;
-                if (!FULL && j >= nblk) break;
+            for (uint32_t jj = 2 * half; jj < 2 * half + 2; ++jj) {
+                // dword jj holds blocks 2jj and 2jj+1: bytes (A, B, A', B')
+                uint32_t lo4[NR], hi4[NR], sw[NR];
 #pragma unroll
                 for (int i = 0; i < NR; ++i) {
-                    const float qa = h ? ubyte2(lo4[i]) : ubyte0(lo4[i]);
-                    const float qb = h ? ubyte3(lo4[i]) : ubyte1(lo4[i]);
-                    const float qc = h ? ubyte2(hi4[i]) : ubyte0(hi4[i]);
-                    const float qd = h ? ubyte3(hi4[i]) : ubyte1(hi4[i]);
-                    // lo = fma(q[l], x[l], q[8+l]*x[8+l]); hi likewise for 16+l, 24+l
-                    const float lo = fma_rn(qa, xv[j].x, qb * xv[j].y);
-                    const float hi = fma_rn(qc, xv[j].z, qd * xv[j].w);
-                    const float c = (lo + hi) - sx8[j];
-                    const float d = half_bits_to_float(h ? (sw[i] >> 16) : (sw[i] & 0xFFFFu));
-                    t[i] = fma_rn(c, d, t[i]);
+                    const uint32_t qw = jj == 0 ? k[i].q.x : jj == 1 ? k[i].q.y : jj == 2 ? k[i].q.z : k[i].q.w;
+                    sw[i] = jj == 0 ? k[i].s.x : jj == 1 ? k[i].s.y : jj == 2 ? k[i].s.z : k[i].s.w;
+                    lo4[i] = qw & 0x0F0F0F0Fu;
+                    hi4[i] = (qw >> 4) & 0x0F0F0F0Fu;
+                }
+#pragma unroll
+                for (uint32_t h = 0; h < 2; ++h) {
+                    const uint32_t j = 2 * jj + h, q = j - 4 * half;
+                    if (!FULL && j >= nblk) break;
+#pragma unroll
+                    for (int i = 0; i < NR; ++i) {
+                        const float qa = h ? ubyte2(lo4[i]) : ubyte0(lo4[i]);
+                        const float qb = h ? ubyte3(lo4[i]) : ubyte1(lo4[i]);
+                        const float qc = h ? ubyte2(hi4[i]) : ubyte0(hi4[i]);
+                        const float qd = h ? ubyte3(hi4[i]) : ubyte1(hi4[i]);
+                        // lo = fma(q[l], x[l], q[8+l]*x[8+l]); hi likewise for 16+l, 24+l
+                        const float lo = fma_rn(qa, xv[q].x, qb * xv[q].y);
+                        const float hi = fma_rn(qc, xv[q].z, qd * xv[q].w);
+                        const float c = (lo + hi) - sx8[q];
+                        const float d = half_bits_to_float(h ? (sw[i] >> 16) : (sw[i] & 0xFFFFu));
+                        t[i] = fma_rn(c, d, t[i]);
+                    }
                 }
             }
         }
@@ -365,46 +371,62 @@ __device__ __forceinline__ void run_chunks_pf(const typename T::Row (&rows)[NR],
 // A row stream with PF chunks per row in flight across LDS tiles: prime()
 // requests chunks 0..PF-1 (before the first tile is staged, so the weight
 // loads overlap the staging); run() consumes chunks [c0, c1) of the current
-// tile and keeps requesting chunk c + PF up to the row's last chunk, so the
-// loads of the next tile are already in flight when its staging starts.
+// tile and keeps requesting chunk c + PF, so the loads of the next tile are
+// already in flight when its staging starts.
 // The chunks live in a ring of kSlots = PF + 1 register slots: the load for
 // chunk c + PF goes into the slot chunk c - 1 just left, before chunk c is
-// consumed, with every slot index a compile-time constant. Every tile must
-// start at a multiple of kSlots chunks.
+// consumed, with every slot index a compile-time constant. Every load is
+// issued unconditionally (past the row's last chunk it re-reads that chunk,
+// which the caches hold): a load under a branch makes the compiler's wait
+// counts conservative, and it then waits for every load in flight before
+// each chunk, which removes the prefetch. Every tile must start at a multiple
+// of kSlots chunks.
 template <class T, int NR, int PF>
 struct ChunkStream {
     static constexpr int kSlots = PF + 1;
     typename T::Chunk buf[kSlots][NR];
 
     __device__ __forceinline__ void prime(const typename T::Row (&rows)[NR], uint32_t c_end) {
+        const uint32_t last = c_end - 1;
 #pragma unroll
-        for (int p = 0; p < PF; ++p)
-            if (static_cast<uint32_t>(p) < c_end) {
+        for (int p = 0; p < PF; ++p) {
+            const uint32_t c = static_cast<uint32_t>(p) < last ? static_cast<uint32_t>(p) : last;
 #pragma unroll
-                for (int i = 0; i < NR; ++i) buf[p][i] = T::load(rows[i], p);
-            }
+            for (int i = 0; i < NR; ++i) buf[p][i] = T::load(rows[i], c);
+        }
     }
 
     __device__ __forceinline__ void run(const typename T::Row (&rows)[NR], uint32_t c0, uint32_t c1,
                                         uint32_t c_end, uint32_t blocks, uint32_t tile_b0,
                                         uint32_t nb_tile, const float *lds, uint32_t l, float (&t)[NR]) {
         const uint32_t full_end = blocks / T::kPerChunk; // chunks [0, full_end) hold kPerChunk blocks
-        for (uint32_t c = c0; c < c1; c += kSlots) {
+        const uint32_t last = c_end - 1;
+        const uint32_t cf = c1 < full_end ? c1 : full_end;
+        uint32_t c = c0;
+        // steady state: whole rings of full chunks, one basic block per ring
+        for (; c + kSlots <= cf; c += kSlots) {
 #pragma unroll
             for (int p = 0; p < kSlots; ++p) {
                 const uint32_t cc = c + p;
-                if (cc >= c1) break;
-                if (cc + PF < c_end) {
+                const uint32_t nxt = cc + PF < last ? cc + PF : last;
 #pragma unroll
-                    for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(rows[i], cc + PF);
-                }
-                const uint32_t b = cc * T::kPerChunk;
-                if (cc < full_end) {
-                    T::template step<NR, true>(buf[p], lds, nb_tile, b - tile_b0, T::kPerChunk, l, t);
-                } else {
-                    T::template step<NR, false>(buf[p], lds, nb_tile, b - tile_b0, blocks - b, l, t);
-                }
+                for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(rows[i], nxt);
+                T::template step<NR, true>(buf[p], lds, nb_tile, cc * T::kPerChunk - tile_b0, T::kPerChunk, l, t);
             }
+        }
+        // the rest of the tile (fewer than kSlots chunks, the last may be partial)
+#pragma unroll
+        for (int p = 0; p < kSlots; ++p) {
+            const uint32_t cc = c + p;
+            if (cc >= c1) break;
+            const uint32_t nxt = cc + PF < last ? cc + PF : last;
+#pragma unroll
+            for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(rows[i], nxt);
+            const uint32_t b = cc * T::kPerChunk;
+            if (cc < full_end)
+                T::template step<NR, true>(buf[p], lds, nb_tile, b - tile_b0, T::kPerChunk, l, t);
+            else
+                T::template step<NR, false>(buf[p], lds, nb_tile, b - tile_b0, blocks - b, l, t);
         }
     }
 };

@@ -75,8 +75,12 @@ __device__ inline float normalised(float x, const float *w, uint32_t k, double s
 // Writes RMSNorm(x) into hs (LDS, H floats); NT threads, x held in registers
 // (H <= kMaxHidden). The norm gains are requested with x. Every thread of the
 // workgroup calls it; ends with a barrier.
+// When some value is too close to a float rounding boundary, the sum is redone
+// in the reference's order from a copy of x in `scratch` (LDS, H floats; may be
+// nullptr, then x is read again from memory); returns true when `scratch` was
+// overwritten.
 template <uint32_t NT>
-__device__ void rmsnorm_lds(const RouteArgs &a, const float *__restrict__ x, float *hs) {
+__device__ bool rmsnorm_lds(const RouteArgs &a, const float *__restrict__ x, float *hs, float *scratch) {
     constexpr uint32_t kPer = kMaxHidden / NT;
     __shared__ double wave_part[NT / 64];
     __shared__ double ss_s;
@@ -120,21 +124,31 @@ __device__ void rmsnorm_lds(const RouteArgs &a, const float *__restrict__ x, flo
     }
     if (unsafe) atomicOr(&unsafe_s, 1);
     __syncthreads();
-    if (unsafe_s) {
-        if (tid == 0) {
-            double ss = 0.0;
-            for (uint32_t k = 0; k < H; ++k) ss += static_cast<double>(x[k]) * static_cast<double>(x[k]);
-            ss_s = ss;
-        }
-        __syncthreads();
-        scale = 1.0 / sqrt(ss_s / static_cast<double>(H) + a.rms_eps);
+    if (!unsafe_s) return false;
+    if (scratch) {
 #pragma unroll
         for (uint32_t i = 0; i < kPer; ++i) {
             const uint32_t k = tid + i * NT;
-            if (k < H) hs[k] = normalised(xv[i], a.norm_weight, k, scale, a.norm_bias);
+            if (k < H) scratch[k] = xv[i];
         }
         __syncthreads();
     }
+    if (tid == 0) {
+        const float *src = scratch ? scratch : x;
+        double ss = 0.0;
+#pragma unroll 16
+        for (uint32_t k = 0; k < H; ++k) ss += static_cast<double>(src[k]) * static_cast<double>(src[k]);
+        ss_s = ss;
+    }
+    __syncthreads();
+    scale = 1.0 / sqrt(ss_s / static_cast<double>(H) + a.rms_eps);
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+        const uint32_t k = tid + i * NT;
+        if (k < H) hs[k] = normalised(xv[i], a.norm_weight, k, scale, a.norm_bias);
+    }
+    __syncthreads();
+    return scratch != nullptr;
 }
 
 // Softmax (float max, double exp and sum, float quotient), stable top-k on
@@ -232,7 +246,7 @@ __global__ __launch_bounds__(NT) void route_kernel(RouteArgs a, uint32_t rows_ld
     const uint32_t c = tid & 15, grp = tid >> 4;
 
     if (rows_lds == 0) {
-        rmsnorm_lds<NT>(a, x + static_cast<uint64_t>(t) * H, hs);
+        rmsnorm_lds<NT>(a, x + static_cast<uint64_t>(t) * H, hs, nullptr);
         for (uint32_t e0 = 0; e0 < E; e0 += NT / 16) {
             const uint32_t e = e0 + grp;
             const uint32_t er = e < E ? e : E - 1;
@@ -246,19 +260,27 @@ __global__ __launch_bounds__(NT) void route_kernel(RouteArgs a, uint32_t rows_ld
             const float4 *src = reinterpret_cast<const float4 *>(a.router + static_cast<uint64_t>(e0) * H);
             float4 *dst = reinterpret_cast<float4 *>(rows);
             const uint32_t n4 = nr * H / 4;
-            for (uint32_t i0 = tid; i0 < n4; i0 += 8 * NT) {
-                float4 v[8];
+            // stage this pass's router rows; a second time when the exact
+            // RMSNorm fallback used the rows' LDS as its copy of x
+            for (int again = 0; again < 2; ++again) {
+                for (uint32_t i0 = tid; i0 < n4; i0 += 8 * NT) {
+                    float4 v[8];
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const uint32_t i = i0 + u * NT;
-                    v[u] = src[i < n4 ? i : n4 - 1];
+                    for (int u = 0; u < 8; ++u) {
+                        const uint32_t i = i0 + u * NT;
+                        v[u] = src[i < n4 ? i : n4 - 1];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        if (i0 + u * NT < n4) dst[i0 + u * NT] = v[u];
                 }
-#pragma unroll
-                for (int u = 0; u < 8; ++u)
-                    if (i0 + u * NT < n4) dst[i0 + u * NT] = v[u];
+                if (e0 > 0 || again) {
+                    __syncthreads();
+                    break;
+                }
+                // ends with a barrier
+                if (!rmsnorm_lds<NT>(a, x + static_cast<uint64_t>(t) * H, hs, rows)) break;
             }
-            if (e0 == 0) rmsnorm_lds<NT>(a, x + static_cast<uint64_t>(t) * H, hs); // ends with a barrier
-            else __syncthreads();
             for (uint32_t r = grp; r < nr; r += NT / 16) {
                 const float v = f32_row_chains(rows + static_cast<uint64_t>(r) * H, hs, H, c);
                 const uint32_t e = e0 + r;
@@ -284,8 +306,10 @@ __device__ inline float swiglu(float gate, float up) {
 
 // Gate and up rows j of the expert at rank blockIdx.y, RJ rows per thread:
 // the first PF chunks of every row are requested before h is staged.
+// Four wavefronts per SIMD (at most 128 VGPRs): the whole grid of a Mixtral
+// expert pair is then resident at once.
 template <class T, int RJ, int PF>
-__global__ __launch_bounds__(kThreads) void gate_up_kernel(ExpertArgs a, const float *__restrict__ h,
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gate_up_kernel(ExpertArgs a, const float *__restrict__ h,
                                                            const uint32_t *__restrict__ ids,
                                                            float *__restrict__ act,
                                                            uint32_t *__restrict__ status) {
@@ -447,7 +471,7 @@ __global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const 
 // ------------------------------------------------------------ launchers --
 
 // Prefetch depth (chunks in flight per row) of each pass.
-constexpr int kGateUpPF = 4;
+constexpr int kGateUpPF = 1;
 constexpr int kDownPF = 8;
 
 template <class T>

@@ -94,6 +94,31 @@ def test_decode_mixtral_shape_q4_0(gpu):
     assert check_layer(gpu, lw, x) == 0
 
 
+def test_route_and_decode_at_rmsnorm_near_ties(gpu):
+    """Tokens whose RMSNorm output lies within 2e-15 of a float midpoint
+    (tests/near_ties.py): the device's parallel sum cannot settle those, and
+    the in-order sum it falls back to must give the oracle's h, logits, ids
+    and weights bit for bit, on the batched route and on the decode layer."""
+    import torch
+    import near_ties as nt
+    lw = wl.make_layer(4096, 256, 8, 2, wl.Q4_0, 21)
+    X = wl.inputs(4096, 6, 23) * np.float32(2.5)
+    x = np.stack([nt.craft(X[t], lw.norm_weight, lw.rms_eps)[0] for t in range(len(X))])
+    dl = DeviceLayer(lw, gpu)
+    xd = torch.from_numpy(x).to(gpu)
+    h, logits, ids, w = dl.route(xd)
+    torch.cuda.synchronize()
+    assert dl.status() == 0
+    hl = host_layer(lw)
+    for i in range(len(x)):
+        hh, lg, pr, ii, ww = hl.route(x[i])
+        assert np.array_equal(bits(to_np(h[i])), bits(hh)), f"h token {i}"
+        assert np.array_equal(bits(to_np(logits[i])), bits(lg)), f"logits token {i}"
+        assert np.array_equal(to_np(ids[i]).astype(np.uint32), ii), f"ids token {i}"
+        assert np.array_equal(bits(to_np(w[i])), bits(ww)), f"weights token {i}"
+    assert check_layer(gpu, lw, x) == 0
+
+
 def test_decode_reports_nonfinite_scores(gpu):
     import torch
     lw = wl.make_layer(64, 128, 4, 2, wl.F32, 3)

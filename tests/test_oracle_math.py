@@ -113,3 +113,24 @@ def test_bucket_inverts_routing_table():
             want = [(t, r) for t in range(T) for r in range(K) if ids[t, r] == e]
             got = list(zip(tl[off[e]:off[e + 1]], rl[off[e]:off[e + 1]]))
             assert got == want
+
+
+def test_rmsnorm_in_order_at_rounding_near_ties():
+    """Tokens crafted so one RMSNorm output lies within 2e-15 (relative) of a
+    float midpoint: the oracle keeps the in-order double sum there, and a
+    pairwise sum of the same squares rounds at least one of them the other
+    way, so these tokens tell the two orders apart."""
+    import near_ties as nt
+    lw = wl.make_layer(4096, 256, 8, 2, wl.Q4_0, 21)
+    X = wl.inputs(4096, 3, 22) * np.float32(2.5)
+    flips = 0
+    for t in range(3):
+        x, k, d = nt.craft(X[t], lw.norm_weight, lw.rms_eps)
+        assert d < 2e-15
+        yd = nt.in_order_rmsnorm_double(x, lw.norm_weight, lw.rms_eps)
+        got = fo.rmsnorm(x, lw.norm_weight, lw.rms_eps)
+        assert np.array_equal(got, yd.astype(np.float32))
+        x64 = x.astype(np.float64)
+        sp = 1.0 / np.sqrt(np.sum(x64 * x64) / x.size + lw.rms_eps)
+        flips += np.float32((x64[k] * sp) * np.float64(lw.norm_weight[k])) != got[k]
+    assert flips >= 1
