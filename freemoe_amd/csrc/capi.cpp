@@ -23,19 +23,24 @@ struct Fence {
     bool deferred = false;
 };
 
-// Workspace layout of the MoE entry points (all offsets 256-byte aligned):
+// Workspace layout of fmx_moe_route / fmx_moe_decode (all offsets 256-byte
+// aligned):
 //   [0, 256)     error word (uint32)
 //   h            hidden floats (decode: one token)
 //   act          top_k x ffn floats (decode)
+//   logits       tokens x experts floats (decode: one token; routing without a
+//                caller's logits array: every token)
 struct DecodeWorkspace {
-    uint64_t h = 0, act = 0, total = 0;
+    uint64_t h = 0, act = 0, logits = 0, total = 0;
 };
 
-DecodeWorkspace decode_workspace(const fmx_moe_layer *L) {
+DecodeWorkspace decode_workspace(const fmx_moe_layer *L, uint32_t tokens) {
     DecodeWorkspace w;
     w.h = kStatusBytes;
     w.act = w.h + align_up(static_cast<uint64_t>(L->hidden) * 4, 256);
-    w.total = w.act + align_up(static_cast<uint64_t>(L->top_k) * L->ffn * 4, 256);
+    w.logits = w.act + align_up(static_cast<uint64_t>(L->top_k) * L->ffn * 4, 256);
+    const uint64_t t = tokens ? tokens : 1;
+    w.total = w.logits + align_up(t * L->experts * 4, 256);
     return w;
 }
 
@@ -43,10 +48,11 @@ DecodeWorkspace decode_workspace(const fmx_moe_layer *L) {
 //   [0, 256) error word | h [tokens x hidden] f32 | offsets [experts + 1] |
 //   token_list, rank_list, slot_of [pairs] | row tiles [1 + 3 * max_tiles] |
 //   x [pairs x hidden] bf16 | act [pairs x ffn] bf16 | dn [pairs x hidden] f32 |
-//   the decode scratch (act of one token) for shapes the GEMMs do not tile
+//   the decode scratch (act of one token) for shapes the GEMMs do not tile |
+//   logits [tokens x experts] f32
 struct PrefillWorkspace {
     uint64_t h = 0, offsets = 0, token_list = 0, rank_list = 0, slot_of = 0, tiles = 0, x = 0, act = 0, dn = 0,
-             dec_act = 0, total = 0;
+             dec_act = 0, logits = 0, total = 0;
     uint32_t pairs = 0, max_tiles = 0;
 };
 
@@ -68,6 +74,7 @@ PrefillWorkspace prefill_workspace(const fmx_moe_layer *L, uint32_t tokens) {
     w.act = take(P * F * 2);
     w.dn = take(P * H * 4);
     w.dec_act = take(static_cast<uint64_t>(L->top_k) * F * 4);
+    w.logits = take(static_cast<uint64_t>(tokens) * E * 4);
     w.total = o;
     return w;
 }
@@ -85,6 +92,8 @@ int validate_layer(const fmx_moe_layer *L) {
     if (L->top_k > 32 || L->experts > 256) return FMX_ERR_INVALID_ARGUMENT;
     if (L->hidden > 16384 || L->hidden % 4) return FMX_ERR_SHAPE_MISMATCH; // routing stages x as float4
     if (!L->router || !L->gate || !L->up || !L->down) return FMX_ERR_INVALID_ARGUMENT;
+    // the routing kernels read x, the router rows and the norm gains as float4
+    if (!aligned16(L->router) || (L->norm_weight && !aligned16(L->norm_weight))) return FMX_ERR_INVALID_ARGUMENT;
     if (L->router_type != FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
     return FMX_OK;
 }
@@ -317,8 +326,7 @@ int fmx_clear_faults(void) {
 
 uint64_t fmx_moe_workspace_bytes(const fmx_moe_layer *L, uint32_t tokens) {
     if (validate_layer(L)) return 0;
-    (void)tokens;
-    return decode_workspace(L).total;
+    return decode_workspace(L, tokens).total;
 }
 
 int fmx_moe_route(const fmx_moe_layer *L, const float *x, uint32_t tokens, float *h, float *logits,
@@ -328,12 +336,16 @@ int fmx_moe_route(const fmx_moe_layer *L, const float *x, uint32_t tokens, float
     if (int rc = validate_layer(L)) return rc;
     if (tokens == 0) return FMX_OK;
     if (!x || !ids || !weights || !workspace || workspace_bytes < kStatusBytes) return FMX_ERR_INVALID_ARGUMENT;
-    if (!aligned16(x)) return FMX_ERR_INVALID_ARGUMENT;
+    if (!aligned16(x) || (h && !aligned16(h))) return FMX_ERR_INVALID_ARGUMENT;
+    const DecodeWorkspace ws = decode_workspace(L, tokens);
+    if (!logits && workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    uint32_t *status = static_cast<uint32_t *>(workspace);
+    uint8_t *base = static_cast<uint8_t *>(workspace);
+    uint32_t *status = reinterpret_cast<uint32_t *>(base);
+    float *lg = logits ? logits : reinterpret_cast<float *>(base + ws.logits);
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
     FMX_LAUNCH_CHECK();
-    return launch_route(route_args(L), x, tokens, h, logits, ids, weights, status, s);
+    return launch_route(route_args(L), x, tokens, h, lg, ids, weights, status, s);
 }
 
 int fmx_moe_decode(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
@@ -343,23 +355,24 @@ int fmx_moe_decode(const fmx_moe_layer *L, const float *x, float *out, uint32_t 
     if (tokens == 0) return FMX_OK;
     if (!x || !out || !ids || !weights || !workspace) return FMX_ERR_INVALID_ARGUMENT;
     if (!aligned16(x) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
-    const DecodeWorkspace ws = decode_workspace(L);
+    const DecodeWorkspace ws = decode_workspace(L, 1);
     if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
     ExpertArgs ea;
-    if (int rc = prepare_expert_args(L, &ea)) return rc;
+    if (int rc = prepare_expert_args(L, route_args(L), &ea)) return rc;
     const RouteArgs ra = route_args(L);
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint8_t *base = static_cast<uint8_t *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(base);
     float *h = reinterpret_cast<float *>(base + ws.h);
+    float *lg = reinterpret_cast<float *>(base + ws.logits);
     DecodeScratch sc;
     sc.act = reinterpret_cast<float *>(base + ws.act);
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
     FMX_LAUNCH_CHECK();
     const uint64_t H = L->hidden, K = L->top_k;
     for (uint32_t t = 0; t < tokens; ++t) {
-        if (int rc = launch_route_decode(ra, x + t * H, h, ids + t * K, weights + t * K, status, s)) return rc;
-        if (int rc = launch_experts(ea, x + t * H, h, ids + t * K, weights + t * K, sc, out + t * H, status, s))
+        if (int rc = launch_route_logits(ra, x + t * H, 1, h, lg, s)) return rc;
+        if (int rc = launch_experts(ea, x + t * H, h, lg, ids + t * K, weights + t * K, sc, out + t * H, status, s))
             return rc;
     }
     return FMX_OK;
@@ -374,16 +387,17 @@ int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uin
     kernel_ms[0] = kernel_ms[1] = kernel_ms[2] = 0.0;
     if (tokens == 0) return FMX_OK;
     if (!x || !out || !ids || !weights || !workspace) return FMX_ERR_INVALID_ARGUMENT;
-    const DecodeWorkspace ws = decode_workspace(L);
+    const DecodeWorkspace ws = decode_workspace(L, 1);
     if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
     ExpertArgs ea;
-    if (int rc = prepare_expert_args(L, &ea)) return rc;
+    if (int rc = prepare_expert_args(L, route_args(L), &ea)) return rc;
     const RouteArgs ra = route_args(L);
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!aligned16(x) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
     uint8_t *base = static_cast<uint8_t *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(base);
     float *h = reinterpret_cast<float *>(base + ws.h);
+    float *lg = reinterpret_cast<float *>(base + ws.logits);
     DecodeScratch sc;
     sc.act = reinterpret_cast<float *>(base + ws.act);
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
@@ -400,11 +414,11 @@ int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uin
         for (uint32_t i = 0; i < n && rc == FMX_OK; ++i) {
             const uint64_t t = t0 + i;
             (void)hipEventRecord(ev[i][0], s);
-            rc = launch_route_decode(ra, x + t * H, h, ids + t * K, weights + t * K, status, s);
+            rc = launch_route_logits(ra, x + t * H, 1, h, lg, s);
             (void)hipEventRecord(ev[i][1], s);
             if (rc == FMX_OK)
-                rc = launch_experts(ea, x + t * H, h, ids + t * K, weights + t * K, sc, out + t * H, status, s,
-                                    ev[i][2]);
+                rc = launch_experts(ea, x + t * H, h, lg, ids + t * K, weights + t * K, sc, out + t * H, status,
+                                    s, ev[i][2]);
             (void)hipEventRecord(ev[i][3], s);
         }
         if (hipStreamSynchronize(s) != hipSuccess) rc = FMX_ERR_LAUNCH_FAILED;
@@ -439,7 +453,7 @@ int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t
     const PrefillWorkspace ws = prefill_workspace(L, tokens);
     if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
     ExpertArgs ea;
-    if (int rc = prepare_expert_args(L, &ea)) return rc;
+    if (int rc = prepare_expert_args(L, route_args(L), &ea)) return rc;
     const RouteArgs ra = route_args(L);
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint8_t *base = static_cast<uint8_t *>(workspace);
@@ -447,7 +461,9 @@ int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t
     float *h = reinterpret_cast<float *>(base + ws.h);
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
     FMX_LAUNCH_CHECK();
-    if (int rc = launch_route(ra, x, tokens, h, nullptr, ids, weights, status, s)) return rc;
+    if (int rc = launch_route(ra, x, tokens, h, reinterpret_cast<float *>(base + ws.logits), ids, weights, status,
+                              s))
+        return rc;
     const uint64_t H = L->hidden, K = L->top_k;
     if (!prefill_gemm_supported(ea)) {
         // shapes the grouped GEMMs do not tile (and F32 experts): the decode
@@ -455,7 +471,7 @@ int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t
         DecodeScratch sc;
         sc.act = reinterpret_cast<float *>(base + ws.dec_act);
         for (uint32_t t = 0; t < tokens; ++t)
-            if (int rc = launch_experts(ea, x + t * H, h + t * H, ids + t * K, weights + t * K, sc, out + t * H,
+            if (int rc = launch_experts(ea, x + t * H, h + t * H, nullptr, ids + t * K, weights + t * K, sc, out + t * H,
                                         status, s))
                 return rc;
         return FMX_OK;

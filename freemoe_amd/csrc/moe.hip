@@ -33,9 +33,7 @@ namespace fmx {
 
 namespace {
 
-constexpr uint32_t kRouteThreads = 256;      // batched routing: one workgroup per token
-constexpr uint32_t kDecodeRouteThreads = 1024;
-constexpr uint32_t kMaxHidden = 16384;         // hidden sizes the routing kernels accept
+constexpr uint32_t kMaxHidden = 16384; // hidden sizes the routing kernels accept
 // Dynamic LDS these kernels request at most: a gfx950 workgroup may hold
 // 160 KiB, of which 1 KiB is left for the kernels' static LDS.
 constexpr size_t kMaxLds = 159 * 1024;
@@ -72,229 +70,300 @@ __device__ inline float normalised(float x, const float *w, uint32_t k, double s
     return static_cast<float>(static_cast<double>(x) * scale * static_cast<double>(gain));
 }
 
-// Writes RMSNorm(x) into hs (LDS, H floats); NT threads, x held in registers
-// (H <= kMaxHidden). The norm gains are requested with x. Every thread of the
-// workgroup calls it; ends with a barrier.
-// When some value is too close to a float rounding boundary, the sum is redone
-// in the reference's order from a copy of x in `scratch` (LDS, H floats; may be
-// nullptr, then x is read again from memory); returns true when `scratch` was
-// overwritten.
+// ------------------------------------------------------------- routing --
+
+__device__ inline double readlane_double(double v, uint32_t lane) {
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+    const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(b), lane);
+    const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane);
+    return __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hi) << 32) | lo));
+}
+
+__device__ inline uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        const uint64_t o = __shfl_xor(static_cast<unsigned long long>(v), m, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+__device__ inline float wave_max_float(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+
+struct Routing {
+    uint32_t id;  // expert of rank (lane) r < top_k
+    float weight; // its routing weight
+};
+
+// Routing of one token from its E <= 256 router logits, by one wavefront
+// (every lane calls it; lane r < top_k receives rank r):
+//   softmax (engine.cpp:378-393): float max, double exp(v - max) summed in
+//   index order, float quotients;
+//   stable top-k (engine.cpp:395-411): the highest probability first, ties to
+//   the lower index; picked as the wave maximum of (probability bits, ~index),
+//   which orders non-negative floats and breaks ties the same way;
+//   weights (engine.cpp:1680-1702): float sum of the picked probabilities in
+//   rank order, optional division by it (plus or at least epsilon), scale.
+// A logit that is not finite (the reference raises INTERNAL_ERROR) sets *bad
+// and yields expert r with weight 0, which keeps every later kernel in bounds.
+__device__ Routing wave_route(const RouteArgs &a, const float *__restrict__ logits, bool *bad) {
+    constexpr int kSlots = 4; // 64 * kSlots >= experts
+    const uint32_t E = a.experts, K = a.top_k, lane = threadIdx.x & 63;
+    float v[kSlots];
+    bool nonfinite = false;
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const uint32_t e = lane + 64 * j;
+        v[j] = e < E ? logits[e] : 0.0f;
+        if (e < E) {
+            nonfinite |= !__builtin_isfinite(v[j]);
+            m = fmaxf(m, v[j]);
+        }
+    }
+    Routing r;
+    if (__any(nonfinite)) {
+        *bad = true;
+        r.id = lane;
+        r.weight = 0.0f;
+        return r;
+    }
+    *bad = false;
+    m = wave_max_float(m);
+    double ex[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j)
+        ex[j] = lane + 64 * j < E ? exp(static_cast<double>(v[j]) - static_cast<double>(m)) : 0.0;
+    double sum = 0.0;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        if (64u * j >= E) break;
+        const uint32_t n = E - 64 * j < 64 ? E - 64 * j : 64;
+        for (uint32_t i = 0; i < n; ++i) sum += readlane_double(ex[j], i);
+    }
+    uint64_t key[kSlots];
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const uint32_t e = lane + 64 * j;
+        const float p = static_cast<float>(ex[j] / sum);
+        key[j] = e < E ? (static_cast<uint64_t>(__float_as_uint(p)) << 32) | (0xFFFFFFFFu - e) : 0;
+    }
+    float total = 0.0f;
+    r.id = 0;
+    r.weight = 0.0f;
+    for (uint32_t k = 0; k < K; ++k) {
+        uint64_t best = key[0];
+#pragma unroll
+        for (int j = 1; j < kSlots; ++j) best = key[j] > best ? key[j] : best;
+        best = wave_max_u64(best);
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j)
+            if (key[j] == best) key[j] = 0;
+        const float p = __uint_as_float(static_cast<uint32_t>(best >> 32));
+        total += p;
+        if (lane == k) {
+            r.id = 0xFFFFFFFFu - static_cast<uint32_t>(best);
+            r.weight = p;
+        }
+    }
+    float wv = r.weight;
+    if (a.weights_norm) {
+        const double den = a.epsilon_additive ? static_cast<double>(total) + a.weights_epsilon
+                                              : fmax(static_cast<double>(total), a.weights_epsilon);
+        wv = static_cast<float>(static_cast<double>(wv) / den);
+    }
+    r.weight = static_cast<float>(static_cast<double>(wv) * a.weights_scale);
+    return r;
+}
+
+// LDS layout of route_rows_kernel: h and the router row each as 16 chains of
+// `cs` floats, element k at (k % 16) * cs + k / 16, so that chain lane c reads
+// its elements in order with 16-byte loads. cs = 4 (mod 64) puts the 16
+// lanes' 16-byte reads on distinct banks.
+__host__ __device__ inline uint32_t route_chain_stride(uint32_t hidden) {
+    const uint32_t cs = hidden / 16 + 1;
+    return cs + (68u - cs % 64u) % 64u;
+}
+
+// Router logit of row blockIdx.y for token blockIdx.x. Every workgroup of the
+// token computes the token's RMSNorm (engine.cpp:723-740) from x held in
+// registers (4 float4 per thread: hidden <= 16 NT), the first one writes it to
+// h_out; then lanes 0-15 run the row's 16 FMA chains of the reference's
+// gemv_avx2_row order (8 lanes x 2 accumulators, lane tree, sequential tail)
+// and lane 0 adds the logit bias (engine.cpp:1611-1616).
+//
+// RMSNorm's sum of squares is a sequential double sum in the reference. Here
+// it is a parallel sum plus a certificate: every normalised value is checked
+// to lie farther from a float rounding boundary than the worst-case
+// difference between the two sums can move it; only when one is that close
+// does one lane redo the sum in the reference's order. Either way h is the
+// reference's h bit for bit.
 template <uint32_t NT>
-__device__ bool rmsnorm_lds(const RouteArgs &a, const float *__restrict__ x, float *hs, float *scratch) {
-    constexpr uint32_t kPer = kMaxHidden / NT;
+__global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float *__restrict__ x,
+                                                        float *__restrict__ h_out, float *__restrict__ logits) {
+    constexpr uint32_t P = 4;
+    extern __shared__ __align__(16) float lds[];
     __shared__ double wave_part[NT / 64];
     __shared__ double ss_s;
     __shared__ int unsafe_s;
-    const uint32_t H = a.hidden, tid = threadIdx.x;
-    float xv[kPer];
+    const uint32_t H = a.hidden, E = a.experts, tid = threadIdx.x;
+    const uint32_t t = blockIdx.x, row = blockIdx.y;
+    const uint32_t H4 = H / 4, cs = route_chain_stride(H);
+    float *hs = lds;
+    float *rs = lds + 16 * cs;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + static_cast<uint64_t>(t) * H);
+    const float4 *r4 = reinterpret_cast<const float4 *>(a.router + static_cast<uint64_t>(row) * H);
+    const float4 *g4 = reinterpret_cast<const float4 *>(a.norm_weight);
+    float4 xv[P], gv[P], rv[P];
+#pragma unroll
+    for (uint32_t i = 0; i < P; ++i) {
+        const uint32_t q = tid + i * NT;
+        const uint32_t qc = q < H4 ? q : H4 - 1;
+        xv[i] = x4[qc];
+        rv[i] = r4[qc];
+        gv[i] = g4 ? g4[qc] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
     double part = 0.0;
 #pragma unroll
-    for (uint32_t i = 0; i < kPer; ++i) {
-        const uint32_t k = tid + i * NT;
-        xv[i] = k < H ? x[k] : 0.0f;
-        if (k < H) hs[k] = a.norm_weight ? a.norm_weight[k] : 1.0f;
+    for (uint32_t i = 0; i < P; ++i) {
+        if (tid + i * NT < H4) {
+            part += static_cast<double>(xv[i].x) * static_cast<double>(xv[i].x);
+            part += static_cast<double>(xv[i].y) * static_cast<double>(xv[i].y);
+            part += static_cast<double>(xv[i].z) * static_cast<double>(xv[i].z);
+            part += static_cast<double>(xv[i].w) * static_cast<double>(xv[i].w);
+        }
     }
-#pragma unroll
-    for (uint32_t i = 0; i < kPer; ++i) part += static_cast<double>(xv[i]) * static_cast<double>(xv[i]);
     part = wave_sum_double(part);
     if ((tid & 63) == 0) wave_part[tid >> 6] = part;
     if (tid == 0) unsafe_s = 0;
     __syncthreads();
-    if (tid == 0) {
-        double ss = wave_part[0];
-        for (uint32_t w = 1; w < NT / 64; ++w) ss += wave_part[w];
-        ss_s = ss;
-    }
-    __syncthreads();
+    double ss = wave_part[0];
+#pragma unroll
+    for (uint32_t w = 1; w < NT / 64; ++w) ss += wave_part[w];
     // |parallel sum - sequential sum| <= (H + 32) u ss; scale moves by half of
-    // that plus a few roundings (see header)
+    // that plus a few roundings
     const double rel_tol = 0.6e-16 * static_cast<double>(H + 32) + 2e-15;
-    double scale = 1.0 / sqrt(ss_s / static_cast<double>(H) + a.rms_eps);
+    float hv[4 * P];
     bool unsafe = false;
+    for (int pass = 0; pass < 2; ++pass) {
+        const double scale = 1.0 / sqrt(ss / static_cast<double>(H) + a.rms_eps);
 #pragma unroll
-    for (uint32_t i = 0; i < kPer; ++i) {
-        const uint32_t k = tid + i * NT;
-        if (k < H) {
-            const float gain = a.norm_weight ? static_cast<float>(a.norm_bias + static_cast<double>(hs[k])) : 1.0f;
-            const double yd = static_cast<double>(xv[i]) * scale * static_cast<double>(gain);
-            const float f = static_cast<float>(yd);
-            hs[k] = f;
-            unsafe |= rounding_unsafe(yd, f, rel_tol);
+        for (uint32_t i = 0; i < P; ++i) {
+            const float xs[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            const float gs[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w};
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                const float gain = g4 ? static_cast<float>(a.norm_bias + static_cast<double>(gs[j])) : 1.0f;
+                const double yd = static_cast<double>(xs[j]) * scale * static_cast<double>(gain);
+                hv[4 * i + j] = static_cast<float>(yd);
+                if (pass == 0 && tid + i * NT < H4) unsafe |= rounding_unsafe(yd, hv[4 * i + j], rel_tol);
+            }
         }
-    }
-    if (unsafe) atomicOr(&unsafe_s, 1);
-    __syncthreads();
-    if (!unsafe_s) return false;
-    if (scratch) {
+        if (pass == 1) break;
+        if (__any(unsafe) && (tid & 63) == 0) unsafe_s = 1;
+        __syncthreads();
+        if (!unsafe_s) break;
+        // the reference's order: x into LDS, one lane sums it
+        float4 *xl = reinterpret_cast<float4 *>(rs);
 #pragma unroll
-        for (uint32_t i = 0; i < kPer; ++i) {
-            const uint32_t k = tid + i * NT;
-            if (k < H) scratch[k] = xv[i];
+        for (uint32_t i = 0; i < P; ++i)
+            if (tid + i * NT < H4) xl[tid + i * NT] = xv[i];
+        __syncthreads();
+        if (tid == 0) {
+            double s = 0.0;
+#pragma unroll 8
+            for (uint32_t q = 0; q < H4; ++q) {
+                const float4 v = xl[q];
+                s += static_cast<double>(v.x) * static_cast<double>(v.x);
+                s += static_cast<double>(v.y) * static_cast<double>(v.y);
+                s += static_cast<double>(v.z) * static_cast<double>(v.z);
+                s += static_cast<double>(v.w) * static_cast<double>(v.w);
+            }
+            ss_s = s;
         }
         __syncthreads();
+        ss = ss_s;
     }
-    if (tid == 0) {
-        const float *src = scratch ? scratch : x;
-        double ss = 0.0;
-#pragma unroll 16
-        for (uint32_t k = 0; k < H; ++k) ss += static_cast<double>(src[k]) * static_cast<double>(src[k]);
-        ss_s = ss;
-    }
-    __syncthreads();
-    scale = 1.0 / sqrt(ss_s / static_cast<double>(H) + a.rms_eps);
+    // h and the router row into the chain layout
 #pragma unroll
-    for (uint32_t i = 0; i < kPer; ++i) {
-        const uint32_t k = tid + i * NT;
-        if (k < H) hs[k] = normalised(xv[i], a.norm_weight, k, scale, a.norm_bias);
-    }
-    __syncthreads();
-    return scratch != nullptr;
-}
-
-// Softmax (float max, double exp and sum, float quotient), stable top-k on
-// the probabilities (ties to the lower index) and the routing weights, from
-// the E logits in logit_s (LDS). exps (E doubles) and prob_s (E floats) are
-// LDS scratch. NT threads; every thread of the workgroup calls it.
-template <uint32_t NT>
-__device__ void finish_routing(const RouteArgs &a, const float *logit_s, double *exps, float *prob_s,
-                               uint32_t *__restrict__ ids, float *__restrict__ weights,
-                               uint32_t *__restrict__ status) {
-    __shared__ float max_s;
-    __shared__ int bad_s;
-    __shared__ double sum_s;
-    const uint32_t E = a.experts, K = a.top_k, tid = threadIdx.x;
-    if (tid == 0) {
-        float m = logit_s[0];
-        int bad = 0;
-        for (uint32_t e = 0; e < E; ++e) {
-            if (!__builtin_isfinite(logit_s[e])) bad = 1;
-            if (logit_s[e] > m) m = logit_s[e];
-        }
-        max_s = m;
-        bad_s = bad;
-    }
-    __syncthreads();
-    if (bad_s) {
-        // The reference raises INTERNAL_ERROR here. Record it and emit a
-        // routing that keeps every later kernel in bounds.
-        if (tid == 0) atomicOr(status, STATUS_NONFINITE_SCORE);
-        for (uint32_t i = tid; i < K; i += NT) {
-            ids[i] = i < E ? i : 0;
-            weights[i] = 0.0f;
-        }
-        return;
-    }
-    for (uint32_t e = tid; e < E; e += NT) exps[e] = exp(static_cast<double>(logit_s[e]) - static_cast<double>(max_s));
-    __syncthreads();
-    if (tid == 0) {
-        double s = 0.0;
-        for (uint32_t e = 0; e < E; ++e) s += exps[e];
-        sum_s = s;
-    }
-    __syncthreads();
-    for (uint32_t e = tid; e < E; e += NT) prob_s[e] = static_cast<float>(exps[e] / sum_s);
-    __syncthreads();
-    if (tid == 0) {
-        uint32_t chosen[32];
-        float wv[32];
-        float total = 0.0f;
-        for (uint32_t r = 0; r < K; ++r) {
-            uint32_t best = E;
-            for (uint32_t e = 0; e < E; ++e) {
-                bool taken = false;
-                for (uint32_t q = 0; q < r; ++q) taken |= chosen[q] == e;
-                if (taken) continue;
-                if (best == E || prob_s[e] > prob_s[best]) best = e;
+    for (uint32_t i = 0; i < P; ++i) {
+        const uint32_t q = tid + i * NT;
+        if (q < H4) {
+            const uint32_t s = q >> 2, c0 = (q & 3) * 4;
+            const float rr[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                hs[(c0 + j) * cs + s] = hv[4 * i + j];
+                rs[(c0 + j) * cs + s] = rr[j];
             }
-            chosen[r] = best;
+            if (row == 0 && h_out)
+                reinterpret_cast<float4 *>(h_out + static_cast<uint64_t>(t) * H)[q] =
+                    make_float4(hv[4 * i], hv[4 * i + 1], hv[4 * i + 2], hv[4 * i + 3]);
         }
-        for (uint32_t r = 0; r < K; ++r) {
-            wv[r] = prob_s[chosen[r]];
-            total += wv[r];
+    }
+    __syncthreads();
+    if (tid < 16) {
+        const uint32_t c = tid, S = H / 16, n16 = S * 16;
+        const float4 *h4 = reinterpret_cast<const float4 *>(hs + c * cs);
+        const float4 *w4 = reinterpret_cast<const float4 *>(rs + c * cs);
+        float acc = 0.0f;
+#pragma unroll 8
+        for (uint32_t i = 0; i < S / 4; ++i) {
+            const float4 hq = h4[i], wq = w4[i];
+            acc = fma_rn(wq.x, hq.x, acc);
+            acc = fma_rn(wq.y, hq.y, acc);
+            acc = fma_rn(wq.z, hq.z, acc);
+            acc = fma_rn(wq.w, hq.w, acc);
         }
-        if (a.weights_norm) {
-            const double den = a.epsilon_additive ? static_cast<double>(total) + a.weights_epsilon
-                                                  : fmax(static_cast<double>(total), a.weights_epsilon);
-            for (uint32_t r = 0; r < K; ++r) wv[r] = static_cast<float>(static_cast<double>(wv[r]) / den);
-        }
-        for (uint32_t r = 0; r < K; ++r) {
-            ids[r] = chosen[r];
-            weights[r] = static_cast<float>(static_cast<double>(wv[r]) * a.weights_scale);
-        }
+        for (uint32_t s = S / 4 * 4; s < S; ++s) acc = fma_rn(rs[c * cs + s], hs[c * cs + s], acc);
+        const bool tail8 = H - n16 >= 8;
+        if (tail8 && c < 8) acc = fma_rn(rs[c * cs + S], hs[c * cs + S], acc);
+        const float tt = acc + lane_xor(acc, 8);
+        float total = hsum8_lanes(tt);
+        for (uint32_t k = tail8 ? n16 + 8 : n16; k < H; ++k)
+            total = fma_rn(rs[(k - n16) * cs + S], hs[(k - n16) * cs + S], total);
+        if (c == 0) logits[static_cast<uint64_t>(t) * E + row] = a.router_bias ? total + a.router_bias[row] : total;
     }
 }
 
-// Routing, one workgroup of NT threads per token. rows_lds = 0: the 16 chain
-// lanes of a router row read it from global memory (batched prefill: many
-// tokens in flight hide the latency). rows_lds > 0: the router is staged into
-// LDS rows_lds rows at a time with every thread's loads in flight together,
-// and the chains read LDS (decode: one token, latency exposed).
-template <uint32_t NT>
-__global__ __launch_bounds__(NT) void route_kernel(RouteArgs a, uint32_t rows_lds, const float *__restrict__ x,
-                                                   float *__restrict__ h_out, float *__restrict__ logits_out,
-                                                   uint32_t *__restrict__ ids, float *__restrict__ weights,
-                                                   uint32_t *__restrict__ status) {
-    extern __shared__ __align__(16) double lds_d[];
-    const uint32_t H = a.hidden, E = a.experts, K = a.top_k;
-    const uint32_t tid = threadIdx.x, t = blockIdx.x;
-    double *exps = lds_d;                                   // [E]
-    float *hs = reinterpret_cast<float *>(lds_d + E);       // [H]
-    float *logit_s = hs + H;                                // [E]
-    float *prob_s = logit_s + E;                            // [E]
-    float *rows = reinterpret_cast<float *>(reinterpret_cast<char *>(lds_d) +
-                                            align_up(E * sizeof(double) + (H + 2 * E) * sizeof(float), 16));
-    const uint32_t c = tid & 15, grp = tid >> 4;
-
-    if (rows_lds == 0) {
-        rmsnorm_lds<NT>(a, x + static_cast<uint64_t>(t) * H, hs, nullptr);
-        for (uint32_t e0 = 0; e0 < E; e0 += NT / 16) {
-            const uint32_t e = e0 + grp;
-            const uint32_t er = e < E ? e : E - 1;
-            const float v = f32_row_chains(a.router + static_cast<uint64_t>(er) * H, hs, H, c);
-            if (c == 0 && e < E) logit_s[e] = a.router_bias ? v + a.router_bias[e] : v;
-        }
-    } else {
-        for (uint32_t e0 = 0; e0 < E; e0 += rows_lds) {
-            const uint32_t nr = E - e0 < rows_lds ? E - e0 : rows_lds;
-            if (e0 > 0) __syncthreads(); // the previous rows' chains are done
-            const float4 *src = reinterpret_cast<const float4 *>(a.router + static_cast<uint64_t>(e0) * H);
-            float4 *dst = reinterpret_cast<float4 *>(rows);
-            const uint32_t n4 = nr * H / 4;
-            // stage this pass's router rows; a second time when the exact
-            // RMSNorm fallback used the rows' LDS as its copy of x
-            for (int again = 0; again < 2; ++again) {
-                for (uint32_t i0 = tid; i0 < n4; i0 += 8 * NT) {
-                    float4 v[8];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        const uint32_t i = i0 + u * NT;
-                        v[u] = src[i < n4 ? i : n4 - 1];
-                    }
-#pragma unroll
-                    for (int u = 0; u < 8; ++u)
-                        if (i0 + u * NT < n4) dst[i0 + u * NT] = v[u];
-                }
-                if (e0 > 0 || again) {
-                    __syncthreads();
-                    break;
-                }
-                // ends with a barrier
-                if (!rmsnorm_lds<NT>(a, x + static_cast<uint64_t>(t) * H, hs, rows)) break;
-            }
-            for (uint32_t r = grp; r < nr; r += NT / 16) {
-                const float v = f32_row_chains(rows + static_cast<uint64_t>(r) * H, hs, H, c);
-                const uint32_t e = e0 + r;
-                if (c == 0) logit_s[e] = a.router_bias ? v + a.router_bias[e] : v;
-            }
-        }
+// ids / weights of token blockIdx.x from its logits; one wavefront.
+__global__ __launch_bounds__(64) void route_finish_kernel(RouteArgs a, const float *__restrict__ logits,
+                                                          uint32_t *__restrict__ ids,
+                                                          float *__restrict__ weights,
+                                                          uint32_t *__restrict__ status) {
+    const uint32_t t = blockIdx.x, lane = threadIdx.x;
+    bool bad;
+    const Routing r = wave_route(a, logits + static_cast<uint64_t>(t) * a.experts, &bad);
+    if (lane < a.top_k) {
+        ids[static_cast<uint64_t>(t) * a.top_k + lane] = r.id;
+        weights[static_cast<uint64_t>(t) * a.top_k + lane] = r.weight;
     }
-    __syncthreads();
-    if (h_out)
-        for (uint32_t k = tid; k < H; k += NT) h_out[static_cast<uint64_t>(t) * H + k] = hs[k];
-    if (logits_out)
-        for (uint32_t e = tid; e < E; e += NT) logits_out[static_cast<uint64_t>(t) * E + e] = logit_s[e];
-    finish_routing<NT>(a, logit_s, exps, prob_s, ids + static_cast<uint64_t>(t) * K,
-                       weights + static_cast<uint64_t>(t) * K, status);
+    if (bad && lane == 0) atomicOr(status, STATUS_NONFINITE_SCORE);
+}
+
+// The expert of rank `rank` for an expert kernel: from the routing computed
+// in this wavefront when `logits` is given (the first workgroup also stores
+// ids, weights and the error flag for the kernels after it), else from ids.
+__device__ inline uint32_t expert_of_rank(const RouteArgs &ra, const float *__restrict__ logits,
+                                          const uint32_t *__restrict__ ids, uint32_t rank, bool first_block,
+                                          uint32_t *__restrict__ ids_out, float *__restrict__ w_out,
+                                          uint32_t *__restrict__ status) {
+    if (!logits) return ids[rank];
+    bool bad;
+    const Routing r = wave_route(ra, logits, &bad);
+    const uint32_t lane = threadIdx.x & 63;
+    if (first_block && threadIdx.x < 64) {
+        if (lane < ra.top_k) {
+            ids_out[lane] = r.id;
+            w_out[lane] = r.weight;
+        }
+        if (bad && lane == 0) atomicOr(status, STATUS_NONFINITE_SCORE);
+    }
+    return __builtin_amdgcn_readlane(static_cast<int>(r.id), rank);
 }
 
 // ------------------------------------------------------------ experts --
@@ -309,14 +378,13 @@ __device__ inline float swiglu(float gate, float up) {
 // Four wavefronts per SIMD (at most 128 VGPRs): the whole grid of a Mixtral
 // expert pair is then resident at once.
 template <class T, int RJ, int PF>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gate_up_kernel(ExpertArgs a, const float *__restrict__ h,
-                                                           const uint32_t *__restrict__ ids,
-                                                           float *__restrict__ act,
-                                                           uint32_t *__restrict__ status) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gate_up_kernel(
+    ExpertArgs a, const float *__restrict__ h, const float *__restrict__ logits, uint32_t *__restrict__ ids,
+    float *__restrict__ w, float *__restrict__ act, uint32_t *__restrict__ status) {
     extern __shared__ __align__(16) float lds[];
     const uint32_t tid = threadIdx.x, l = tid & 7, slot = tid >> 3;
     const uint32_t rank = blockIdx.y;
-    const uint32_t e = ids[rank];
+    const uint32_t e = expert_of_rank(a.route, logits, ids, rank, blockIdx.x == 0 && rank == 0, ids, w, status);
     if (e >= a.experts) {
         if (tid == 0 && blockIdx.x == 0) atomicOr(status, STATUS_BAD_EXPERT);
         return;
@@ -414,12 +482,13 @@ __global__ __launch_bounds__(kThreads) void down_kernel(ExpertArgs a, const floa
 
 // F32 experts: 16 lanes per row, x read through the cache.
 __global__ __launch_bounds__(kThreads) void gate_up_f32_kernel(ExpertArgs a, const float *__restrict__ h,
-                                                               const uint32_t *__restrict__ ids,
+                                                               const float *__restrict__ logits,
+                                                               uint32_t *__restrict__ ids, float *__restrict__ w,
                                                                float *__restrict__ act,
                                                                uint32_t *__restrict__ status) {
     const uint32_t tid = threadIdx.x, c = tid & 15;
     const uint32_t rank = blockIdx.y;
-    const uint32_t e = ids[rank];
+    const uint32_t e = expert_of_rank(a.route, logits, ids, rank, blockIdx.x == 0 && rank == 0, ids, w, status);
     if (e >= a.experts) {
         if (tid == 0 && blockIdx.x == 0) atomicOr(status, STATUS_BAD_EXPERT);
         return;
@@ -475,8 +544,8 @@ constexpr int kGateUpPF = 1;
 constexpr int kDownPF = 8;
 
 template <class T>
-int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const uint32_t *ids,
-                     const float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
+int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
+                     float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
                      hipEvent_t mid) {
     constexpr int RJ = 1;
     const size_t lds_gu = static_cast<size_t>(a.gu_tile) * T::kLdsFloatsPerBlock * sizeof(float);
@@ -486,8 +555,8 @@ int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const 
     auto dn = down_kernel<T, kDownPF>;
     if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds_gu)) return rc;
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds_dn)) return rc;
-    hipLaunchKernelGGL(gu, dim3(div_up(a.ffn, (kThreads / 8) * RJ), a.top_k), dim3(kThreads), lds_gu, s, a, h, ids,
-                       ws.act, status);
+    hipLaunchKernelGGL(gu, dim3(div_up(a.ffn, (kThreads / 8) * RJ), a.top_k), dim3(kThreads), lds_gu, s, a, h,
+                       logits, ids, w, ws.act, status);
     FMX_LAUNCH_CHECK();
     if (mid) FMX_HIP_TRY(hipEventRecord(mid, s));
     const uint32_t jpw = (kThreads / 8) / a.top_k;
@@ -518,50 +587,40 @@ int allow_lds(const void *fn, size_t bytes) {
     return FMX_OK;
 }
 
-size_t route_lds_bytes(uint32_t hidden, uint32_t experts, uint32_t rows_lds) {
-    const size_t base = static_cast<size_t>(experts) * sizeof(double) + (hidden + 2ull * experts) * sizeof(float);
-    return align_up(base, 16) + static_cast<size_t>(rows_lds) * hidden * sizeof(float);
-}
+size_t route_lds_bytes(uint32_t hidden) { return 2ull * 16 * route_chain_stride(hidden) * sizeof(float); }
 
-// Router rows that fit in LDS next to the routing state (0: none fit).
-uint32_t route_rows_in_lds(const RouteArgs &a) {
-    const size_t base = route_lds_bytes(a.hidden, a.experts, 0);
-    if (a.hidden % 4 || base + a.hidden * sizeof(float) > kMaxLds) return 0;
-    const uint32_t rows = static_cast<uint32_t>((kMaxLds - base) / (a.hidden * sizeof(float)));
-    return rows < a.experts ? rows : a.experts;
-}
-
-// One 1024-thread workgroup per token with the router staged in LDS; when
-// not even one router row fits, 256 threads per token reading it from memory.
-int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
-                 uint32_t *ids, float *weights, uint32_t *status, hipStream_t s) {
-    if (a.hidden > kMaxHidden) return FMX_ERR_SHAPE_MISMATCH;
-    const uint32_t rows = route_rows_in_lds(a);
-    if (rows > 0) {
-        const size_t lds = route_lds_bytes(a.hidden, a.experts, rows);
-        auto k = route_kernel<kDecodeRouteThreads>;
-        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
-        hipLaunchKernelGGL(k, dim3(tokens), dim3(kDecodeRouteThreads), lds, s, a, rows, x, h, logits, ids, weights,
-                           status);
-        FMX_LAUNCH_CHECK();
-        return FMX_OK;
-    }
-    const size_t lds = route_lds_bytes(a.hidden, a.experts, 0);
+// One workgroup per (token, router row): 256 threads up to hidden 4096, 1024
+// beyond (each thread holds 16 elements of the token).
+int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
+                        hipStream_t s) {
+    if (a.hidden > kMaxHidden || a.hidden % 4 || a.experts == 0) return FMX_ERR_SHAPE_MISMATCH;
+    const size_t lds = route_lds_bytes(a.hidden);
     if (lds > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
-    auto k = route_kernel<kRouteThreads>;
-    if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
-    hipLaunchKernelGGL(k, dim3(tokens), dim3(kRouteThreads), lds, s, a, 0u, x, h, logits, ids, weights, status);
+    const dim3 grid(tokens, a.experts);
+    if (a.hidden <= 16 * 256) {
+        auto k = route_rows_kernel<256>;
+        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+        hipLaunchKernelGGL(k, grid, dim3(256), lds, s, a, x, h, logits);
+    } else {
+        auto k = route_rows_kernel<1024>;
+        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+        hipLaunchKernelGGL(k, grid, dim3(1024), lds, s, a, x, h, logits);
+    }
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
 
-int launch_route_decode(const RouteArgs &a, const float *x, float *h, uint32_t *ids, float *weights,
-                        uint32_t *status, hipStream_t s) {
-    return launch_route(a, x, 1, h, nullptr, ids, weights, status, s);
+int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
+                 uint32_t *ids, float *weights, uint32_t *status, hipStream_t s) {
+    if (int rc = launch_route_logits(a, x, tokens, h, logits, s)) return rc;
+    hipLaunchKernelGGL(route_finish_kernel, dim3(tokens), dim3(64), 0, s, a, logits, ids, weights, status);
+    FMX_LAUNCH_CHECK();
+    return FMX_OK;
 }
 
-int prepare_expert_args(const fmx_moe_layer *L, ExpertArgs *a) {
+int prepare_expert_args(const fmx_moe_layer *L, const RouteArgs &route, ExpertArgs *a) {
     ExpertArgs e;
+    e.route = route;
     e.hidden = L->hidden;
     e.ffn = L->ffn;
     e.experts = L->experts;
@@ -595,14 +654,14 @@ int prepare_expert_args(const fmx_moe_layer *L, ExpertArgs *a) {
     return FMX_OK;
 }
 
-int launch_experts(const ExpertArgs &a, const float *x, const float *h, const uint32_t *ids,
-                   const float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
+int launch_experts(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
+                   float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
                    hipEvent_t mid) {
     float *act = ws.act;
     if (a.type_gu == FMX_TYPE_F32) {
         if (a.top_k > kThreads / 16 || a.type_dn != FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
         hipLaunchKernelGGL(gate_up_f32_kernel, dim3(div_up(a.ffn, kThreads / 16), a.top_k), dim3(kThreads), 0, s,
-                           a, h, ids, act, status);
+                           a, h, logits, ids, w, act, status);
         FMX_LAUNCH_CHECK();
         if (mid) FMX_HIP_TRY(hipEventRecord(mid, s));
     }
@@ -615,9 +674,9 @@ int launch_experts(const ExpertArgs &a, const float *x, const float *h, const ui
     }
     if (a.type_gu != a.type_dn) return FMX_ERR_UNSUPPORTED_QUANTISATION;
     switch (a.type_gu) {
-    case FMX_TYPE_Q4_0: return launch_experts_q<Q40>(a, x, h, ids, w, ws, out, status, s, mid);
-    case FMX_TYPE_Q8_0: return launch_experts_q<Q80>(a, x, h, ids, w, ws, out, status, s, mid);
-    case FMX_TYPE_Q4_K: return launch_experts_q<Q4K>(a, x, h, ids, w, ws, out, status, s, mid);
+    case FMX_TYPE_Q4_0: return launch_experts_q<Q40>(a, x, h, logits, ids, w, ws, out, status, s, mid);
+    case FMX_TYPE_Q8_0: return launch_experts_q<Q80>(a, x, h, logits, ids, w, ws, out, status, s, mid);
+    case FMX_TYPE_Q4_K: return launch_experts_q<Q4K>(a, x, h, logits, ids, w, ws, out, status, s, mid);
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }

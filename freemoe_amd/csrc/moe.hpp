@@ -26,6 +26,7 @@ struct ExpertArgs {
     const void *const *down;
     PackedGeometry gu, dn;
     uint32_t gu_tile, dn_tile;
+    RouteArgs route; // softmax / top-k / weight options, for routing from logits
 };
 
 // Device scratch of one decode step (in the caller's workspace).
@@ -33,20 +34,22 @@ struct DecodeScratch {
     float *act; // [top_k x ffn] SwiGLU activations
 };
 
-// LDS of the routing kernel with `rows_lds` router rows staged.
-size_t route_lds_bytes(uint32_t hidden, uint32_t experts, uint32_t rows_lds);
+// Router logits of `tokens` rows of x ([tokens x experts]); h (optional)
+// receives the normalised rows.
+int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
+                        hipStream_t s);
+// launch_route_logits, then ids / weights ([tokens x top_k]) from the logits.
 int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                  uint32_t *ids, float *weights, uint32_t *status, hipStream_t s);
-// Routing of one token by one 1024-thread workgroup with the router staged
-// in LDS (decode).
-int launch_route_decode(const RouteArgs &a, const float *x, float *h, uint32_t *ids, float *weights,
-                        uint32_t *status, hipStream_t s);
-int prepare_expert_args(const fmx_moe_layer *L, ExpertArgs *a);
+int prepare_expert_args(const fmx_moe_layer *L, const RouteArgs &route, ExpertArgs *a);
 // Decode experts for one token: gate/up + SwiGLU into act[top_k x ffn], then
 // down + combine + residual into out[hidden].
+// With `logits` ([experts]), the gate/up kernel computes the token's routing
+// from them and stores it into ids / w (top_k each) for the down kernel and
+// the caller; without, ids / w hold the routing already.
 // `mid`, when given, is recorded between the gate/up and the down launch.
-int launch_experts(const ExpertArgs &a, const float *x, const float *h, const uint32_t *ids,
-                   const float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
+int launch_experts(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
+                   float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
                    hipEvent_t mid = nullptr);
 
 } // namespace fmx

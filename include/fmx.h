@@ -141,11 +141,11 @@ int fmx_matvec(uint32_t type_id, const void *packed, const float *x, float *y,
  * routed experts without a host round trip. */
 typedef struct fmx_moe_layer {
     uint32_t hidden, ffn, experts, top_k;
-    const float *norm_weight;     /* [hidden] RMSNorm gain, NULL = unit gain */
+    const float *norm_weight;     /* [hidden] RMSNorm gain, NULL = unit gain (16-byte aligned) */
     double rms_eps;               /* ModelConfig::rms_eps */
     double norm_bias;             /* 1.0 when norm weights are zero-centred */
     uint32_t router_type;         /* FMX_TYPE_F32 */
-    const void *router;           /* [experts x hidden] raw row-major */
+    const void *router;           /* [experts x hidden] raw row-major (16-byte aligned) */
     const float *router_bias;     /* [experts] logit bias (ffn_gate_inp.bias) or NULL */
     int32_t weights_norm;         /* expert_weights_norm */
     int32_t epsilon_additive;     /* expert_weights_epsilon_additive */
