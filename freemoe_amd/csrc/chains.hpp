@@ -17,34 +17,49 @@
 namespace fmx {
 
 // ------------------------------------------------------------- staging --
+// The first batch of a staging pass (kStageBatch float4 per thread), loaded
+// ahead so a kernel can request x before it knows what else it needs.
+constexpr int kStageBatch = 4;
+struct XBatch {
+    float4 v[kStageBatch];
+};
+
+__device__ __forceinline__ void load_batch(XBatch &b, const float *__restrict__ x, uint32_t e0, uint32_t n,
+                                           uint32_t i0, uint32_t nthreads) {
+    const float4 *src = reinterpret_cast<const float4 *>(x + e0);
+    const uint32_t n4 = n / 4;
+#pragma unroll
+    for (int u = 0; u < kStageBatch; ++u) {
+        const uint32_t i = i0 + u * nthreads;
+        b.v[u] = src[i < n4 ? i : n4 - 1];
+    }
+}
+
 // Copies elements [e0, e0 + n) of x (n a multiple of 4, x + e0 16-byte
 // aligned) into LDS in a lane-major order: element i goes to float
 // slot(i) * 4 + (i % 32) / 8, where a slot (16 bytes) holds the four elements
-// of a 32-element run that lane i % 8 consumes. All of a thread's global
-// loads (up to 8 float4) are in flight together; consecutive elements land in
-// consecutive lanes' slots, kLaneSlots slots apart.
-template <uint32_t kLaneSlots, class Slot>
+// of a 32-element run that lane i % 8 consumes. A thread's global loads go in
+// batches of kStageBatch float4, in flight together; consecutive elements land
+// in consecutive lanes' slots, kLaneSlots slots apart. kPre: `pre` holds the
+// first batch, loaded by load_batch(pre, x, e0, n, tid, nthreads).
+template <uint32_t kLaneSlots, bool kPre, class Slot>
 __device__ __forceinline__ void scatter_lanes(const float *__restrict__ x, uint32_t e0, uint32_t n, float *lds,
-                                              uint32_t tid, uint32_t nthreads, Slot slot) {
-    const float4 *src = reinterpret_cast<const float4 *>(x + e0);
+                                              uint32_t tid, uint32_t nthreads, Slot slot, const XBatch &pre) {
     const uint32_t n4 = n / 4;
-    for (uint32_t i0 = tid; i0 < n4; i0 += 8 * nthreads) {
-        float4 v[8];
+    for (uint32_t i0 = tid; i0 < n4; i0 += kStageBatch * nthreads) {
+        XBatch b;
+        if (kPre && i0 == tid) b = pre;
+        else load_batch(b, x, e0, n, i0, nthreads);
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const uint32_t i = i0 + u * nthreads;
-            v[u] = src[i < n4 ? i : n4 - 1];
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kStageBatch; ++u) {
             const uint32_t i = i0 + u * nthreads;
             if (i < n4) {
                 const uint32_t e = 4 * i;
                 float *d = lds + slot(e) * 4 + ((e & 31) >> 3);
-                d[0] = v[u].x;
-                d[4 * kLaneSlots] = v[u].y;
-                d[8 * kLaneSlots] = v[u].z;
-                d[12 * kLaneSlots] = v[u].w;
+                d[0] = b.v[u].x;
+                d[4 * kLaneSlots] = b.v[u].y;
+                d[8 * kLaneSlots] = b.v[u].z;
+                d[12 * kLaneSlots] = b.v[u].w;
             }
         }
     }
@@ -63,10 +78,11 @@ struct Q40 {
     // xs[b][l] = (x[l], x[8+l], x[16+l], x[24+l]) of block b, then per (b, l)
     // 8 * ((x[l] + x[8+l]) + (x[16+l] + x[24+l])) (the scaling is exact). The
     // caller's barrier after stage() publishes the sums.
-    __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb,
-                                 float *lds, uint32_t tid, uint32_t nthreads) {
-        scatter_lanes<1>(x, b0 * 32, nb * 32, lds, tid, nthreads,
-                      [](uint32_t e) { return (e >> 5) * 8 + (e & 7); });
+    template <bool kPre = false>
+    __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds, uint32_t tid,
+                                 uint32_t nthreads, const XBatch &pre = XBatch()) {
+        scatter_lanes<1, kPre>(x, b0 * 32, nb * 32, lds, tid, nthreads,
+                               [](uint32_t e) { return (e >> 5) * 8 + (e & 7); }, pre);
         __syncthreads();
         const float4 *xs = reinterpret_cast<const float4 *>(lds);
         float *s8 = lds + nb * 32;
@@ -167,10 +183,11 @@ struct Q80 {
     static constexpr uint32_t kLdsFloatsPerBlock = 32;
 
     // xs[b][l] = (x[l], x[8+l], x[16+l], x[24+l]) of block b.
-    __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb,
-                                 float *lds, uint32_t tid, uint32_t nthreads) {
-        scatter_lanes<1>(x, b0 * 32, nb * 32, lds, tid, nthreads,
-                      [](uint32_t e) { return (e >> 5) * 8 + (e & 7); });
+    template <bool kPre = false>
+    __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds, uint32_t tid,
+                                 uint32_t nthreads, const XBatch &pre = XBatch()) {
+        scatter_lanes<1, kPre>(x, b0 * 32, nb * 32, lds, tid, nthreads,
+                               [](uint32_t e) { return (e >> 5) * 8 + (e & 7); }, pre);
         __syncthreads();
     }
 
@@ -243,12 +260,13 @@ struct Q4K {
     // k = 0..3; then per (super-block, g) the low and high 32-element sums in
     // the reference's order (per-lane sums of four, then the 8-lane tree). The
     // caller's barrier after stage() publishes the sums.
-    __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb,
-                                 float *lds, uint32_t tid, uint32_t nthreads) {
+    template <bool kPre = false>
+    __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds, uint32_t tid,
+                                 uint32_t nthreads, const XBatch &pre = XBatch()) {
         // element e of the tile: super-block e/256, group (e%256)/64, half (e%64)/32
-        scatter_lanes<2>(x, b0 * 256, nb * 256, lds, tid, nthreads, [](uint32_t e) {
-            return (((e >> 6) * 8 + (e & 7)) * 2) + ((e >> 5) & 1);
-        });
+        scatter_lanes<2, kPre>(
+            x, b0 * 256, nb * 256, lds, tid, nthreads,
+            [](uint32_t e) { return (((e >> 6) * 8 + (e & 7)) * 2) + ((e >> 5) & 1); }, pre);
         __syncthreads();
         const float4 *xs = reinterpret_cast<const float4 *>(lds);
         float *sums = lds + nb * 256;
@@ -411,6 +429,9 @@ struct ChunkStream {
                 const uint32_t nxt = cc + PF < last ? cc + PF : last;
 #pragma unroll
                 for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(rows[i], nxt);
+                // the scheduler would otherwise sink loads whose data is used
+                // late in a step down to that use, emptying the prefetch ring
+                __builtin_amdgcn_sched_barrier(0);
                 T::template step<NR, true>(buf[p], lds, nb_tile, cc * T::kPerChunk - tile_b0, T::kPerChunk, l, t);
             }
         }

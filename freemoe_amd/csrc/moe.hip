@@ -45,23 +45,23 @@ __device__ inline double wave_sum_double(double v) {
     return v;
 }
 
-// The float after f towards +infinity (f finite).
-__device__ inline float float_up(float f) {
-    if (f == 0.0f) return __uint_as_float(1u);
-    const uint32_t b = __float_as_uint(f);
-    return __uint_as_float((b >> 31) ? b - 1 : b + 1);
-}
-
-// True when float(yd) could change if yd moved by rel_tol of itself: the
-// rounding boundaries around f are the midpoints to its neighbours, exact in
-// double.
-__device__ inline bool rounding_unsafe(double yd, float f, double rel_tol) {
-    if (!__builtin_isfinite(f) || __builtin_isnan(yd)) return true;
-    if (yd == 0.0) return false;
-    const double tol = __builtin_fabs(yd) * rel_tol;
-    const double lo = (static_cast<double>(f) + static_cast<double>(-float_up(-f))) * 0.5;
-    const double hi = (static_cast<double>(f) + static_cast<double>(float_up(f))) * 0.5;
-    return (yd - lo) <= tol || (hi - yd) <= tol;
+// True when float(yd) could change if yd moved by up to tol_ulps(yd) of its
+// own units in the last place. For yd in float's normal range the float
+// grid points are the doubles whose low 29 mantissa bits are zero and the
+// rounding boundaries (midpoints) those whose low 29 bits are 2^28, so the
+// distance to the nearest boundary is |low29 - 2^28| ulps. tol0 = ceil(rel *
+// 2^52) bounds rel * |yd| / ulp(yd) = rel * 2^52 * 1.m from above through the
+// top 8 mantissa bits. Values outside float's normal range (other than 0),
+// infinities and NaN always count as unsafe.
+__device__ inline bool rounding_unsafe(double yd, uint32_t tol0) {
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(yd));
+    const uint32_t hi = static_cast<uint32_t>(b >> 32);
+    const uint32_t ex = (hi >> 20) & 0x7FFu;
+    if (ex < 1023u - 126u || ex >= 1023u + 127u) return yd != 0.0;
+    const uint32_t low29 = static_cast<uint32_t>(b) & 0x1FFFFFFFu;
+    const uint32_t d = low29 >= (1u << 28) ? low29 - (1u << 28) : (1u << 28) - low29;
+    const uint32_t m8 = (hi >> 12) & 0xFFu;
+    return d <= tol0 + ((tol0 * (m8 + 1u)) >> 8) + 1u;
 }
 
 __device__ inline float normalised(float x, const float *w, uint32_t k, double scale,
@@ -247,6 +247,7 @@ __global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float
     // |parallel sum - sequential sum| <= (H + 32) u ss; scale moves by half of
     // that plus a few roundings
     const double rel_tol = 0.6e-16 * static_cast<double>(H + 32) + 2e-15;
+    const uint32_t tol0 = static_cast<uint32_t>(ceil(rel_tol * 4503599627370496.0)); // rel_tol * 2^52
     float hv[4 * P];
     bool unsafe = false;
     for (int pass = 0; pass < 2; ++pass) {
@@ -260,7 +261,7 @@ __global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float
                 const float gain = g4 ? static_cast<float>(a.norm_bias + static_cast<double>(gs[j])) : 1.0f;
                 const double yd = static_cast<double>(xs[j]) * scale * static_cast<double>(gain);
                 hv[4 * i + j] = static_cast<float>(yd);
-                if (pass == 0 && tid + i * NT < H4) unsafe |= rounding_unsafe(yd, hv[4 * i + j], rel_tol);
+                if (pass == 0 && tid + i * NT < H4) unsafe |= rounding_unsafe(yd, tol0);
             }
         }
         if (pass == 1) break;
@@ -384,6 +385,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     extern __shared__ __align__(16) float lds[];
     const uint32_t tid = threadIdx.x, l = tid & 7, slot = tid >> 3;
     const uint32_t rank = blockIdx.y;
+    const uint32_t blocks = a.gu.blocks;
+    // h's first tile is requested before the routing, whose loads it overlaps
+    XBatch hb;
+    load_batch(hb, h, 0, (blocks < a.gu_tile ? blocks : a.gu_tile) * T::kBlock, tid, kThreads);
     const uint32_t e = expert_of_rank(a.route, logits, ids, rank, blockIdx.x == 0 && rank == 0, ids, w, status);
     if (e >= a.experts) {
         if (tid == 0 && blockIdx.x == 0) atomicOr(status, STATUS_BAD_EXPERT);
@@ -403,14 +408,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         t[2 * m] = 0.0f;
         t[2 * m + 1] = 0.0f;
     }
-    const uint32_t blocks = a.gu.blocks;
     const uint32_t c_end = (blocks + T::kPerChunk - 1) / T::kPerChunk;
     ChunkStream<T, 2 * RJ, PF> cs;
     cs.prime(rw, c_end);
     for (uint32_t tb = 0; tb < blocks; tb += a.gu_tile) {
         const uint32_t nb = blocks - tb < a.gu_tile ? blocks - tb : a.gu_tile;
         __syncthreads();
-        T::stage(h, tb, nb, lds, tid, kThreads);
+        if (tb == 0) T::template stage<true>(h, tb, nb, lds, tid, kThreads, hb);
+        else T::stage(h, tb, nb, lds, tid, kThreads);
         __syncthreads();
         cs.run(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, c_end, blocks, tb, nb, lds, l,
                t);
@@ -428,8 +433,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
 // residual (engine.cpp:813-816, 1822). Row slot s handles rank s / jpw, row
 // s % jpw of this workgroup's jpw rows (jpw = 32 / top_k); every rank's
 // activations are staged together, so one workgroup finishes its rows alone.
+// The activations fill the LDS, so one workgroup (one wavefront per SIMD)
+// runs per CU: the wavefront may use every register, which holds a deep
+// prefetch ring.
 template <class T, int PF>
-__global__ __launch_bounds__(kThreads) void down_kernel(ExpertArgs a, const float *__restrict__ x,
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void down_kernel(ExpertArgs a, const float *__restrict__ x,
                                                         const float *__restrict__ act,
                                                         const uint32_t *__restrict__ ids,
                                                         const float *__restrict__ w,
@@ -541,7 +549,7 @@ __global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const 
 
 // Prefetch depth (chunks in flight per row) of each pass.
 constexpr int kGateUpPF = 1;
-constexpr int kDownPF = 8;
+constexpr int kDownPF = 16;
 
 template <class T>
 int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
