@@ -17,19 +17,21 @@
 namespace fmx {
 
 // ------------------------------------------------------------- staging --
-// The first batch of a staging pass (kStageBatch float4 per thread), loaded
-// ahead so a kernel can request x before it knows what else it needs.
-constexpr int kStageBatch = 4;
+// One batch of a staging pass: N float4 per thread, in flight together. A
+// kernel may load the first batch ahead, to request x before it knows what
+// else it needs.
+template <int N>
 struct XBatch {
-    float4 v[kStageBatch];
+    float4 v[N];
 };
 
-__device__ __forceinline__ void load_batch(XBatch &b, const float *__restrict__ x, uint32_t e0, uint32_t n,
+template <int N>
+__device__ __forceinline__ void load_batch(XBatch<N> &b, const float *__restrict__ x, uint32_t e0, uint32_t n,
                                            uint32_t i0, uint32_t nthreads) {
     const float4 *src = reinterpret_cast<const float4 *>(x + e0);
     const uint32_t n4 = n / 4;
 #pragma unroll
-    for (int u = 0; u < kStageBatch; ++u) {
+    for (int u = 0; u < N; ++u) {
         const uint32_t i = i0 + u * nthreads;
         b.v[u] = src[i < n4 ? i : n4 - 1];
     }
@@ -39,19 +41,19 @@ __device__ __forceinline__ void load_batch(XBatch &b, const float *__restrict__ 
 // aligned) into LDS in a lane-major order: element i goes to float
 // slot(i) * 4 + (i % 32) / 8, where a slot (16 bytes) holds the four elements
 // of a 32-element run that lane i % 8 consumes. A thread's global loads go in
-// batches of kStageBatch float4, in flight together; consecutive elements land
-// in consecutive lanes' slots, kLaneSlots slots apart. kPre: `pre` holds the
-// first batch, loaded by load_batch(pre, x, e0, n, tid, nthreads).
-template <uint32_t kLaneSlots, bool kPre, class Slot>
+// batches of N float4; consecutive elements land in consecutive lanes' slots,
+// kLaneSlots slots apart. kPre: `pre` holds the first batch, loaded by
+// load_batch(pre, x, e0, n, tid, nthreads).
+template <uint32_t kLaneSlots, int N, bool kPre, class Slot>
 __device__ __forceinline__ void scatter_lanes(const float *__restrict__ x, uint32_t e0, uint32_t n, float *lds,
-                                              uint32_t tid, uint32_t nthreads, Slot slot, const XBatch &pre) {
+                                              uint32_t tid, uint32_t nthreads, Slot slot, const XBatch<N> &pre) {
     const uint32_t n4 = n / 4;
-    for (uint32_t i0 = tid; i0 < n4; i0 += kStageBatch * nthreads) {
-        XBatch b;
+    for (uint32_t i0 = tid; i0 < n4; i0 += N * nthreads) {
+        XBatch<N> b;
         if (kPre && i0 == tid) b = pre;
         else load_batch(b, x, e0, n, i0, nthreads);
 #pragma unroll
-        for (int u = 0; u < kStageBatch; ++u) {
+        for (int u = 0; u < N; ++u) {
             const uint32_t i = i0 + u * nthreads;
             if (i < n4) {
                 const uint32_t e = 4 * i;
@@ -78,10 +80,10 @@ struct Q40 {
     // xs[b][l] = (x[l], x[8+l], x[16+l], x[24+l]) of block b, then per (b, l)
     // 8 * ((x[l] + x[8+l]) + (x[16+l] + x[24+l])) (the scaling is exact). The
     // caller's barrier after stage() publishes the sums.
-    template <bool kPre = false>
+    template <int N = 8, bool kPre = false>
     __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds, uint32_t tid,
-                                 uint32_t nthreads, const XBatch &pre = XBatch()) {
-        scatter_lanes<1, kPre>(x, b0 * 32, nb * 32, lds, tid, nthreads,
+                                 uint32_t nthreads, const XBatch<N> &pre = XBatch<N>()) {
+        scatter_lanes<1, N, kPre>(x, b0 * 32, nb * 32, lds, tid, nthreads,
                                [](uint32_t e) { return (e >> 5) * 8 + (e & 7); }, pre);
         __syncthreads();
         const float4 *xs = reinterpret_cast<const float4 *>(lds);
@@ -183,10 +185,10 @@ struct Q80 {
     static constexpr uint32_t kLdsFloatsPerBlock = 32;
 
     // xs[b][l] = (x[l], x[8+l], x[16+l], x[24+l]) of block b.
-    template <bool kPre = false>
+    template <int N = 8, bool kPre = false>
     __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds, uint32_t tid,
-                                 uint32_t nthreads, const XBatch &pre = XBatch()) {
-        scatter_lanes<1, kPre>(x, b0 * 32, nb * 32, lds, tid, nthreads,
+                                 uint32_t nthreads, const XBatch<N> &pre = XBatch<N>()) {
+        scatter_lanes<1, N, kPre>(x, b0 * 32, nb * 32, lds, tid, nthreads,
                                [](uint32_t e) { return (e >> 5) * 8 + (e & 7); }, pre);
         __syncthreads();
     }
@@ -260,11 +262,11 @@ struct Q4K {
     // k = 0..3; then per (super-block, g) the low and high 32-element sums in
     // the reference's order (per-lane sums of four, then the 8-lane tree). The
     // caller's barrier after stage() publishes the sums.
-    template <bool kPre = false>
+    template <int N = 8, bool kPre = false>
     __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds, uint32_t tid,
-                                 uint32_t nthreads, const XBatch &pre = XBatch()) {
+                                 uint32_t nthreads, const XBatch<N> &pre = XBatch<N>()) {
         // element e of the tile: super-block e/256, group (e%256)/64, half (e%64)/32
-        scatter_lanes<2, kPre>(
+        scatter_lanes<2, N, kPre>(
             x, b0 * 256, nb * 256, lds, tid, nthreads,
             [](uint32_t e) { return (((e >> 6) * 8 + (e & 7)) * 2) + ((e >> 5) & 1); }, pre);
         __syncthreads();
@@ -399,7 +401,10 @@ __device__ __forceinline__ void run_chunks_pf(const typename T::Row (&rows)[NR],
 // counts conservative, and it then waits for every load in flight before
 // each chunk, which removes the prefetch. Every tile must start at a multiple
 // of kSlots chunks.
-template <class T, int NR, int PF>
+// The compiler's wait counts are conservative at a loop's head: the first
+// chunk of every pass through the steady-state loop waits for every load in
+// flight. U rings per pass (U * kSlots chunks) make that wait rare.
+template <class T, int NR, int PF, int U = 1>
 struct ChunkStream {
     static constexpr int kSlots = PF + 1;
     typename T::Chunk buf[kSlots][NR];
@@ -421,7 +426,23 @@ struct ChunkStream {
         const uint32_t last = c_end - 1;
         const uint32_t cf = c1 < full_end ? c1 : full_end;
         uint32_t c = c0;
-        // steady state: whole rings of full chunks, one basic block per ring
+        // steady state: U whole rings of full chunks per pass, one basic block
+        if (U > 1)
+            for (; c + kSlots * U <= cf; c += kSlots * U) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+#pragma unroll
+                    for (int p = 0; p < kSlots; ++p) {
+                        const uint32_t cc = c + u * kSlots + p;
+                        const uint32_t nxt = cc + PF < last ? cc + PF : last;
+#pragma unroll
+                        for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(rows[i], nxt);
+                        __builtin_amdgcn_sched_barrier(0);
+                        T::template step<NR, true>(buf[p], lds, nb_tile, cc * T::kPerChunk - tile_b0,
+                                                   T::kPerChunk, l, t);
+                    }
+                }
+            }
         for (; c + kSlots <= cf; c += kSlots) {
 #pragma unroll
             for (int p = 0; p < kSlots; ++p) {

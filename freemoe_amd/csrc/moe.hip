@@ -38,6 +38,12 @@ constexpr uint32_t kMaxHidden = 16384; // hidden sizes the routing kernels accep
 // 160 KiB, of which 1 KiB is left for the kernels' static LDS.
 constexpr size_t kMaxLds = 159 * 1024;
 constexpr uint32_t kThreads = 256;
+// Rings per pass of the down kernel's steady-state loop: for Q4_0, 7 chunks
+// in flight make 8-chunk rings, so a Mixtral down row (56 chunks) is one pass.
+template <class T>
+constexpr int down_rings() {
+    return T::kType == FMX_TYPE_Q4_0 ? 7 : 1;
+}
 
 __device__ inline double wave_sum_double(double v) {
 #pragma unroll
@@ -387,7 +393,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const uint32_t rank = blockIdx.y;
     const uint32_t blocks = a.gu.blocks;
     // h's first tile is requested before the routing, whose loads it overlaps
-    XBatch hb;
+    XBatch<4> hb;
     load_batch(hb, h, 0, (blocks < a.gu_tile ? blocks : a.gu_tile) * T::kBlock, tid, kThreads);
     const uint32_t e = expert_of_rank(a.route, logits, ids, rank, blockIdx.x == 0 && rank == 0, ids, w, status);
     if (e >= a.experts) {
@@ -414,7 +420,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     for (uint32_t tb = 0; tb < blocks; tb += a.gu_tile) {
         const uint32_t nb = blocks - tb < a.gu_tile ? blocks - tb : a.gu_tile;
         __syncthreads();
-        if (tb == 0) T::template stage<true>(h, tb, nb, lds, tid, kThreads, hb);
+        if (tb == 0) T::template stage<4, true>(h, tb, nb, lds, tid, kThreads, hb);
         else T::stage(h, tb, nb, lds, tid, kThreads);
         __syncthreads();
         cs.run(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, c_end, blocks, tb, nb, lds, l,
@@ -464,13 +470,24 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const uint32_t blocks = a.dn.blocks;
     const uint32_t c_end = (blocks + T::kPerChunk - 1) / T::kPerChunk;
     const uint32_t tile_floats = a.dn_tile * T::kLdsFloatsPerBlock;
-    ChunkStream<T, 1, PF> cs;
+    ChunkStream<T, 1, PF, down_rings<T>()> cs;
     cs.prime(rw, c_end);
     for (uint32_t tb = 0; tb < blocks; tb += a.dn_tile) {
         const uint32_t nb = blocks - tb < a.dn_tile ? blocks - tb : a.dn_tile;
         __syncthreads();
-        for (uint32_t r = 0; r < K; ++r)
-            T::stage(act + static_cast<uint64_t>(r) * a.ffn, tb, nb, lds + r * tile_floats, tid, kThreads);
+        const uint32_t tile_elems = nb * T::kBlock;
+        if (K == 2 && tile_elems <= 16 * 4 * kThreads) {
+            // both ranks' activations requested together: one memory latency
+            XBatch<16> b0, b1;
+            load_batch(b0, act, tb * T::kBlock, tile_elems, tid, kThreads);
+            load_batch(b1, act + a.ffn, tb * T::kBlock, tile_elems, tid, kThreads);
+            T::template stage<16, true>(act, tb, nb, lds, tid, kThreads, b0);
+            T::template stage<16, true>(act + a.ffn, tb, nb, lds + tile_floats, tid, kThreads, b1);
+        } else {
+            for (uint32_t r = 0; r < K; ++r)
+                T::template stage<16>(act + static_cast<uint64_t>(r) * a.ffn, tb, nb, lds + r * tile_floats, tid,
+                                      kThreads);
+        }
         __syncthreads();
         cs.run(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, c_end, blocks, tb, nb,
                lds + rank * tile_floats, l, t);
@@ -549,7 +566,7 @@ __global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const 
 
 // Prefetch depth (chunks in flight per row) of each pass.
 constexpr int kGateUpPF = 1;
-constexpr int kDownPF = 16;
+constexpr int kDownPF = 7;
 
 template <class T>
 int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
