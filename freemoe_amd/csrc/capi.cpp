@@ -47,7 +47,7 @@ DecodeWorkspace decode_workspace(const fmx_moe_layer *L, uint32_t tokens) {
 // Prefill workspace (all offsets 256-byte aligned), pairs = tokens * top_k:
 //   [0, 256) error word | h [tokens x hidden] f32 | offsets [experts + 1] |
 //   token_list, rank_list, slot_of [pairs] | row tiles [1 + 3 * max_tiles] |
-//   x [pairs x hidden] bf16 | act [pairs x ffn] bf16 | dn [pairs x hidden] f32 |
+//   x [pairs x hidden] bf16 | act [pairs x ffn] bf16 | dn [splits x pairs x hidden] f32 |
 //   the decode scratch (act of one token) for shapes the GEMMs do not tile |
 //   logits [tokens x experts] f32
 struct PrefillWorkspace {
@@ -70,9 +70,11 @@ PrefillWorkspace prefill_workspace(const fmx_moe_layer *L, uint32_t tokens) {
     w.rank_list = take(P * 4);
     w.slot_of = take(P * 4);
     w.tiles = take((1 + 3ull * w.max_tiles) * 4);
-    w.x = take(P * H * 2);
-    w.act = take(P * F * 2);
-    w.dn = take(P * H * 4);
+    // the GEMMs read 256 rows from every tile's first row: both activation
+    // matrices carry that many rows of padding
+    w.x = take((P + kPrefillTileRows) * H * 2);
+    w.act = take((P + kPrefillTileRows) * F * 2);
+    w.dn = take(prefill_down_splits(L->experts, L->ffn) * P * H * 4);
     w.dec_act = take(static_cast<uint64_t>(L->top_k) * F * 4);
     w.logits = take(static_cast<uint64_t>(tokens) * E * 4);
     w.total = o;
@@ -486,13 +488,14 @@ int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t
     b.x = reinterpret_cast<__bf16 *>(base + ws.x);
     b.act = reinterpret_cast<__bf16 *>(base + ws.act);
     b.dn = reinterpret_cast<float *>(base + ws.dn);
+    b.splits = prefill_down_splits(L->experts, L->ffn);
     if (int rc = launch_bucket(ids, tokens, L->top_k, L->experts, reinterpret_cast<uint32_t *>(base + ws.offsets),
                                reinterpret_cast<uint32_t *>(base + ws.token_list),
                                reinterpret_cast<uint32_t *>(base + ws.rank_list), slot_of, status, s,
                                reinterpret_cast<uint32_t *>(base + ws.tiles), kPrefillTileRows))
         return rc;
     if (int rc = launch_prefill_experts(ea, b, ws.max_tiles, s)) return rc;
-    return launch_combine(x, b.dn, slot_of, weights, L->hidden, L->top_k, tokens, out, s);
+    return launch_combine(x, b.dn, b.splits, b.pairs, slot_of, weights, L->hidden, L->top_k, tokens, out, s);
 }
 
 int fmx_moe_status(void *workspace, void *stream) {

@@ -118,59 +118,82 @@ struct Q40 {
         return k;
     }
 
-    // Blocks j < nblk of chunk `k` (block index within the LDS tile: tb0 + j).
-    // FULL: all kPerChunk blocks are present, so the LDS reads of the whole
-    // chunk are issued before the arithmetic.
-    template <int NR, bool FULL = false>
-    __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t nb_tile,
-                                uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
+    // The x values of half a chunk (4 blocks) from LDS: per block the lane's
+    // float4 and its 8 * sum.
+    struct XHalf {
+        float4 xv[4];
+        float sx8[4];
+    };
+    // Blocks 4 * half .. 4 * half + 3 of the chunk whose first block sits at
+    // tile block tb0 (blocks past nblk read block 0 instead).
+    __device__ static void read_half(XHalf &xh, const float *lds, uint32_t nb_tile, uint32_t tb0, uint32_t half,
+                                     uint32_t l, uint32_t nblk = kPerChunk) {
         const float4 *xs = reinterpret_cast<const float4 *>(lds) + tb0 * 8 + l;
         const float *s8 = lds + nb_tile * 32 + tb0 * 8 + l;
-        // two halves of four blocks: each half's LDS reads are issued before its
-        // arithmetic (bounded register use)
 #pragma unroll
-        for (uint32_t half = 0; half < 2; ++half) {
-            float4 xv[4];
-            float sx8[4];
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t j = 4 * half + q;
+            const uint32_t jr = j < nblk ? j : 0;
+            xh.xv[q] = xs[jr * 8];
+            xh.sx8[q] = s8[jr * 8];
+        }
+    }
+
+    // The arithmetic of blocks 4 * half + q, q < nq, of chunk `k`.
+    template <int NR, bool FULL>
+    __device__ static void compute_half(const Chunk (&k)[NR], const XHalf &xh, uint32_t half, uint32_t nq,
+                                        float (&t)[NR]) {
 #pragma unroll
-            for (uint32_t q = 0; q < 4; ++q) {
-                const uint32_t j = 4 * half + q;
-                const uint32_t jr = FULL || j < nblk ? j : 0;
-                xv[q] = xs[jr * 8];
-                sx8[q] = s8[jr * 8];
+        for (uint32_t jj = 2 * half; jj < 2 * half + 2; ++jj) {
+            // dword jj holds blocks 2jj and 2jj+1: bytes (A, B, A', B')
+            uint32_t lo4[NR], hi4[NR], sw[NR];
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                const uint32_t qw = jj == 0 ? k[i].q.x : jj == 1 ? k[i].q.y : jj == 2 ? k[i].q.z : k[i].q.w;
+                sw[i] = jj == 0 ? k[i].s.x : jj == 1 ? k[i].s.y : jj == 2 ? k[i].s.z : k[i].s.w;
+                lo4[i] = qw & 0x0F0F0F0Fu;
+                hi4[i] = (qw >> 4) & 0x0F0F0F0Fu;
             }
 #pragma unroll
-            for (uint32_t jj = 2 * half; jj < 2 * half + 2; ++jj) {
-                // dword jj holds blocks 2jj and 2jj+1: bytes (A, B, A', B')
-                uint32_t lo4[NR], hi4[NR], sw[NR];
+            for (uint32_t h = 0; h < 2; ++h) {
+                const uint32_t q = 2 * jj + h - 4 * half;
+                if (!FULL && q >= nq) break;
 #pragma unroll
                 for (int i = 0; i < NR; ++i) {
-                    const uint32_t qw = jj == 0 ? k[i].q.x : jj == 1 ? k[i].q.y : jj == 2 ? k[i].q.z : k[i].q.w;
-                    sw[i] = jj == 0 ? k[i].s.x : jj == 1 ? k[i].s.y : jj == 2 ? k[i].s.z : k[i].s.w;
-                    lo4[i] = qw & 0x0F0F0F0Fu;
-                    hi4[i] = (qw >> 4) & 0x0F0F0F0Fu;
-                }
-#pragma unroll
-                for (uint32_t h = 0; h < 2; ++h) {
-                    const uint32_t j = 2 * jj + h, q = j - 4 * half;
-                    if (!FULL && j >= nblk) break;
-#pragma unroll
-                    for (int i = 0; i < NR; ++i) {
-                        const float qa = h ? ubyte2(lo4[i]) : ubyte0(lo4[i]);
-                        const float qb = h ? ubyte3(lo4[i]) : ubyte1(lo4[i]);
-                        const float qc = h ? ubyte2(hi4[i]) : ubyte0(hi4[i]);
-                        const float qd = h ? ubyte3(hi4[i]) : ubyte1(hi4[i]);
-                        // lo = fma(q[l], x[l], q[8+l]*x[8+l]); hi likewise for 16+l, 24+l
-                        const float lo = fma_rn(qa, xv[q].x, qb * xv[q].y);
-                        const float hi = fma_rn(qc, xv[q].z, qd * xv[q].w);
-                        const float c = (lo + hi) - sx8[q];
-                        const float d = half_bits_to_float(h ? (sw[i] >> 16) : (sw[i] & 0xFFFFu));
-                        t[i] = fma_rn(c, d, t[i]);
-                    }
+                    const float qa = h ? ubyte2(lo4[i]) : ubyte0(lo4[i]);
+                    const float qb = h ? ubyte3(lo4[i]) : ubyte1(lo4[i]);
+                    const float qc = h ? ubyte2(hi4[i]) : ubyte0(hi4[i]);
+                    const float qd = h ? ubyte3(hi4[i]) : ubyte1(hi4[i]);
+                    // lo = fma(q[l], x[l], q[8+l]*x[8+l]); hi likewise for 16+l, 24+l
+                    const float lo = fma_rn(qa, xh.xv[q].x, qb * xh.xv[q].y);
+                    const float hi = fma_rn(qc, xh.xv[q].z, qd * xh.xv[q].w);
+                    const float c = (lo + hi) - xh.sx8[q];
+                    const float d = half_bits_to_float(h ? (sw[i] >> 16) : (sw[i] & 0xFFFFu));
+                    t[i] = fma_rn(c, d, t[i]);
                 }
             }
         }
     }
+
+    // Blocks j < nblk of chunk `k` (block index within the LDS tile: tb0 + j),
+    // in two halves of four blocks whose LDS reads are issued before their
+    // arithmetic. FULL: all kPerChunk blocks are present.
+    template <int NR, bool FULL = false>
+    __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t nb_tile,
+                                uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
+#pragma unroll
+        for (uint32_t half = 0; half < 2; ++half) {
+            if (!FULL && 4 * half >= nblk) break;
+            XHalf xh;
+            read_half(xh, lds, nb_tile, tb0, half, l, FULL ? kPerChunk : nblk);
+            const uint32_t nq = FULL ? 4 : (nblk - 4 * half < 4 ? nblk - 4 * half : 4);
+            compute_half<NR, FULL>(k, xh, half, nq, t);
+        }
+    }
+
+    // Half-chunk LDS pipelining (ChunkStream with kPipelined): the next half's
+    // reads are in flight during this half's arithmetic.
+    static constexpr bool kHalves = true;
 
     // The row's value from the lane chains (all 8 lanes end with it).
     __device__ static float finish(float t) { return hsum8_lanes(t); }
@@ -404,10 +427,33 @@ __device__ __forceinline__ void run_chunks_pf(const typename T::Row (&rows)[NR],
 // The compiler's wait counts are conservative at a loop's head: the first
 // chunk of every pass through the steady-state loop waits for every load in
 // flight. U rings per pass (U * kSlots chunks) make that wait rare.
-template <class T, int NR, int PF, int U = 1>
+// kPipe (types with XHalf / read_half / compute_half): in the steady state
+// the LDS reads of the next half chunk are in flight during the arithmetic of
+// the current one, for kernels with too few wavefronts per SIMD to hide LDS
+// latency by switching.
+template <class T, int NR, int PF, int U = 1, bool kPipe = false>
 struct ChunkStream {
     static constexpr int kSlots = PF + 1;
     typename T::Chunk buf[kSlots][NR];
+
+    // One full chunk `cc` from `cur`, with `xa` holding its first half's x
+    // values on entry and the next chunk's (chunk cn) on return; requests
+    // chunk `nxt` into `dst` first.
+    template <class XH>
+    __device__ __forceinline__ void pipe_step(const typename T::Row (&rows)[NR], const typename T::Chunk (&cur)[NR],
+                                              typename T::Chunk (&dst)[NR], uint32_t nxt, uint32_t cc,
+                                              uint32_t cn, const float *lds, uint32_t nb_tile, uint32_t tile_b0,
+                                              uint32_t l, float (&t)[NR], XH &xa, XH &xb) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) dst[i] = T::load(rows[i], nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        T::read_half(xb, lds, nb_tile, cc * T::kPerChunk - tile_b0, 1, l);
+        __builtin_amdgcn_sched_barrier(0);
+        T::template compute_half<NR, true>(cur, xa, 0, 4, t);
+        T::read_half(xa, lds, nb_tile, cn * T::kPerChunk - tile_b0, 0, l);
+        __builtin_amdgcn_sched_barrier(0);
+        T::template compute_half<NR, true>(cur, xb, 1, 4, t);
+    }
 
     __device__ __forceinline__ void prime(const typename T::Row (&rows)[NR], uint32_t c_end) {
         const uint32_t last = c_end - 1;
@@ -426,8 +472,36 @@ struct ChunkStream {
         const uint32_t last = c_end - 1;
         const uint32_t cf = c1 < full_end ? c1 : full_end;
         uint32_t c = c0;
+        if constexpr (kPipe) {
+            typename T::XHalf xa, xb;
+            if (c + kSlots <= cf) T::read_half(xa, lds, nb_tile, c * T::kPerChunk - tile_b0, 0, l);
+            if (U > 1)
+                for (; c + kSlots * U <= cf; c += kSlots * U) {
+#pragma unroll
+                    for (int u = 0; u < U; ++u) {
+#pragma unroll
+                        for (int p = 0; p < kSlots; ++p) {
+                            const uint32_t cc = c + u * kSlots + p;
+                            const uint32_t nxt = cc + PF < last ? cc + PF : last;
+                            const uint32_t cn = cc + 1 < cf ? cc + 1 : cc;
+                            pipe_step(rows, buf[p], buf[(p + PF) % kSlots], nxt, cc, cn, lds, nb_tile, tile_b0, l,
+                                      t, xa, xb);
+                        }
+                    }
+                }
+            for (; c + kSlots <= cf; c += kSlots) {
+#pragma unroll
+                for (int p = 0; p < kSlots; ++p) {
+                    const uint32_t cc = c + p;
+                    const uint32_t nxt = cc + PF < last ? cc + PF : last;
+                    const uint32_t cn = cc + 1 < cf ? cc + 1 : cc;
+                    pipe_step(rows, buf[p], buf[(p + PF) % kSlots], nxt, cc, cn, lds, nb_tile, tile_b0, l, t, xa,
+                              xb);
+                }
+            }
+        }
         // steady state: U whole rings of full chunks per pass, one basic block
-        if (U > 1)
+        if (!kPipe && U > 1)
             for (; c + kSlots * U <= cf; c += kSlots * U) {
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
@@ -443,7 +517,7 @@ struct ChunkStream {
                     }
                 }
             }
-        for (; c + kSlots <= cf; c += kSlots) {
+        for (; !kPipe && c + kSlots <= cf; c += kSlots) {
 #pragma unroll
             for (int p = 0; p < kSlots; ++p) {
                 const uint32_t cc = c + p;

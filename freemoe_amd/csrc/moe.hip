@@ -470,7 +470,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const uint32_t blocks = a.dn.blocks;
     const uint32_t c_end = (blocks + T::kPerChunk - 1) / T::kPerChunk;
     const uint32_t tile_floats = a.dn_tile * T::kLdsFloatsPerBlock;
-    ChunkStream<T, 1, PF, down_rings<T>()> cs;
+    ChunkStream<T, 1, PF, down_rings<T>(), T::kType == FMX_TYPE_Q4_0> cs;
     cs.prime(rw, c_end);
     for (uint32_t tb = 0; tb < blocks; tb += a.dn_tile) {
         const uint32_t nb = blocks - tb < a.dn_tile ? blocks - tb : a.dn_tile;

@@ -7,8 +7,9 @@
 //   -> gather: h rows of each (token, expert) pair into an expert-contiguous
 //      bf16 matrix X [pairs x hidden]
 //   -> gate/up grouped GEMM on bf16 MFMA, weights dequantised from their
-//      packed blocks into LDS, SwiGLU in the epilogue -> act [pairs x ffn] bf16
-//   -> down grouped GEMM -> D [pairs x hidden] f32
+//      packed blocks in registers, SwiGLU in the epilogue -> act [pairs x ffn]
+//      bf16
+//   -> down grouped GEMM (K split in two for few experts) -> D f32 partials
 //   -> combine per token in rank order plus the residual.
 //
 // K order. The packed expert slots (quant.hip) keep each lane's 16-byte slice
@@ -18,14 +19,7 @@
 // one packed slot serves both decode and prefill, and every weight byte is
 // read from HBM in 16-byte runs straight into the dequantiser.
 //
-// Tiles. A workgroup (8 wavefronts) owns one row tile of one expert (up to 128
-// token-expert pairs) and 128 weight rows (gate/up: 64 gate rows and the same
-// 64 up rows, arranged so SwiGLU pairs meet in one lane); wavefront w computes
-// rows 32 (w / 2) .. +32 against weight rows 64 (w % 2) .. +64. It walks K in
-// steps of 128 packed positions with three steps of weight slices and
-// activation rows in flight: each step is dequantised (weights) and copied
-// (activations) into one of two LDS buffer pairs and fed from LDS to
-// v_mfma_f32_32x32x16_bf16.
+// Tiles: see "the GEMMs" below.
 #include "bucket.hpp"
 #include "fmx_internal.hpp"
 #include "moe.hpp"
@@ -38,10 +32,6 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr uint32_t kGemmThreads = 512;            // 8 wavefronts
-constexpr uint32_t kTileN = 128;                  // weight rows per workgroup
-constexpr uint32_t kStepK = 128;                  // packed K positions per step
-constexpr uint32_t kWBufElems = kTileN * kStepK;  // one LDS weight tile (bf16)
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     const __bf16 x = static_cast<__bf16>(a), y = static_cast<__bf16>(b);
@@ -50,33 +40,52 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 }
 
 // ------------------------------------------------------------ block types --
-// kChunkK: elements per packed chunk. kSlices: 16-byte lane slices a step of
-// kStepK positions covers. elem(p) / pos(e): element held at packed position p
-// of a chunk, and its inverse. Slice: a slice's raw bytes plus its scales;
-// dequant() writes the slice's values, in position order, as bf16 pairs.
+// kChunkK: elements per packed chunk (eight 16-byte lane slices). elem(p) /
+// pos(e): element held at packed position p of a chunk, and its inverse.
+// WStep: a lane's packed bytes (and scales) for one GEMM K step; dequant_kk()
+// turns 8 consecutive positions of it into the bf16 B operand of one MFMA.
 
 struct GQ80 {
     static constexpr uint32_t kType = FMX_TYPE_Q8_0;
     static constexpr uint32_t kChunkK = 128;
-    static constexpr uint32_t kSlices = 8;                 // a step is a whole chunk
-    static constexpr uint32_t kValsPerSlice = 16;
     // position p = 16 l + 4 j + k holds element 32 j + 8 k + l
     __host__ __device__ static uint32_t elem(uint32_t p) { return 32 * ((p & 15) >> 2) + 8 * (p & 3) + (p >> 4); }
     __host__ __device__ static uint32_t pos(uint32_t e) { return 16 * (e & 7) + 4 * (e >> 5) + ((e & 31) >> 3); }
-    struct Slice {
-        uint4 q;
-        uint2 d; // the chunk's four block scales
+    // A lane's half of a K step (64 positions = half a chunk): slices
+    // 4 (step % 2) + 2 h and the next (positions 32 h .. +32 of the step), and
+    // the chunk's four block scales.
+    struct WStep {
+        uint4 q[2];
+        uint2 d;
     };
-    // Slice s (0..7) of chunk c of row r.
-    __device__ static Slice load(const uint8_t *packed, const PackedGeometry &g, uint32_t r, uint32_t c,
-                                 uint32_t s) {
-        Slice v;
-        v.q = ld16(packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + s) * 16);
-        v.d = ld8(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(c) * 8);
-        return v;
+    __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
+                                     uint32_t step, uint32_t h) {
+        const uint32_t c = step >> 1, s0 = 4 * (step & 1) + 2 * h;
+        const uint8_t *q = packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + s0) * 16;
+        w.q[0] = ld16(q);
+        w.q[1] = ld16(q + 16);
+        w.d = ld8(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(c) * 8);
     }
-    __device__ static void dequant(const Slice &v, uint32_t *out) {
-        const uint32_t w[4] = {v.q.x, v.q.y, v.q.z, v.q.w};
+    __device__ static void decode_header(WStep &) {}
+    // Positions 32 h + 8 kk .. +8 of the step: bytes 8 (kk % 2) .. +8 of the
+    // lane's slice kk / 2, i.e. blocks 2 (kk % 2) and 2 (kk % 2) + 1.
+    __device__ static bf16x8 dequant_kk(const WStep &w, int kk) {
+        const uint4 q = w.q[kk >> 1];
+        const uint32_t lo = (kk & 1) ? q.z : q.x, hi = (kk & 1) ? q.w : q.y;
+        const uint32_t dd = (kk & 1) ? w.d.y : w.d.x;
+        const float d0 = half_bits_to_float(dd & 0xFFFFu), d1 = half_bits_to_float(dd >> 16);
+        uint32_t v[4];
+        v[0] = pack_bf16x2(d0 * static_cast<float>(static_cast<int8_t>(lo)),
+                           d0 * static_cast<float>(static_cast<int8_t>(lo >> 8)));
+        v[1] = pack_bf16x2(d0 * static_cast<float>(static_cast<int8_t>(lo >> 16)),
+                           d0 * static_cast<float>(static_cast<int8_t>(lo >> 24)));
+        v[2] = pack_bf16x2(d1 * static_cast<float>(static_cast<int8_t>(hi)),
+                           d1 * static_cast<float>(static_cast<int8_t>(hi >> 8)));
+        v[3] = pack_bf16x2(d1 * static_cast<float>(static_cast<int8_t>(hi >> 16)),
+                           d1 * static_cast<float>(static_cast<int8_t>(hi >> 24)));
+        return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
+    }
+};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float d = half_bits_to_float(j & 2 ? ((j & 1) ? v.d.y >> 16 : v.d.y & 0xFFFFu)
@@ -94,8 +103,6 @@ struct GQ80 {
 struct GQ40 {
     static constexpr uint32_t kType = FMX_TYPE_Q4_0;
     static constexpr uint32_t kChunkK = 256;
-    static constexpr uint32_t kSlices = 4;                 // a step is half a chunk
-    static constexpr uint32_t kValsPerSlice = 32;
     // position p = 32 l + 4 j + 2 which + nib holds element 32 j + 16 nib + 8 which + l
     __host__ __device__ static uint32_t elem(uint32_t p) {
         const uint32_t l = p >> 5, q = p & 31, nib = q & 1, which = (q >> 1) & 1, j = q >> 2;
@@ -105,19 +112,38 @@ struct GQ40 {
         const uint32_t j = e >> 5, r = e & 31, nib = r >> 4, which = (r >> 3) & 1, l = r & 7;
         return 32 * l + 4 * j + 2 * which + nib;
     }
-    struct Slice {
+    // A lane's half of a K step (64 positions = a quarter chunk): slice
+    // 2 (step % 4) + h (positions 32 h .. +32 of the step) and the chunk's
+    // eight block scales.
+    struct WStep {
         uint4 q;
-        uint4 d; // the chunk's eight block scales
+        uint4 d;
     };
-    __device__ static Slice load(const uint8_t *packed, const PackedGeometry &g, uint32_t r, uint32_t c,
-                                 uint32_t s) {
-        Slice v;
-        v.q = ld16(packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + s) * 16);
-        v.d = ld16(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(c) * 16);
-        return v;
+    __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
+                                     uint32_t step, uint32_t h) {
+        const uint32_t c = step >> 2, sl = 2 * (step & 3) + h;
+        w.q = ld16(packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + sl) * 16);
+        w.d = ld16(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(c) * 16);
     }
-    __device__ static void dequant(const Slice &v, uint32_t *out) {
-        const uint32_t w[4] = {v.q.x, v.q.y, v.q.z, v.q.w};
+    __device__ static void decode_header(WStep &) {}
+    // Positions 32 h + 8 kk .. +8 of the step: dword kk of the lane's slice;
+    // its bytes are blocks 2 kk (bytes 0, 1) and 2 kk + 1 (bytes 2, 3), low
+    // nibble first.
+    __device__ static bf16x8 dequant_kk(const WStep &w, int kk) {
+        const uint32_t qw = kk == 0 ? w.q.x : kk == 1 ? w.q.y : kk == 2 ? w.q.z : w.q.w;
+        const uint32_t dd = kk == 0 ? w.d.x : kk == 1 ? w.d.y : kk == 2 ? w.d.z : w.d.w;
+        const float d0 = half_bits_to_float(dd & 0xFFFFu), d1 = half_bits_to_float(dd >> 16);
+        uint32_t v[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint32_t byte = (qw >> (8 * b)) & 0xFFu;
+            const float d = b < 2 ? d0 : d1;
+            v[b] = pack_bf16x2(d * static_cast<float>(static_cast<int32_t>(byte & 15u) - 8),
+                               d * static_cast<float>(static_cast<int32_t>(byte >> 4) - 8));
+        }
+        return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
+    }
+};
         const uint32_t dw[4] = {v.d.x, v.d.y, v.d.z, v.d.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -140,8 +166,6 @@ struct GQ40 {
 struct GQ4K {
     static constexpr uint32_t kType = FMX_TYPE_Q4_K;
     static constexpr uint32_t kChunkK = 256;
-    static constexpr uint32_t kSlices = 4;
-    static constexpr uint32_t kValsPerSlice = 32;
     // position p = 32 l + 8 g + 2 k + nib holds element 64 g + 32 nib + 8 k + l
     __host__ __device__ static uint32_t elem(uint32_t p) {
         const uint32_t l = p >> 5, q = p & 31, nib = q & 1, k = (q >> 1) & 3, g = q >> 3;
@@ -151,23 +175,39 @@ struct GQ4K {
         const uint32_t g = e >> 6, r = e & 63, nib = r >> 5, k = (r >> 3) & 3, l = r & 7;
         return 32 * l + 8 * g + 2 * k + nib;
     }
-    struct Slice {
+    // A lane's half of a K step: as Q4_0, with the super-block header.
+    struct WStep {
         uint4 q;
-        uint4 h; // the super-block header: d, dmin, 12 bytes of 6-bit scales and mins
+        uint4 hd;
     };
-    __device__ static Slice load(const uint8_t *packed, const PackedGeometry &g, uint32_t r, uint32_t c,
-                                 uint32_t s) {
-        Slice v;
-        v.q = ld16(packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + s) * 16);
-        v.h = ld16(packed + (static_cast<uint64_t>(r) * g.chunks + c) * 16);
-        return v;
+    __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
+                                     uint32_t step, uint32_t h) {
+        const uint32_t c = step >> 2, sl = 2 * (step & 3) + h;
+        w.q = ld16(packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + sl) * 16);
+        w.hd = ld16(packed + (static_cast<uint64_t>(r) * g.chunks + c) * 16);
     }
-    __device__ static void dequant(const Slice &v, uint32_t *out) {
+    // Positions 32 h + 8 kk .. +8 of the step: dword kk of the lane's slice,
+    // group kk: low nibbles sub-block 2 kk, high 2 kk + 1.
+    __device__ static bf16x8 dequant_kk(const WStep &w, int kk) {
+        const uint32_t qw = kk == 0 ? w.q.x : kk == 1 ? w.q.y : kk == 2 ? w.q.z : w.q.w;
         uint8_t hdr[16];
-        memcpy(hdr, &v.h, 16);
+        memcpy(hdr, &w.hd, 16);
         const float d = half_bits_to_float(hdr[0] | (hdr[1] << 8));
         const float dmin = half_bits_to_float(hdr[2] | (hdr[3] << 8));
-        const uint32_t w[4] = {v.q.x, v.q.y, v.q.z, v.q.w};
+        uint32_t sc1, m1, sc2, m2;
+        k4_scale_min(2 * kk, hdr + 4, sc1, m1);
+        k4_scale_min(2 * kk + 1, hdr + 4, sc2, m2);
+        const float d1 = d * static_cast<float>(sc1), mm1 = dmin * static_cast<float>(m1);
+        const float d2 = d * static_cast<float>(sc2), mm2 = dmin * static_cast<float>(m2);
+        uint32_t v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t byte = (qw >> (8 * k)) & 0xFFu;
+            v[k] = pack_bf16x2(d1 * static_cast<float>(byte & 15u) - mm1, d2 * static_cast<float>(byte >> 4) - mm2);
+        }
+        return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
+    }
+};
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             uint32_t sc1, m1, sc2, m2;
@@ -186,136 +226,38 @@ struct GQ4K {
     }
 };
 
-// Weight rows of a tile. Gated (gate/up): LDS row block b = lr / 32 holds
-// gate rows (b even) or up rows (b odd) n0 + 32 (b / 2) + lr % 32, so each
-// wavefront's two 32-row blocks are the gate and up rows of the same ffn
-// rows. Plain (down): LDS row lr is matrix row n0 + lr.
-struct TileRows {
-    const uint8_t *gate_or_w, *up;
-    uint32_t n0;
-    bool gated;
-    __device__ void at(uint32_t lr, const uint8_t *&w, uint32_t &r) const {
-        if (gated) {
-            const uint32_t b = lr >> 5;
-            w = (b & 1) ? up : gate_or_w;
-            r = n0 + 32 * (b >> 1) + (lr & 31);
-        } else {
-            w = gate_or_w;
-            r = n0 + lr;
-        }
-    }
-};
+// ------------------------------------------------------------ the GEMMs --
+//
+// One workgroup (4 wavefronts, one per SIMD) multiplies a row tile of one
+// expert (up to 256 token-expert pairs = 8 blocks of 32) by 128 weight
+// columns; wavefront w owns two 32-column blocks (gate/up: gate and up of the
+// same 32 ffn rows, so SwiGLU pairs meet in one lane; down: 64 rows).
+//
+// Weights never touch LDS: each lane loads its own two rows' packed bytes for
+// a K step (64 packed positions; lanes 0-31 take positions 0-31, lanes 32-63
+// positions 32-63) from HBM into registers, two steps ahead, and dequantises
+// 8 positions (one MFMA K slice) at a time as the B operand. Each weight byte
+// is read once per row tile, and a row tile holds all of an expert's pairs up
+// to 256. Activations: the tile's rows for the next step are loaded during
+// this one and stored to the other of two LDS buffers, where all four
+// wavefronts read their A operands.
+//
+// v_mfma_f32_32x32x16_bf16: A lane l = tile row 32 mb + l % 32, B lane l =
+// column l % 32, both at positions 32 (l / 32) + 8 kk .. +8 of the step (a GEMM
+// may contract over K in any order, as long as A and B agree); C element r of
+// lane l = row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
 
-// LDS tiles (weights and activations): 128 rows x 128 bf16 (256 bytes), the
-// 16-byte granule g of row r stored at granule g ^ (r & 15), so the 16 rows an
-// MFMA operand read or a store touches at once fall in 16 distinct bank groups.
-__device__ __forceinline__ uint32_t tile_offset(uint32_t row, uint32_t granule) {
-    return row * kStepK + ((granule ^ (row & 15)) << 3);
-}
+constexpr uint32_t kGThreads = 256;
+constexpr uint32_t kGBlocks = kPrefillTileRows / 32;         // 8 row blocks of 32
+constexpr uint32_t kGStepK = 64;                              // packed positions per K step
+constexpr uint32_t kGRowBytes = kGStepK * 2;                  // 128 bytes of a tile row
+constexpr uint32_t kGBufBytes = kPrefillTileRows * kGRowBytes; // one LDS activation buffer
 
-// One K step of the weight tile: thread t loads slices of LDS row t / 4.
-template <class T>
-struct WeightStep {
-    static constexpr uint32_t kPerThread = T::kSlices * kTileN / kGemmThreads; // 2 (Q8_0) or 1 (Q4)
-    typename T::Slice s[kPerThread];
-
-    // w / r: the matrix and row of this thread's LDS row (tid / 4).
-    __device__ void load(const uint8_t *w, uint32_t r, const PackedGeometry &g, uint32_t step, uint32_t tid) {
-        const uint32_t c = step * kStepK / T::kChunkK;
-        const uint32_t s0 = (step * kStepK % T::kChunkK) / (T::kChunkK / 8); // first slice of the step
-#pragma unroll
-        for (uint32_t i = 0; i < kPerThread; ++i) s[i] = T::load(w, g, r, c, s0 + (tid & 3) * kPerThread + i);
-    }
-
-    // Dequantised values into LDS row tid / 4 at the step's positions of the slices.
-    __device__ void store(__bf16 *wbuf, uint32_t tid) const {
-        const uint32_t lr = tid >> 2;
-#pragma unroll
-        for (uint32_t i = 0; i < kPerThread; ++i) {
-            uint32_t v[T::kValsPerSlice / 2];
-            T::dequant(s[i], v);
-            const uint32_t g0 = ((tid & 3) * kPerThread + i) * (T::kValsPerSlice / 8);
-#pragma unroll
-            for (uint32_t q = 0; q < T::kValsPerSlice / 8; ++q)
-                *reinterpret_cast<uint4 *>(wbuf + tile_offset(lr, g0 + q)) =
-                    make_uint4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-        }
-    }
-};
-
-// One K step of the activation tile: thread t copies 64 bytes (positions
-// 32 (t % 4) .. +32) of tile row t / 4, i.e. matrix row `xrow`.
-struct XStep {
-    uint4 v[4];
-    __device__ void load(const __bf16 *x, uint64_t ld, uint32_t xrow, uint32_t step, uint32_t tid) {
-        const __bf16 *src = x + static_cast<uint64_t>(xrow) * ld + step * kStepK + 32 * (tid & 3);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) v[q] = ld16(src + 8 * q);
-    }
-    __device__ void store(__bf16 *xbuf, uint32_t tid) const {
-#pragma unroll
-        for (uint32_t q = 0; q < 4; ++q) *reinterpret_cast<uint4 *>(xbuf + tile_offset(tid >> 2, 4 * (tid & 3) + q)) = v[q];
-    }
-};
-
-// K steps whose loads are in flight ahead of the step being consumed. The
-// loads of a step are issued together and consumed together, in issue order,
-// so a wait for one step never waits on a later one. Every step issues its
-// loads unconditionally (past the last step they re-read the last step, which
-// the caches still hold), so the compiler's wait counts stay exact.
-constexpr uint32_t kLead = 4;
-
-// The shared main loop over `steps` K steps. Per step: wait for that step's
-// weight slices and activation rows, dequantise / copy them into one of two
-// LDS buffer pairs, request step + kLead, barrier, then wavefront w multiplies
-// tile rows 32 (w / 2) .. +32 against weight row blocks 2 (w % 2), +1:
-// acc[j] += X . W^T, operands read from LDS.
-template <class T>
-__device__ void gemm_tile(const TileRows &tr, const PackedGeometry &g, const __bf16 *x, uint64_t ldx,
-                          uint32_t xrow, bool active, uint32_t steps, __bf16 *lds, f32x16 (&acc)[2]) {
-    const uint32_t tid = threadIdx.x, lane = tid & 63, mb = tid >> 7, nb0 = 2 * ((tid >> 6) & 1);
-    const uint8_t *wrow;
-    uint32_t rrow;
-    tr.at(tid >> 2, wrow, rrow);
-    WeightStep<T> ws[kLead];
-    XStep xs[kLead];
-    const uint32_t last = steps - 1;
-#pragma unroll
-    for (uint32_t p = 0; p < kLead; ++p) {
-        ws[p].load(wrow, rrow, g, p < last ? p : last, tid);
-        xs[p].load(x, ldx, xrow, p < last ? p : last, tid);
-    }
-    for (uint32_t st0 = 0; st0 < steps; st0 += kLead) {
-#pragma unroll
-        for (uint32_t u = 0; u < kLead; ++u) {
-            const uint32_t st = st0 + u;
-            if (st >= steps) break;
-            __bf16 *wbuf = lds + (st & 1) * 2 * kWBufElems;
-            __bf16 *xbuf = wbuf + kWBufElems;
-            ws[u].store(wbuf, tid);
-            xs[u].store(xbuf, tid);
-            const uint32_t nxt = st + kLead < last ? st + kLead : last;
-            ws[u].load(wrow, rrow, g, nxt, tid);
-            xs[u].load(x, ldx, xrow, nxt, tid);
-            __syncthreads();
-            if (active) {
-                const uint32_t arow = 32 * mb + (lane & 31);
-#pragma unroll
-                for (uint32_t kk = 0; kk < kStepK / 16; ++kk) {
-                    const uint32_t gr = 2 * kk + (lane >> 5);
-                    const bf16x8 av = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(xbuf + tile_offset(arow, gr)));
-#pragma unroll
-                    for (uint32_t j = 0; j < 2; ++j) {
-                        const uint32_t brow = 32 * (nb0 + j) + (lane & 31);
-                        const uint4 bv = *reinterpret_cast<const uint4 *>(wbuf + tile_offset(brow, gr));
-                        acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, __builtin_bit_cast(bf16x8, bv), acc[j], 0,
-                                                                        0, 0);
-                    }
-                }
-            }
-        }
-    }
-}
+// LDS activation tile: 256 rows x 64 bf16 (128 bytes, eight 16-byte granules);
+// granule g of row r sits at granule g ^ ((r / 2) % 8). A pass of 16 lanes of
+// an A-operand read (16 consecutive rows, one granule) or of a store (8
+// granules of 2 rows, 8 rows apart) then touches 16 distinct bank groups.
+__device__ __forceinline__ uint32_t xswz(uint32_t row) { return (row >> 1) & 7u; }
 
 // Row tile `mt` of the bucketed pairs: (expert, first row, rows); false when
 // mt is past the tiles the bucketing produced (or a tile is malformed).
@@ -327,6 +269,118 @@ __device__ inline bool row_tile(const uint32_t *tiles, uint32_t mt, uint32_t exp
     rows = tiles[3 + 3 * mt];
     return e < experts && rows > 0 && rows <= kPrefillTileRows && row0 <= pairs && rows <= pairs - row0;
 }
+
+// One GEMM of a workgroup: weight steps in a ring of three register slots,
+// this thread's share of the next activation step, the accumulators of NMB
+// row blocks (the kernels instantiate one per possible block count, so no
+// MFMA sits under a branch).
+// Thread t stages granule t % 8 of tile rows t / 8 + 32 i (i < 8); the
+// activation matrix has at least 256 readable rows past every tile's first
+// row (the workspace pads it), and rows past the tile only feed output rows
+// that are never written.
+template <class T, uint32_t NMB>
+struct GemmWave {
+    typename T::WStep w[3][2];
+    uint4 xv[8];
+    f32x16 acc[NMB][2];
+
+    __device__ __forceinline__ void load_x(const __bf16 *src, uint64_t ld, uint32_t k0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = ld16(src + static_cast<uint64_t>(32 * i) * ld + k0);
+    }
+    // st: byte address of this thread's granule in row t / 8 of the buffer
+    __device__ __forceinline__ void store_x(char *st) const {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4 *>(st + i * 32 * kGRowBytes) = xv[i];
+    }
+
+    // The MFMAs of one K step from ring slot `slot`; a_kk[kk]: byte address of
+    // the lane's A operand of slice kk in row block 0 of the step's buffer.
+    __device__ __forceinline__ void multiply(int slot, const char *const (&a_kk)[4]) {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const bf16x8 b0 = T::dequant_kk(w[slot][0], kk), b1 = T::dequant_kk(w[slot][1], kk);
+#pragma unroll
+            for (uint32_t mb = 0; mb < NMB; ++mb) {
+                const bf16x8 av =
+                    __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(a_kk[kk] + mb * 32 * kGRowBytes));
+                acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b0, acc[mb][0], 0, 0, 0);
+                acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b1, acc[mb][1], 0, 0, 0);
+            }
+            // one K slice at a time: bounds the operands in flight
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+
+    // One step: request weights of step `nw` into `slot_next`, multiply step
+    // (ring slot `slot`, LDS buffer `buf`), stage the next step's activations
+    // into the other buffer, request the activations of step `nx`.
+    __device__ __forceinline__ void step(int slot, int slot_next, uint32_t buf, uint32_t nw, uint32_t nx,
+                                         const uint8_t *m0, uint32_t r0, const uint8_t *m1, uint32_t r1,
+                                         const PackedGeometry &g, const __bf16 *xsrc, uint64_t ldx, char *lds,
+                                         uint32_t aoff0, uint32_t stoff, uint32_t h) {
+        T::load_step(w[slot_next][0], m0, g, r0, nw, h);
+        T::load_step(w[slot_next][1], m1, g, r1, nw, h);
+        __builtin_amdgcn_sched_barrier(0);
+        const char *a_kk[4];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) a_kk[kk] = lds + buf * kGBufBytes + (aoff0 ^ (kk << 4));
+        multiply(slot, a_kk);
+        store_x(lds + (buf ^ 1) * kGBufBytes + stoff);
+        load_x(xsrc, ldx, nx * kGStepK);
+        __syncthreads();
+    }
+
+    // K steps [s0, s0 + steps) against weight rows (m0, r0) and (m1, r1).
+    __device__ __forceinline__ void run(const uint8_t *m0, uint32_t r0, const uint8_t *m1, uint32_t r1,
+                                        const PackedGeometry &g, const __bf16 *xsrc, uint64_t ldx, uint32_t s0,
+                                        uint32_t steps, char *lds) {
+        const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
+        const uint32_t last = s0 + steps - 1;
+        // A operand of slice kk: row lane % 32 of the block, granule 4 h + kk
+        const uint32_t ar = lane & 31;
+        const uint32_t aoff0 = ar * kGRowBytes + (((4 * h) ^ xswz(ar)) << 4);
+        // staging: row tid / 8, granule tid % 8
+        const uint32_t sr = tid >> 3, sg = tid & 7;
+        const uint32_t stoff = sr * kGRowBytes + ((sg ^ xswz(sr)) << 4);
+        xsrc += static_cast<uint64_t>(sr) * ldx + 8 * sg;
+#pragma unroll
+        for (uint32_t mb = 0; mb < NMB; ++mb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[mb][j][i] = 0.0f;
+        // prologue: weights of steps s0, s0 + 1; activations of s0 into buffer 0
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t st = s0 + p < last ? s0 + p : last;
+            T::load_step(w[p][0], m0, g, r0, st, h);
+            T::load_step(w[p][1], m1, g, r1, st, h);
+        }
+        load_x(xsrc, ldx, s0 * kGStepK);
+        store_x(lds + stoff);
+        load_x(xsrc, ldx, (s0 + 1 < last ? s0 + 1 : last) * kGStepK);
+        __syncthreads();
+        uint32_t s = 0;
+        // steady state: three steps (one turn of the ring) per pass
+        for (; s + 3 <= steps; s += 3) {
+#pragma unroll
+            for (int u = 0; u < 3; ++u) {
+                const uint32_t st = s0 + s + u;
+                const uint32_t nxt = st + 2 < last ? st + 2 : last;
+                step(u, (u + 2) % 3, (s + u) & 1, nxt, nxt, m0, r0, m1, r1, g, xsrc, ldx, lds, aoff0, stoff, h);
+            }
+        }
+        // the remaining steps (fewer than three)
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+            if (s + u >= steps) break;
+            const uint32_t st = s0 + s + u;
+            const uint32_t nxt = st + 2 < last ? st + 2 : last;
+            step(u, (u + 2) % 3, (s + u) & 1, nxt, nxt, m0, r0, m1, r1, g, xsrc, ldx, lds, aoff0, stoff, h);
+        }
+    }
+};
 
 // ------------------------------------------------------------------ kernels --
 
@@ -349,82 +403,103 @@ __global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ h
     *reinterpret_cast<uint4 *>(x + static_cast<uint64_t>(s) * hidden + p0) = make_uint4(v[0], v[1], v[2], v[3]);
 }
 
-// Gate and up of 64 ffn rows for one row tile, SwiGLU, and the activations
-// written as bf16 in the down projection's packed K order.
-// grid: (max row tiles, ffn / 64): row tiles of one ffn slice run together,
-// so tiles of one expert share the slice's weights through the caches.
-template <class T, class TD>
-__global__ __launch_bounds__(kGemmThreads) void gate_up_gemm_kernel(ExpertArgs a, const uint32_t *__restrict__ tiles,
-                                                                     uint32_t pairs, const __bf16 *__restrict__ x,
-                                                                     __bf16 *__restrict__ act) {
-    extern __shared__ __align__(16) __bf16 tiles_lds[];
-    uint32_t e, row0, rows;
-    if (!row_tile(tiles, blockIdx.x, a.experts, pairs, e, row0, rows)) return;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t n0 = blockIdx.y * 64;
-    const TileRows tr{static_cast<const uint8_t *>(a.gate[e]), static_cast<const uint8_t *>(a.up[e]), n0, true};
-    const uint32_t mb = wave >> 1;
-    const bool active = 32 * mb < rows;
-    const uint32_t xr = tid >> 2; // the tile row this thread copies
-    const uint32_t xrow = row0 + (xr < rows ? xr : rows - 1);
-    f32x16 acc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
-    gemm_tile<T>(tr, a.gu, x, a.hidden, xrow, active, a.hidden / kStepK, tiles_lds, acc);
-    if (!active) return;
+// Gate and up of 128 ffn rows (32 per wavefront) for one row tile of NMB row
+// blocks, SwiGLU, and the activations written as bf16 in the down
+// projection's packed K order.
+template <class T, class TD, uint32_t NMB>
+__device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, uint32_t row0, uint32_t rows,
+                             const __bf16 *__restrict__ x, __bf16 *__restrict__ act, char *lds) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t f = blockIdx.y * 128 + 32 * wave + (lane & 31);
+    GemmWave<T, NMB> gw;
+    gw.run(static_cast<const uint8_t *>(a.gate[e]), f, static_cast<const uint8_t *>(a.up[e]), f, a.gu,
+           x + static_cast<uint64_t>(row0) * a.hidden, a.hidden, 0, a.hidden / kGStepK, lds);
     const uint32_t F = a.ffn;
-    // acc[0] = gate, acc[1] = up of ffn row n0 + 32 (wave % 2) + lane % 32
-    const uint32_t n = n0 + 32 * (wave & 1) + (lane & 31);
-    const uint32_t col = n / TD::kChunkK * TD::kChunkK + TD::pos(n % TD::kChunkK);
+    const uint32_t col = f / TD::kChunkK * TD::kChunkK + TD::pos(f % TD::kChunkK);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const uint32_t m = 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m >= rows) continue;
-        const float gv = acc[0][r], uv = acc[1][r];
-        act[static_cast<uint64_t>(row0 + m) * F + col] = static_cast<__bf16>(gv / (1.0f + expf(-gv)) * uv);
+    for (uint32_t mb = 0; mb < NMB; ++mb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t m = 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m >= rows) continue;
+            const float gv = gw.acc[mb][0][r], uv = gw.acc[mb][1][r];
+            act[static_cast<uint64_t>(row0 + m) * F + col] = static_cast<__bf16>(gv / (1.0f + expf(-gv)) * uv);
+        }
     }
 }
 
-// Down rows [128 nt, +128) for one row tile into D [pairs x hidden] f32.
-// grid: (max row tiles, hidden / 128).
-template <class T>
-__global__ __launch_bounds__(kGemmThreads) void down_gemm_kernel(ExpertArgs a, const uint32_t *__restrict__ tiles,
-                                                                  uint32_t pairs, const __bf16 *__restrict__ act,
-                                                                  float *__restrict__ dn) {
-    extern __shared__ __align__(16) __bf16 tiles_lds[];
+// grid: (max row tiles, ffn / 128).
+template <class T, class TD>
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gate_up_gemm_kernel(
+    ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, const __bf16 *__restrict__ x,
+    __bf16 *__restrict__ act) {
+    extern __shared__ __align__(16) char xlds[];
     uint32_t e, row0, rows;
     if (!row_tile(tiles, blockIdx.x, a.experts, pairs, e, row0, rows)) return;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t n0 = blockIdx.y * kTileN;
-    const TileRows tr{static_cast<const uint8_t *>(a.down[e]), nullptr, n0, false};
-    const uint32_t mb = wave >> 1;
-    const bool active = 32 * mb < rows;
-    const uint32_t xr = tid >> 2; // the tile row this thread copies
-    const uint32_t xrow = row0 + (xr < rows ? xr : rows - 1);
-    f32x16 acc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
-    gemm_tile<T>(tr, a.dn, act, a.ffn, xrow, active, a.ffn / kStepK, tiles_lds, acc);
-    if (!active) return;
+    switch ((rows + 31) / 32) {
+    case 1: gate_up_tile<T, TD, 1>(a, e, row0, rows, x, act, xlds); break;
+    case 2: gate_up_tile<T, TD, 2>(a, e, row0, rows, x, act, xlds); break;
+    case 3: gate_up_tile<T, TD, 3>(a, e, row0, rows, x, act, xlds); break;
+    case 4: gate_up_tile<T, TD, 4>(a, e, row0, rows, x, act, xlds); break;
+    case 5: gate_up_tile<T, TD, 5>(a, e, row0, rows, x, act, xlds); break;
+    case 6: gate_up_tile<T, TD, 6>(a, e, row0, rows, x, act, xlds); break;
+    case 7: gate_up_tile<T, TD, 7>(a, e, row0, rows, x, act, xlds); break;
+    default: gate_up_tile<T, TD, 8>(a, e, row0, rows, x, act, xlds); break;
+    }
+}
+
+// Down rows [256 blockIdx.y, +256) (64 per wavefront) for one row tile of NMB
+// row blocks, over K steps [blockIdx.z * steps, +steps), into D[blockIdx.z]
+// [pairs x hidden] f32.
+template <class T, uint32_t NMB>
+__device__ __forceinline__ void down_tile(const ExpertArgs &a, uint32_t e, uint32_t row0, uint32_t rows, uint32_t pairs,
+                          const __bf16 *__restrict__ act, uint32_t steps, float *__restrict__ dn, char *lds) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t n = blockIdx.y * 256 + 64 * wave + (lane & 31);
+    const uint8_t *wd = static_cast<const uint8_t *>(a.down[e]);
+    GemmWave<T, NMB> gw;
+    gw.run(wd, n, wd, n + 32, a.dn, act + static_cast<uint64_t>(row0) * a.ffn, a.ffn, blockIdx.z * steps, steps,
+           lds);
     const uint32_t H = a.hidden;
-    const uint32_t nb0 = 2 * (wave & 1);
+    float *dst = dn + static_cast<uint64_t>(blockIdx.z) * pairs * H;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const uint32_t m = 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m >= rows) continue;
-        float *dst = dn + static_cast<uint64_t>(row0 + m) * H + n0 + (lane & 31);
+    for (uint32_t mb = 0; mb < NMB; ++mb) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) dst[32 * (nb0 + j)] = acc[j][r];
+        for (int r = 0; r < 16; ++r) {
+            const uint32_t m = 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            if (m >= rows) continue;
+            float *o = dst + static_cast<uint64_t>(row0 + m) * H + n;
+            o[0] = gw.acc[mb][0][r];
+            o[32] = gw.acc[mb][1][r];
+        }
+    }
+}
+
+// grid: (max row tiles, hidden / 256, K splits).
+template <class T>
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void down_gemm_kernel(
+    ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, const __bf16 *__restrict__ act,
+    uint32_t steps, float *__restrict__ dn) {
+    extern __shared__ __align__(16) char xlds[];
+    uint32_t e, row0, rows;
+    if (!row_tile(tiles, blockIdx.x, a.experts, pairs, e, row0, rows)) return;
+    switch ((rows + 31) / 32) {
+    case 1: down_tile<T, 1>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
+    case 2: down_tile<T, 2>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
+    case 3: down_tile<T, 3>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
+    case 4: down_tile<T, 4>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
+    case 5: down_tile<T, 5>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
+    case 6: down_tile<T, 6>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
+    case 7: down_tile<T, 7>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
+    default: down_tile<T, 8>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
     }
 }
 
 // out[t] = x[t] + ((0 + w_0 D_0) + w_1 D_1 ...) in rank order (engine.cpp:1517,
-// 1770, 813-816). grid: (ceil(hidden / 256), tokens).
+// 1770, 813-816), each D the sum of the K splits' partial products in split
+// order. grid: (ceil(hidden / 256), tokens).
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ x, const float *__restrict__ dn,
+                                                      uint32_t splits, uint64_t split_stride,
                                                       const uint32_t *__restrict__ slot_of,
                                                       const float *__restrict__ w, uint32_t hidden, uint32_t K,
                                                       float *__restrict__ out) {
@@ -433,7 +508,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     float ffn = 0.0f;
     for (uint32_t r = 0; r < K; ++r) {
         const uint64_t i = static_cast<uint64_t>(t) * K + r;
-        ffn = ffn + w[i] * dn[static_cast<uint64_t>(slot_of[i]) * hidden + j];
+        const float *d = dn + static_cast<uint64_t>(slot_of[i]) * hidden + j;
+        float v = d[0];
+        for (uint32_t sp = 1; sp < splits; ++sp) v += d[sp * split_stride];
+        ffn = ffn + w[i] * v;
     }
     out[static_cast<uint64_t>(t) * hidden + j] = x[static_cast<uint64_t>(t) * hidden + j] + ffn;
 }
@@ -451,18 +529,18 @@ int launch_gather(const float *h, uint32_t hidden, uint32_t tokens, const uint32
 
 template <class T, class TD>
 int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s) {
-    const size_t lds = 4ull * kWBufElems * sizeof(__bf16); // two (weights, activations) tile pairs
+    const size_t lds = 2ull * kGBufBytes; // two activation buffers
     auto gu = gate_up_gemm_kernel<T, TD>;
     auto dn = down_gemm_kernel<TD>;
     if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds)) return rc;
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds)) return rc;
     if (b.pairs == 0) return FMX_OK;
     if (int rc = launch_gather<T>(b.h, a.hidden, b.tokens, b.token_list, b.pairs, b.x, s)) return rc;
-    hipLaunchKernelGGL(gu, dim3(max_tiles, a.ffn / 64), dim3(kGemmThreads), lds, s, a, b.tiles, b.pairs, b.x,
-                       b.act);
+    hipLaunchKernelGGL(gu, dim3(max_tiles, a.ffn / 128), dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.x, b.act);
     FMX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(dn, dim3(max_tiles, a.hidden / kTileN), dim3(kGemmThreads), lds, s, a, b.tiles, b.pairs,
-                       b.act, b.dn);
+    const uint32_t steps = a.ffn / kGStepK / b.splits;
+    hipLaunchKernelGGL(dn, dim3(max_tiles, a.hidden / 256, b.splits), dim3(kGThreads), lds, s, a, b.tiles, b.pairs,
+                       b.act, steps, b.dn);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
@@ -481,8 +559,8 @@ uint32_t chunk_k_of(uint32_t type) {
 bool prefill_gemm_supported(const ExpertArgs &a) {
     const uint32_t ck_gu = chunk_k_of(a.type_gu), ck_dn = chunk_k_of(a.type_dn);
     if (ck_gu == 0 || ck_dn == 0) return false;
-    return a.hidden % ck_gu == 0 && a.hidden % kTileN == 0 && a.ffn % ck_dn == 0 && a.ffn % 64 == 0 &&
-           a.hidden % kStepK == 0 && a.ffn % kStepK == 0;
+    return a.hidden % ck_gu == 0 && a.hidden % 256 == 0 && a.ffn % ck_dn == 0 && a.ffn % 128 == 0 &&
+           a.hidden % kGStepK == 0 && a.ffn % kGStepK == 0;
 }
 
 int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s) {
@@ -513,10 +591,16 @@ int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }
 
-int launch_combine(const float *x, const float *dn, const uint32_t *slot_of, const float *w, uint32_t hidden,
-                   uint32_t K, uint32_t tokens, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(combine_kernel, dim3(div_up(hidden, 256), tokens), dim3(256), 0, s, x, dn, slot_of, w, hidden,
-                       K, out);
+uint32_t prefill_down_splits(uint32_t experts, uint32_t ffn) {
+    // few experts give few row tiles: split the down projection's K so that
+    // the grid still covers the device
+    return experts <= 16 && ffn % (2 * kGStepK) == 0 ? 2 : 1;
+}
+
+int launch_combine(const float *x, const float *dn, uint32_t splits, uint32_t pairs, const uint32_t *slot_of,
+                   const float *w, uint32_t hidden, uint32_t K, uint32_t tokens, float *out, hipStream_t s) {
+    hipLaunchKernelGGL(combine_kernel, dim3(div_up(hidden, 256), tokens), dim3(256), 0, s, x, dn, splits,
+                       static_cast<uint64_t>(pairs) * hidden, slot_of, w, hidden, K, out);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }

@@ -14,20 +14,25 @@ struct PrefillBuffers {
     uint32_t pairs;              // tokens * top_k
     __bf16 *x;                   // [pairs x hidden] gathered h in the gate/up packed K order
     __bf16 *act;                 // [pairs x ffn] SwiGLU output in the down packed K order
-    float *dn;                   // [pairs x hidden] down projections
+    float *dn;                   // [splits x pairs x hidden] down projections (partial over K splits)
+    uint32_t splits;             // K splits of the down projection (prefill_down_splits)
 };
 
-// Token-expert pairs per row tile of the grouped GEMMs (4 blocks of 32).
-constexpr uint32_t kPrefillTileRows = 128;
+// Token-expert pairs per row tile of the grouped GEMMs (8 blocks of 32).
+constexpr uint32_t kPrefillTileRows = 256;
 
 // The grouped GEMMs need block-type experts with hidden and ffn multiples of
-// the K step (128), of the types' chunk sizes and of the N tiles (hidden % 128,
-// ffn % 64).
+// the K step (128), of the types' chunk sizes and of the N tiles (hidden % 256,
+// ffn % 128).
 bool prefill_gemm_supported(const ExpertArgs &a);
+// K splits of the down projection (its partial products are summed by the
+// combine).
+uint32_t prefill_down_splits(uint32_t experts, uint32_t ffn);
 // gather -> gate/up GEMM + SwiGLU -> down GEMM, over `max_tiles` row tiles.
 int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s);
-// out[t] = x[t] + sum over ranks (rank order) of w * dn[slot_of[t, r]].
-int launch_combine(const float *x, const float *dn, const uint32_t *slot_of, const float *w, uint32_t hidden,
-                   uint32_t K, uint32_t tokens, float *out, hipStream_t s);
+// out[t] = x[t] + sum over ranks (rank order) of w * (sum over splits of
+// dn[split][slot_of[t, r]]).
+int launch_combine(const float *x, const float *dn, uint32_t splits, uint32_t pairs, const uint32_t *slot_of,
+                   const float *w, uint32_t hidden, uint32_t K, uint32_t tokens, float *out, hipStream_t s);
 
 } // namespace fmx
