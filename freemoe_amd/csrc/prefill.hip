@@ -86,19 +86,6 @@ struct GQ80 {
         return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
     }
 };
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const float d = half_bits_to_float(j & 2 ? ((j & 1) ? v.d.y >> 16 : v.d.y & 0xFFFFu)
-                                                     : ((j & 1) ? v.d.x >> 16 : v.d.x & 0xFFFFu));
-            const float q0 = static_cast<float>(static_cast<int8_t>(w[j]));
-            const float q1 = static_cast<float>(static_cast<int8_t>(w[j] >> 8));
-            const float q2 = static_cast<float>(static_cast<int8_t>(w[j] >> 16));
-            const float q3 = static_cast<float>(static_cast<int8_t>(w[j] >> 24));
-            out[2 * j] = pack_bf16x2(d * q0, d * q1);
-            out[2 * j + 1] = pack_bf16x2(d * q2, d * q3);
-        }
-    }
-};
 
 struct GQ40 {
     static constexpr uint32_t kType = FMX_TYPE_Q4_0;
@@ -142,24 +129,6 @@ struct GQ40 {
                                d * static_cast<float>(static_cast<int32_t>(byte >> 4) - 8));
         }
         return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
-    }
-};
-        const uint32_t dw[4] = {v.d.x, v.d.y, v.d.z, v.d.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            // dword i holds bytes b = 4i..4i+3: blocks 2i (bytes 4i, 4i+1) and 2i+1
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const float d = half_bits_to_float(h ? dw[i] >> 16 : dw[i] & 0xFFFFu);
-#pragma unroll
-                for (int bb = 0; bb < 2; ++bb) {
-                    const uint32_t byte = (w[i] >> (8 * (2 * h + bb))) & 0xFFu;
-                    const float lo = d * static_cast<float>(static_cast<int32_t>(byte & 15u) - 8);
-                    const float hi = d * static_cast<float>(static_cast<int32_t>(byte >> 4) - 8);
-                    out[4 * i + 2 * h + bb] = pack_bf16x2(lo, hi);
-                }
-            }
-        }
     }
 };
 
@@ -206,23 +175,6 @@ struct GQ4K {
             v[k] = pack_bf16x2(d1 * static_cast<float>(byte & 15u) - mm1, d2 * static_cast<float>(byte >> 4) - mm2);
         }
         return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
-    }
-};
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            uint32_t sc1, m1, sc2, m2;
-            k4_scale_min(2 * g, hdr + 4, sc1, m1);
-            k4_scale_min(2 * g + 1, hdr + 4, sc2, m2);
-            // dequantize_block's values: (d * sc) * q - dmin * m (quant.cpp:297-318)
-            const float d1 = d * static_cast<float>(sc1), mm1 = dmin * static_cast<float>(m1);
-            const float d2 = d * static_cast<float>(sc2), mm2 = dmin * static_cast<float>(m2);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t byte = (w[g] >> (8 * k)) & 0xFFu;
-                out[4 * g + k] = pack_bf16x2(d1 * static_cast<float>(byte & 15u) - mm1,
-                                             d2 * static_cast<float>(byte >> 4) - mm2);
-            }
-        }
     }
 };
 
