@@ -33,10 +33,14 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// (bf16(a), bf16(b)) rounded to nearest even, a in the low half: one
+// v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-    const __bf16 x = static_cast<__bf16>(a), y = static_cast<__bf16>(b);
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, x)) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, y)) << 16);
+    const f32x2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // ------------------------------------------------------------ block types --
@@ -51,23 +55,22 @@ struct GQ80 {
     // position p = 16 l + 4 j + k holds element 32 j + 8 k + l
     __host__ __device__ static uint32_t elem(uint32_t p) { return 32 * ((p & 15) >> 2) + 8 * (p & 3) + (p >> 4); }
     __host__ __device__ static uint32_t pos(uint32_t e) { return 16 * (e & 7) + 4 * (e >> 5) + ((e & 31) >> 3); }
-    // A lane's half of a K step (64 positions = half a chunk): slices
-    // 4 (step % 2) + 2 h and the next (positions 32 h .. +32 of the step), and
-    // the chunk's four block scales.
+    // A lane's half of a K step (128 positions = one chunk): slices 4 h ..
+    // 4 h + 3 (positions 64 h .. +64 of the step) and the chunk's four block
+    // scales.
     struct WStep {
-        uint4 q[2];
+        uint4 q[4];
         uint2 d;
     };
     __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
                                      uint32_t step, uint32_t h) {
-        const uint32_t c = step >> 1, s0 = 4 * (step & 1) + 2 * h;
-        const uint8_t *q = packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + s0) * 16;
-        w.q[0] = ld16(q);
-        w.q[1] = ld16(q + 16);
-        w.d = ld8(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(c) * 8);
+        const uint8_t *q = packed + g.scale_bytes + (static_cast<uint64_t>(r) * g.chunks + step) * 128 + h * 64;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.q[i] = ld16(q + 16 * i);
+        w.d = ld8(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(step) * 8);
     }
     __device__ static void decode_header(WStep &) {}
-    // Positions 32 h + 8 kk .. +8 of the step: bytes 8 (kk % 2) .. +8 of the
+    // Positions 64 h + 8 kk .. +8 of the step: bytes 8 (kk % 2) .. +8 of the
     // lane's slice kk / 2, i.e. blocks 2 (kk % 2) and 2 (kk % 2) + 1.
     __device__ static bf16x8 dequant_kk(const WStep &w, int kk) {
         const uint4 q = w.q[kk >> 1];
@@ -99,26 +102,30 @@ struct GQ40 {
         const uint32_t j = e >> 5, r = e & 31, nib = r >> 4, which = (r >> 3) & 1, l = r & 7;
         return 32 * l + 4 * j + 2 * which + nib;
     }
-    // A lane's half of a K step (64 positions = a quarter chunk): slice
-    // 2 (step % 4) + h (positions 32 h .. +32 of the step) and the chunk's
-    // eight block scales.
+    // A lane's half of a K step (128 positions = half a chunk): slices
+    // 4 (step % 2) + 2 h and the next (positions 64 h .. +64 of the step), and
+    // the chunk's eight block scales.
     struct WStep {
-        uint4 q;
+        uint4 q[2];
         uint4 d;
     };
     __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
                                      uint32_t step, uint32_t h) {
-        const uint32_t c = step >> 2, sl = 2 * (step & 3) + h;
-        w.q = ld16(packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + sl) * 16);
+        const uint32_t c = step >> 1, s0 = 4 * (step & 1) + 2 * h;
+        const uint8_t *q = packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + s0) * 16;
+        w.q[0] = ld16(q);
+        w.q[1] = ld16(q + 16);
         w.d = ld16(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(c) * 16);
     }
     __device__ static void decode_header(WStep &) {}
-    // Positions 32 h + 8 kk .. +8 of the step: dword kk of the lane's slice;
-    // its bytes are blocks 2 kk (bytes 0, 1) and 2 kk + 1 (bytes 2, 3), low
-    // nibble first.
+    // Positions 64 h + 8 kk .. +8 of the step: dword kk % 4 of the lane's slice
+    // kk / 4; its bytes are blocks 2 (kk % 4) (bytes 0, 1) and 2 (kk % 4) + 1
+    // (bytes 2, 3), low nibble first.
     __device__ static bf16x8 dequant_kk(const WStep &w, int kk) {
-        const uint32_t qw = kk == 0 ? w.q.x : kk == 1 ? w.q.y : kk == 2 ? w.q.z : w.q.w;
-        const uint32_t dd = kk == 0 ? w.d.x : kk == 1 ? w.d.y : kk == 2 ? w.d.z : w.d.w;
+        const uint4 q = w.q[kk >> 2];
+        const int i = kk & 3;
+        const uint32_t qw = i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
+        const uint32_t dd = i == 0 ? w.d.x : i == 1 ? w.d.y : i == 2 ? w.d.z : w.d.w;
         const float d0 = half_bits_to_float(dd & 0xFFFFu), d1 = half_bits_to_float(dd >> 16);
         uint32_t v[4];
 #pragma unroll
@@ -146,26 +153,30 @@ struct GQ4K {
     }
     // A lane's half of a K step: as Q4_0, with the super-block header.
     struct WStep {
-        uint4 q;
+        uint4 q[2];
         uint4 hd;
     };
     __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
                                      uint32_t step, uint32_t h) {
-        const uint32_t c = step >> 2, sl = 2 * (step & 3) + h;
-        w.q = ld16(packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + sl) * 16);
+        const uint32_t c = step >> 1, s0 = 4 * (step & 1) + 2 * h;
+        const uint8_t *q = packed + g.scale_bytes + ((static_cast<uint64_t>(r) * g.chunks + c) * 8 + s0) * 16;
+        w.q[0] = ld16(q);
+        w.q[1] = ld16(q + 16);
         w.hd = ld16(packed + (static_cast<uint64_t>(r) * g.chunks + c) * 16);
     }
-    // Positions 32 h + 8 kk .. +8 of the step: dword kk of the lane's slice,
-    // group kk: low nibbles sub-block 2 kk, high 2 kk + 1.
+    // Positions 64 h + 8 kk .. +8 of the step: dword g = kk % 4 of the lane's
+    // slice kk / 4, group g: low nibbles sub-block 2 g, high 2 g + 1.
     __device__ static bf16x8 dequant_kk(const WStep &w, int kk) {
-        const uint32_t qw = kk == 0 ? w.q.x : kk == 1 ? w.q.y : kk == 2 ? w.q.z : w.q.w;
+        const uint4 q = w.q[kk >> 2];
+        const int gi = kk & 3;
+        const uint32_t qw = gi == 0 ? q.x : gi == 1 ? q.y : gi == 2 ? q.z : q.w;
         uint8_t hdr[16];
         memcpy(hdr, &w.hd, 16);
         const float d = half_bits_to_float(hdr[0] | (hdr[1] << 8));
         const float dmin = half_bits_to_float(hdr[2] | (hdr[3] << 8));
         uint32_t sc1, m1, sc2, m2;
-        k4_scale_min(2 * kk, hdr + 4, sc1, m1);
-        k4_scale_min(2 * kk + 1, hdr + 4, sc2, m2);
+        k4_scale_min(2 * gi, hdr + 4, sc1, m1);
+        k4_scale_min(2 * gi + 1, hdr + 4, sc2, m2);
         const float d1 = d * static_cast<float>(sc1), mm1 = dmin * static_cast<float>(m1);
         const float d2 = d * static_cast<float>(sc2), mm2 = dmin * static_cast<float>(m2);
         uint32_t v[4];
@@ -181,35 +192,35 @@ struct GQ4K {
 // ------------------------------------------------------------ the GEMMs --
 //
 // One workgroup (4 wavefronts, one per SIMD) multiplies a row tile of one
-// expert (up to 256 token-expert pairs = 8 blocks of 32) by 128 weight
+// expert (up to 192 token-expert pairs = 6 blocks of 32) by 128 weight
 // columns; wavefront w owns two 32-column blocks (gate/up: gate and up of the
 // same 32 ffn rows, so SwiGLU pairs meet in one lane; down: 64 rows).
 //
 // Weights never touch LDS: each lane loads its own two rows' packed bytes for
-// a K step (64 packed positions; lanes 0-31 take positions 0-31, lanes 32-63
-// positions 32-63) from HBM into registers, two steps ahead, and dequantises
+// a K step (128 packed positions; lanes 0-31 take positions 0-63, lanes 32-63
+// positions 64-127) from HBM into registers, two steps ahead, and dequantises
 // 8 positions (one MFMA K slice) at a time as the B operand. Each weight byte
 // is read once per row tile, and a row tile holds all of an expert's pairs up
-// to 256. Activations: the tile's rows for the next step are loaded during
+// to 192. Activations: the tile's rows for the next step are loaded during
 // this one and stored to the other of two LDS buffers, where all four
 // wavefronts read their A operands.
 //
 // v_mfma_f32_32x32x16_bf16: A lane l = tile row 32 mb + l % 32, B lane l =
-// column l % 32, both at positions 32 (l / 32) + 8 kk .. +8 of the step (a GEMM
+// column l % 32, both at positions 64 (l / 32) + 8 kk .. +8 of the step (a GEMM
 // may contract over K in any order, as long as A and B agree); C element r of
 // lane l = row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
 
 constexpr uint32_t kGThreads = 256;
-constexpr uint32_t kGBlocks = kPrefillTileRows / 32;         // 8 row blocks of 32
-constexpr uint32_t kGStepK = 64;                              // packed positions per K step
-constexpr uint32_t kGRowBytes = kGStepK * 2;                  // 128 bytes of a tile row
+constexpr uint32_t kGBlocks = kPrefillTileRows / 32;         // 6 row blocks of 32
+constexpr uint32_t kGStepK = 128;                             // packed positions per K step
+constexpr uint32_t kGRowBytes = kGStepK * 2;                  // 256 bytes of a tile row
 constexpr uint32_t kGBufBytes = kPrefillTileRows * kGRowBytes; // one LDS activation buffer
 
-// LDS activation tile: 256 rows x 64 bf16 (128 bytes, eight 16-byte granules);
-// granule g of row r sits at granule g ^ ((r / 2) % 8). A pass of 16 lanes of
-// an A-operand read (16 consecutive rows, one granule) or of a store (8
-// granules of 2 rows, 8 rows apart) then touches 16 distinct bank groups.
-__device__ __forceinline__ uint32_t xswz(uint32_t row) { return (row >> 1) & 7u; }
+// LDS activation tile: 192 rows x 128 bf16 (256 bytes = the 64 banks, sixteen
+// 16-byte granules); granule g of row r sits at granule g ^ (r % 16). A pass
+// of 16 lanes of an A-operand read (16 consecutive rows, one granule) or of a
+// store (one row, 16 granules) then touches 16 distinct bank groups.
+__device__ __forceinline__ uint32_t xswz(uint32_t row) { return row & 15u; }
 
 // Row tile `mt` of the bucketed pairs: (expert, first row, rows); false when
 // mt is past the tiles the bucketing produced (or a tile is malformed).
@@ -226,41 +237,55 @@ __device__ inline bool row_tile(const uint32_t *tiles, uint32_t mt, uint32_t exp
 // this thread's share of the next activation step, the accumulators of NMB
 // row blocks (the kernels instantiate one per possible block count, so no
 // MFMA sits under a branch).
-// Thread t stages granule t % 8 of tile rows t / 8 + 32 i (i < 8); the
-// activation matrix has at least 256 readable rows past every tile's first
+// Thread t stages granule t % 16 of tile rows t / 16 + 16 i (i < 12); the
+// activation matrix has at least 192 readable rows past every tile's first
 // row (the workspace pads it), and rows past the tile only feed output rows
 // that are never written.
 template <class T, uint32_t NMB>
 struct GemmWave {
     typename T::WStep w[3][2];
-    uint4 xv[8];
+    uint4 xv[kPrefillTileRows / 16];
     f32x16 acc[NMB][2];
 
     __device__ __forceinline__ void load_x(const __bf16 *src, uint64_t ld, uint32_t k0) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xv[i] = ld16(src + static_cast<uint64_t>(32 * i) * ld + k0);
+        for (uint32_t i = 0; i < kPrefillTileRows / 16; ++i) xv[i] = ld16(src + static_cast<uint64_t>(16 * i) * ld + k0);
     }
-    // st: byte address of this thread's granule in row t / 8 of the buffer
+    // st: byte address of this thread's granule in row t / 16 of the buffer
     __device__ __forceinline__ void store_x(char *st) const {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4 *>(st + i * 32 * kGRowBytes) = xv[i];
+        for (uint32_t i = 0; i < kPrefillTileRows / 16; ++i)
+            *reinterpret_cast<uint4 *>(st + i * 16 * kGRowBytes) = xv[i];
     }
 
     // The MFMAs of one K step from ring slot `slot`; a_kk[kk]: byte address of
     // the lane's A operand of slice kk in row block 0 of the step's buffer.
-    __device__ __forceinline__ void multiply(int slot, const char *const (&a_kk)[4]) {
+    // Software-pipelined over the 8 K slices: the A operands (LDS) and the B
+    // operands (dequantised weights) of slice kk + 1 are prepared while the
+    // MFMAs of slice kk run, so the VALU work overlaps the matrix unit.
+    __device__ __forceinline__ void multiply(int slot, const char *const (&a_kk)[8]) {
+        bf16x8 av[2][NMB], bv[2][2];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const bf16x8 b0 = T::dequant_kk(w[slot][0], kk), b1 = T::dequant_kk(w[slot][1], kk);
+        for (uint32_t mb = 0; mb < NMB; ++mb)
+            av[0][mb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(a_kk[0] + mb * 32 * kGRowBytes));
+        bv[0][0] = T::dequant_kk(w[slot][0], 0);
+        bv[0][1] = T::dequant_kk(w[slot][1], 0);
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+            const int c = kk & 1, n = c ^ 1;
+            if (kk + 1 < 8) {
+#pragma unroll
+                for (uint32_t mb = 0; mb < NMB; ++mb)
+                    av[n][mb] = __builtin_bit_cast(
+                        bf16x8, *reinterpret_cast<const uint4 *>(a_kk[kk + 1] + mb * 32 * kGRowBytes));
+                bv[n][0] = T::dequant_kk(w[slot][0], kk + 1);
+                bv[n][1] = T::dequant_kk(w[slot][1], kk + 1);
+            }
 #pragma unroll
             for (uint32_t mb = 0; mb < NMB; ++mb) {
-                const bf16x8 av =
-                    __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(a_kk[kk] + mb * 32 * kGRowBytes));
-                acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b0, acc[mb][0], 0, 0, 0);
-                acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, b1, acc[mb][1], 0, 0, 0);
+                acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[c][mb], bv[c][0], acc[mb][0], 0, 0, 0);
+                acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[c][mb], bv[c][1], acc[mb][1], 0, 0, 0);
             }
-            // one K slice at a time: bounds the operands in flight
-            __builtin_amdgcn_sched_barrier(0);
         }
     }
 
@@ -274,9 +299,9 @@ struct GemmWave {
         T::load_step(w[slot_next][0], m0, g, r0, nw, h);
         T::load_step(w[slot_next][1], m1, g, r1, nw, h);
         __builtin_amdgcn_sched_barrier(0);
-        const char *a_kk[4];
+        const char *a_kk[8];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) a_kk[kk] = lds + buf * kGBufBytes + (aoff0 ^ (kk << 4));
+        for (int kk = 0; kk < 8; ++kk) a_kk[kk] = lds + buf * kGBufBytes + (aoff0 ^ (kk << 4));
         multiply(slot, a_kk);
         store_x(lds + (buf ^ 1) * kGBufBytes + stoff);
         load_x(xsrc, ldx, nx * kGStepK);
@@ -289,11 +314,11 @@ struct GemmWave {
                                         uint32_t steps, char *lds) {
         const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
         const uint32_t last = s0 + steps - 1;
-        // A operand of slice kk: row lane % 32 of the block, granule 4 h + kk
+        // A operand of slice kk: row lane % 32 of the block, granule 8 h + kk
         const uint32_t ar = lane & 31;
-        const uint32_t aoff0 = ar * kGRowBytes + (((4 * h) ^ xswz(ar)) << 4);
-        // staging: row tid / 8, granule tid % 8
-        const uint32_t sr = tid >> 3, sg = tid & 7;
+        const uint32_t aoff0 = ar * kGRowBytes + (((8 * h) ^ xswz(ar)) << 4);
+        // staging: row tid / 16, granule tid % 16
+        const uint32_t sr = tid >> 4, sg = tid & 15;
         const uint32_t stoff = sr * kGRowBytes + ((sg ^ xswz(sr)) << 4);
         xsrc += static_cast<uint64_t>(sr) * ldx + 8 * sg;
 #pragma unroll
@@ -394,9 +419,7 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     case 3: gate_up_tile<T, TD, 3>(a, e, row0, rows, x, act, xlds); break;
     case 4: gate_up_tile<T, TD, 4>(a, e, row0, rows, x, act, xlds); break;
     case 5: gate_up_tile<T, TD, 5>(a, e, row0, rows, x, act, xlds); break;
-    case 6: gate_up_tile<T, TD, 6>(a, e, row0, rows, x, act, xlds); break;
-    case 7: gate_up_tile<T, TD, 7>(a, e, row0, rows, x, act, xlds); break;
-    default: gate_up_tile<T, TD, 8>(a, e, row0, rows, x, act, xlds); break;
+    default: gate_up_tile<T, TD, 6>(a, e, row0, rows, x, act, xlds); break;
     }
 }
 
@@ -441,9 +464,7 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     case 3: down_tile<T, 3>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
     case 4: down_tile<T, 4>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
     case 5: down_tile<T, 5>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
-    case 6: down_tile<T, 6>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
-    case 7: down_tile<T, 7>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
-    default: down_tile<T, 8>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
+    default: down_tile<T, 6>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
     }
 }
 

@@ -18,8 +18,8 @@ struct PrefillBuffers {
     uint32_t splits;             // K splits of the down projection (prefill_down_splits)
 };
 
-// Token-expert pairs per row tile of the grouped GEMMs (8 blocks of 32).
-constexpr uint32_t kPrefillTileRows = 256;
+// Token-expert pairs per row tile of the grouped GEMMs (6 blocks of 32).
+constexpr uint32_t kPrefillTileRows = 192;
 
 // The grouped GEMMs need block-type experts with hidden and ffn multiples of
 // the K step (128), of the types' chunk sizes and of the N tiles (hidden % 256,
