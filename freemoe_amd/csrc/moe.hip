@@ -59,15 +59,18 @@ __device__ inline double wave_sum_double(double v) {
 // 2^52) bounds rel * |yd| / ulp(yd) = rel * 2^52 * 1.m from above through the
 // top 8 mantissa bits. Values outside float's normal range (other than 0),
 // infinities and NaN always count as unsafe.
+// Branch-free (it runs on every element); tol0 < 2^24.
 __device__ inline bool rounding_unsafe(double yd, uint32_t tol0) {
     const uint64_t b = static_cast<uint64_t>(__double_as_longlong(yd));
-    const uint32_t hi = static_cast<uint32_t>(b >> 32);
+    const uint32_t hi = static_cast<uint32_t>(b >> 32), lo = static_cast<uint32_t>(b);
     const uint32_t ex = (hi >> 20) & 0x7FFu;
-    if (ex < 1023u - 126u || ex >= 1023u + 127u) return yd != 0.0;
-    const uint32_t low29 = static_cast<uint32_t>(b) & 0x1FFFFFFFu;
+    const bool outside = ex - (1023u - 126u) >= 253u; // ex < 897 or ex >= 1150
+    const bool nonzero = ((hi << 1) | lo) != 0u;
+    const uint32_t low29 = lo & 0x1FFFFFFFu;
     const uint32_t d = low29 >= (1u << 28) ? low29 - (1u << 28) : (1u << 28) - low29;
     const uint32_t m8 = (hi >> 12) & 0xFFu;
-    return d <= tol0 + ((tol0 * (m8 + 1u)) >> 8) + 1u;
+    const bool near = d <= tol0 + (__umul24(tol0, m8 + 1u) >> 8) + 1u;
+    return outside ? nonzero : near;
 }
 
 __device__ inline float normalised(float x, const float *w, uint32_t k, double scale,
@@ -267,7 +270,7 @@ __global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float
                 const float gain = g4 ? static_cast<float>(a.norm_bias + static_cast<double>(gs[j])) : 1.0f;
                 const double yd = static_cast<double>(xs[j]) * scale * static_cast<double>(gain);
                 hv[4 * i + j] = static_cast<float>(yd);
-                if (pass == 0 && tid + i * NT < H4) unsafe |= rounding_unsafe(yd, tol0);
+                if (pass == 0) unsafe |= (tid + i * NT < H4) & rounding_unsafe(yd, tol0);
             }
         }
         if (pass == 1) break;
@@ -318,8 +321,39 @@ __global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float
         const float4 *h4 = reinterpret_cast<const float4 *>(hs + c * cs);
         const float4 *w4 = reinterpret_cast<const float4 *>(rs + c * cs);
         float acc = 0.0f;
-#pragma unroll 8
-        for (uint32_t i = 0; i < S / 4; ++i) {
+        // the chain is a dependent FMA sequence: its operands come from LDS in
+        // batches of 32 steps, the next batch requested before this one's FMAs
+        constexpr uint32_t kB = 8; // float4 per batch
+        const uint32_t nb = S / 4 / kB;
+        float4 hb[2][kB], wb[2][kB];
+        if (nb > 0) {
+#pragma unroll
+            for (uint32_t q = 0; q < kB; ++q) {
+                hb[0][q] = h4[q];
+                wb[0][q] = w4[q];
+            }
+        }
+        for (uint32_t bi = 0; bi < nb; bi += 2) {
+#pragma unroll
+            for (uint32_t half = 0; half < 2; ++half) {
+                const uint32_t b = bi + half;
+                if (b >= nb) break;
+                const uint32_t nx = (b + 1 < nb ? b + 1 : b) * kB;
+#pragma unroll
+                for (uint32_t q = 0; q < kB; ++q) {
+                    hb[half ^ 1][q] = h4[nx + q];
+                    wb[half ^ 1][q] = w4[nx + q];
+                }
+#pragma unroll
+                for (uint32_t q = 0; q < kB; ++q) {
+                    acc = fma_rn(wb[half][q].x, hb[half][q].x, acc);
+                    acc = fma_rn(wb[half][q].y, hb[half][q].y, acc);
+                    acc = fma_rn(wb[half][q].z, hb[half][q].z, acc);
+                    acc = fma_rn(wb[half][q].w, hb[half][q].w, acc);
+                }
+            }
+        }
+        for (uint32_t i = nb * kB; i < S / 4; ++i) {
             const float4 hq = h4[i], wq = w4[i];
             acc = fma_rn(wq.x, hq.x, acc);
             acc = fma_rn(wq.y, hq.y, acc);
