@@ -84,24 +84,31 @@ def cpu_baseline(lw, x, target_s=15.0, max_tokens=256):
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 PREFILL_WORKLOAD = "mixtral-q8_0"
+RAGGED_WORKLOAD = "finegrained"
+PREFILL_TITLES = {
+    "mixtral-q8_0": "Mixtral-shaped MoE layer prefill, 512 tokens, Q8_0 experts",
+    "finegrained": "fine-grained ragged MoE layer prefill, 2048 tokens, 128 experts top-8, Q4_K experts, "
+                   "Zipf(1.2) router bias",
+}
 
 
-def prefill_leg(dev, seed=1234, reps=10, cpu=True):
-    """The Mixtral-shaped layer with Q8_0 experts over a 512-token prefill:
-    whole-layer time (routing, bucketing, both grouped GEMMs, combine) from
-    HIP events on the launch stream, against bf16 MFMA peak and HBM peak."""
+def prefill_leg(dev, workload=PREFILL_WORKLOAD, seed=1234, reps=10, cpu=True, cpu_seconds=10.0):
+    """A whole-layer prefill (routing, bucketing, both grouped GEMMs, combine)
+    timed with HIP events on the launch stream, against bf16 MFMA peak, HBM
+    peak and the ragged bound sum_e max(flops_e / MFMA peak, bytes_e / HBM
+    peak) over the experts that received tokens."""
     import numpy as np
     import torch
     from freemoe_amd import fmx
     from freemoe_amd import workloads as wl
     from freemoe_amd.device import DeviceLayer
 
-    spec = wl.WORKLOADS[PREFILL_WORKLOAD]
+    spec = dict(wl.WORKLOADS[workload])
     H, F, E, K, T = spec["hidden"], spec["ffn"], spec["experts"], spec["top_k"], spec["tokens"]
     t_gen = time.perf_counter()
-    lw = wl.make_layer(H, F, E, K, spec["type_id"], seed)
+    lw = wl.make_layer(H, F, E, K, spec["type_id"], seed, zipf_s=spec.get("zipf_s"))
     x = wl.inputs(H, T, seed + 1)
-    print(f"[bench] prefill weights in {time.perf_counter() - t_gen:.1f}s", file=sys.stderr, flush=True)
+    print(f"[bench] {workload} weights in {time.perf_counter() - t_gen:.1f}s", file=sys.stderr, flush=True)
     dl = DeviceLayer(lw, dev)
     xd = torch.from_numpy(x).to(dev)
     out = torch.empty_like(xd)
@@ -122,26 +129,32 @@ def prefill_leg(dev, seed=1234, reps=10, cpu=True):
     pairs = T * K
     flops = 6.0 * pairs * H * F
     counts = np.bincount(ids.cpu().numpy().reshape(-1), minlength=E)
-    wbytes = int((counts > 0).sum()) * dl.weight_bytes_per_expert()
+    per_expert = dl.weight_bytes_per_expert()
+    wbytes = int((counts > 0).sum()) * per_expert
     act_bytes = T * H * 4 * 2 + pairs * (H + F) * 2 * 2 + pairs * H * 4 * 2
     tflops = flops / (ms * 1e-3) / 1e12
     gbs = (wbytes + act_bytes) / (ms * 1e-3) / 1e9
-    res = {"workload": "Mixtral-shaped MoE layer prefill, 512 tokens, Q8_0 experts", "tokens": T, "hidden": H,
-           "ffn": F, "experts": E, "top_k": K, "ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
+    ragged_s = sum(max(6.0 * n * H * F / (MFMA_BF16_PEAK_TFLOPS * 1e12), per_expert / (HBM_PEAK_GBS * 1e9))
+                   for n in counts if n > 0)
+    res = {"workload": PREFILL_TITLES[workload], "tokens": T, "hidden": H,
+           "ffn": F, "experts": E, "top_k": K, "expert_weights": wl.TYPE_NAMES[lw.gate_type].upper(),
+           "ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
            "expert_token_counts": counts.tolist(),
            "roofline": {"bound": "mfma", "kernel": "whole layer (route, bucket, gather, gate/up GEMM, down GEMM, "
                                                    "combine)", "achieved": round(tflops, 1),
                         "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flops": flops,
                         "hbm_achieved_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                        "hbm_bytes": wbytes + act_bytes}}
+                        "hbm_bytes": wbytes + act_bytes,
+                        "ragged_bound_ms": round(ragged_s * 1e3, 4),
+                        "ragged_frac": round(ragged_s * 1e3 / ms, 4)}}
     if cpu:
         sys.path.insert(0, str(ROOT / "oracle"))
         import fmoracle as fo
         hl = fo.host_layer(lw)
         n, t0 = 0, time.perf_counter()
         outs = []
-        while n < T and time.perf_counter() - t0 < 10.0:
+        while n < T and time.perf_counter() - t0 < cpu_seconds:
             o, _, _ = hl.ref_forward_batch(x[n:n + 1], fo.ISA_AVX2, threads=2)
             outs.append(o)
             n += 1
@@ -150,8 +163,8 @@ def prefill_leg(dev, seed=1234, reps=10, cpu=True):
         got = out[:n].cpu().numpy().astype(np.float64) - x[:n]
         err = got - ref
         res["cpu_baseline"] = {"value": round(n / dt, 3), "unit": "tokens/s", "cores": 2, "kind": "reference",
-                               "sample": f"first {n} of the 512 tokens, one at a time (the reference has no batched "
-                                         "MoE path), reference gemv_quant at 2 WorkerPool threads"}
+                               "sample": f"first {n} of the {T} tokens, one at a time (the reference has no "
+                                         "batched MoE path), reference gemv_quant at 2 WorkerPool threads"}
         res["parity"] = {"tokens": n, "ids_equal": None,
                          "ffn_rel_norm": float(np.linalg.norm(err) / np.linalg.norm(ref)),
                          "ffn_rel_max": float(np.abs(err).max() / np.abs(ref).max()), "tolerance": 2e-2}
@@ -171,6 +184,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token Q8_0 prefill leg")
     ap.add_argument("--prefill-only", action="store_true", help="run only the prefill leg (for profiling)")
+    ap.add_argument("--ragged-only", action="store_true",
+                    help="run only the fine-grained ragged prefill leg (for profiling)")
     ap.add_argument("--copy-bytes", type=int, default=0,
                     help="also run one plain device-to-device copy of this many bytes (a known-traffic "
                          "kernel that scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters)")
@@ -196,6 +211,10 @@ def main() -> int:
     if args.prefill_only:
         res = prefill_leg(dev, reps=args.steps, cpu=not args.no_cpu_baseline)
         print(json.dumps({"prefill": res}))
+        return 0
+    if args.ragged_only:
+        res = prefill_leg(dev, RAGGED_WORKLOAD, reps=args.steps, cpu=not args.no_cpu_baseline)
+        print(json.dumps({"prefill_ragged": res}))
         return 0
 
     spec = wl.WORKLOADS[WORKLOAD]
@@ -306,6 +325,12 @@ def main() -> int:
             result["prefill"] = prefill_leg(dev, cpu=not args.no_cpu_baseline)
         except Exception as e:  # reported, never silently dropped
             result["prefill"] = {"error": f"{type(e).__name__}: {e}"}
+        print("[bench] ragged prefill leg", file=sys.stderr, flush=True)
+        try:
+            result["prefill_ragged"] = prefill_leg(dev, RAGGED_WORKLOAD, cpu=not args.no_cpu_baseline,
+                                                   cpu_seconds=8.0)
+        except Exception as e:  # reported, never silently dropped
+            result["prefill_ragged"] = {"error": f"{type(e).__name__}: {e}"}
     print(json.dumps(result))
     return 0
 

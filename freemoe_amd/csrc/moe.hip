@@ -189,6 +189,85 @@ __device__ Routing wave_route(const RouteArgs &a, const float *__restrict__ logi
     return r;
 }
 
+// RMSNorm (engine.cpp:723-740) of one token held P float4 per thread
+// (element 4 (tid + i NT) + j in xv[i], its gain in gv[i]) into hv[4 i + j].
+// The reference's sum of squares is a sequential double sum; here it is a
+// parallel sum plus a certificate: every normalised value is checked to lie
+// farther from a float rounding boundary than the worst-case difference
+// between the two sums can move it; only when one is that close does one lane
+// redo the sum in the reference's order, from a copy of x in `scratch` (LDS,
+// at least hidden floats, 16-byte aligned). Either way hv is the reference's h
+// bit for bit. Every thread of the workgroup calls it; it ends after a barrier.
+template <uint32_t NT, uint32_t P>
+__device__ __forceinline__ void token_rmsnorm(const RouteArgs &a, const float4 (&xv)[P], const float4 (&gv)[P],
+                                              bool has_gain, float (&hv)[4 * P], float *scratch) {
+    __shared__ double wave_part[NT / 64];
+    __shared__ double ss_s;
+    __shared__ int unsafe_s;
+    const uint32_t H = a.hidden, tid = threadIdx.x, H4 = H / 4;
+    double part = 0.0;
+#pragma unroll
+    for (uint32_t i = 0; i < P; ++i) {
+        if (tid + i * NT < H4) {
+            part += static_cast<double>(xv[i].x) * static_cast<double>(xv[i].x);
+            part += static_cast<double>(xv[i].y) * static_cast<double>(xv[i].y);
+            part += static_cast<double>(xv[i].z) * static_cast<double>(xv[i].z);
+            part += static_cast<double>(xv[i].w) * static_cast<double>(xv[i].w);
+        }
+    }
+    part = wave_sum_double(part);
+    if ((tid & 63) == 0) wave_part[tid >> 6] = part;
+    if (tid == 0) unsafe_s = 0;
+    __syncthreads();
+    double ss = wave_part[0];
+#pragma unroll
+    for (uint32_t w = 1; w < NT / 64; ++w) ss += wave_part[w];
+    // |parallel sum - sequential sum| <= (H + 32) u ss; scale moves by half of
+    // that plus a few roundings
+    const double rel_tol = 0.6e-16 * static_cast<double>(H + 32) + 2e-15;
+    const uint32_t tol0 = static_cast<uint32_t>(ceil(rel_tol * 4503599627370496.0)); // rel_tol * 2^52
+    bool unsafe = false;
+    for (int pass = 0; pass < 2; ++pass) {
+        const double scale = 1.0 / sqrt(ss / static_cast<double>(H) + a.rms_eps);
+#pragma unroll
+        for (uint32_t i = 0; i < P; ++i) {
+            const float xs[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+            const float gs[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w};
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                const float gain = has_gain ? static_cast<float>(a.norm_bias + static_cast<double>(gs[j])) : 1.0f;
+                const double yd = static_cast<double>(xs[j]) * scale * static_cast<double>(gain);
+                hv[4 * i + j] = static_cast<float>(yd);
+                if (pass == 0) unsafe |= (tid + i * NT < H4) & rounding_unsafe(yd, tol0);
+            }
+        }
+        if (pass == 1) break;
+        if (__any(unsafe) && (tid & 63) == 0) unsafe_s = 1;
+        __syncthreads();
+        if (!unsafe_s) break;
+        // the reference's order: x into LDS, one lane sums it
+        float4 *xl = reinterpret_cast<float4 *>(scratch);
+#pragma unroll
+        for (uint32_t i = 0; i < P; ++i)
+            if (tid + i * NT < H4) xl[tid + i * NT] = xv[i];
+        __syncthreads();
+        if (tid == 0) {
+            double s = 0.0;
+#pragma unroll 8
+            for (uint32_t q = 0; q < H4; ++q) {
+                const float4 v = xl[q];
+                s += static_cast<double>(v.x) * static_cast<double>(v.x);
+                s += static_cast<double>(v.y) * static_cast<double>(v.y);
+                s += static_cast<double>(v.z) * static_cast<double>(v.z);
+                s += static_cast<double>(v.w) * static_cast<double>(v.w);
+            }
+            ss_s = s;
+        }
+        __syncthreads();
+        ss = ss_s;
+    }
+}
+
 // LDS layout of route_rows_kernel: h and the router row each as 16 chains of
 // `cs` floats, element k at (k % 16) * cs + k / 16, so that chain lane c reads
 // its elements in order with 16-byte loads. cs = 4 (mod 64) puts the 16
@@ -216,9 +295,6 @@ __global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float
                                                         float *__restrict__ h_out, float *__restrict__ logits) {
     constexpr uint32_t P = 4;
     extern __shared__ __align__(16) float lds[];
-    __shared__ double wave_part[NT / 64];
-    __shared__ double ss_s;
-    __shared__ int unsafe_s;
     const uint32_t H = a.hidden, E = a.experts, tid = threadIdx.x;
     const uint32_t t = blockIdx.x, row = blockIdx.y;
     const uint32_t H4 = H / 4, cs = route_chain_stride(H);
@@ -236,68 +312,8 @@ __global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float
         rv[i] = r4[qc];
         gv[i] = g4 ? g4[qc] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
-    double part = 0.0;
-#pragma unroll
-    for (uint32_t i = 0; i < P; ++i) {
-        if (tid + i * NT < H4) {
-            part += static_cast<double>(xv[i].x) * static_cast<double>(xv[i].x);
-            part += static_cast<double>(xv[i].y) * static_cast<double>(xv[i].y);
-            part += static_cast<double>(xv[i].z) * static_cast<double>(xv[i].z);
-            part += static_cast<double>(xv[i].w) * static_cast<double>(xv[i].w);
-        }
-    }
-    part = wave_sum_double(part);
-    if ((tid & 63) == 0) wave_part[tid >> 6] = part;
-    if (tid == 0) unsafe_s = 0;
-    __syncthreads();
-    double ss = wave_part[0];
-#pragma unroll
-    for (uint32_t w = 1; w < NT / 64; ++w) ss += wave_part[w];
-    // |parallel sum - sequential sum| <= (H + 32) u ss; scale moves by half of
-    // that plus a few roundings
-    const double rel_tol = 0.6e-16 * static_cast<double>(H + 32) + 2e-15;
-    const uint32_t tol0 = static_cast<uint32_t>(ceil(rel_tol * 4503599627370496.0)); // rel_tol * 2^52
     float hv[4 * P];
-    bool unsafe = false;
-    for (int pass = 0; pass < 2; ++pass) {
-        const double scale = 1.0 / sqrt(ss / static_cast<double>(H) + a.rms_eps);
-#pragma unroll
-        for (uint32_t i = 0; i < P; ++i) {
-            const float xs[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
-            const float gs[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w};
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) {
-                const float gain = g4 ? static_cast<float>(a.norm_bias + static_cast<double>(gs[j])) : 1.0f;
-                const double yd = static_cast<double>(xs[j]) * scale * static_cast<double>(gain);
-                hv[4 * i + j] = static_cast<float>(yd);
-                if (pass == 0) unsafe |= (tid + i * NT < H4) & rounding_unsafe(yd, tol0);
-            }
-        }
-        if (pass == 1) break;
-        if (__any(unsafe) && (tid & 63) == 0) unsafe_s = 1;
-        __syncthreads();
-        if (!unsafe_s) break;
-        // the reference's order: x into LDS, one lane sums it
-        float4 *xl = reinterpret_cast<float4 *>(rs);
-#pragma unroll
-        for (uint32_t i = 0; i < P; ++i)
-            if (tid + i * NT < H4) xl[tid + i * NT] = xv[i];
-        __syncthreads();
-        if (tid == 0) {
-            double s = 0.0;
-#pragma unroll 8
-            for (uint32_t q = 0; q < H4; ++q) {
-                const float4 v = xl[q];
-                s += static_cast<double>(v.x) * static_cast<double>(v.x);
-                s += static_cast<double>(v.y) * static_cast<double>(v.y);
-                s += static_cast<double>(v.z) * static_cast<double>(v.z);
-                s += static_cast<double>(v.w) * static_cast<double>(v.w);
-            }
-            ss_s = s;
-        }
-        __syncthreads();
-        ss = ss_s;
-    }
+    token_rmsnorm<NT, P>(a, xv, gv, g4 != nullptr, hv, rs);
     // h and the router row into the chain layout
 #pragma unroll
     for (uint32_t i = 0; i < P; ++i) {
@@ -368,6 +384,134 @@ __global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float
         for (uint32_t k = tail8 ? n16 + 8 : n16; k < H; ++k)
             total = fma_rn(rs[(k - n16) * cs + S], hs[(k - n16) * cs + S], total);
         if (c == 0) logits[static_cast<uint64_t>(t) * E + row] = a.router_bias ? total + a.router_bias[row] : total;
+    }
+}
+
+// RMSNorm of token blockIdx.x into h (batched routing). NT threads, 4 float4
+// per thread (hidden <= 16 NT); LDS: hidden floats for the in-order fallback.
+template <uint32_t NT>
+__global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *__restrict__ x,
+                                                     float *__restrict__ h) {
+    constexpr uint32_t P = 4;
+    extern __shared__ __align__(16) float lds[];
+    const uint32_t H = a.hidden, H4 = H / 4, tid = threadIdx.x, t = blockIdx.x;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + static_cast<uint64_t>(t) * H);
+    const float4 *g4 = reinterpret_cast<const float4 *>(a.norm_weight);
+    float4 xv[P], gv[P];
+#pragma unroll
+    for (uint32_t i = 0; i < P; ++i) {
+        const uint32_t q = tid + i * NT;
+        const uint32_t qc = q < H4 ? q : H4 - 1;
+        xv[i] = x4[qc];
+        gv[i] = g4 ? g4[qc] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+    }
+    float hv[4 * P];
+    token_rmsnorm<NT, P>(a, xv, gv, g4 != nullptr, hv, lds);
+    float4 *h4 = reinterpret_cast<float4 *>(h + static_cast<uint64_t>(t) * H);
+#pragma unroll
+    for (uint32_t i = 0; i < P; ++i) {
+        const uint32_t q = tid + i * NT;
+        if (q < H4) h4[q] = make_float4(hv[4 * i], hv[4 * i + 1], hv[4 * i + 2], hv[4 * i + 3]);
+    }
+}
+
+// Router logits of 16 tokens x 16 router rows per workgroup (batched
+// routing): every (token, row) pair runs the 16 FMA chains of the reference's
+// gemv_avx2_row order (chain c takes elements 16 s + c, s = 0, 1, ...), lane c
+// of a 16-lane group owning chain c of a 4 x 4 block of pairs (16 independent
+// chains per lane). h and the router rows pass through LDS 256 elements (16
+// steps of every chain) at a time, the next tile requested during this one's
+// FMAs; then the lane tree, the sequential tail and the logit bias, as in
+// f32_row_chains. grid: (ceil(tokens / 16), ceil(experts / 16)).
+constexpr uint32_t kRtPad = 20; // floats per (token or row, chain) in LDS: 16 steps + 4
+__global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const float *__restrict__ h,
+                                                          uint32_t tokens, float *__restrict__ logits) {
+    __shared__ __align__(16) float hl[16][16][kRtPad];
+    __shared__ __align__(16) float wl[16][16][kRtPad];
+    const uint32_t H = a.hidden, E = a.experts, tid = threadIdx.x;
+    const uint32_t c = tid & 15, g = tid >> 4;
+    const uint32_t tg = (g & 3) * 4, rg = (g >> 2) * 4;
+    const uint32_t t0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
+    const uint32_t S = H / 16, n16 = S * 16, ntiles = (S + 15) / 16;
+    // staging: thread -> token / row tid / 16, float4 q = tid % 16 + 16 i of the tile
+    const uint32_t st = tid >> 4, sq = tid & 15;
+    const float *hsrc = h + static_cast<uint64_t>(t0 + st < tokens ? t0 + st : tokens - 1) * H;
+    const float *wsrc = a.router + static_cast<uint64_t>(r0 + st < E ? r0 + st : E - 1) * H;
+    float4 hv[4], wv[4];
+    auto load_tile = [&](uint32_t k) {
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t e = 256 * k + 4 * (sq + 16 * i);
+            const uint32_t ec = e + 4 <= n16 ? e : 0; // past the chains' elements: unused
+            hv[i] = *reinterpret_cast<const float4 *>(hsrc + ec);
+            wv[i] = *reinterpret_cast<const float4 *>(wsrc + ec);
+        }
+    };
+    auto store_tile = [&]() {
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t q = sq + 16 * i, s0 = q >> 2, c0 = 4 * (q & 3);
+            const float hh[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
+            const float ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                hl[st][c0 + j][s0] = hh[j];
+                wl[st][c0 + j][s0] = ww[j];
+            }
+        }
+    };
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    if (ntiles > 0) load_tile(0);
+    for (uint32_t k = 0; k < ntiles; ++k) {
+        store_tile();
+        __syncthreads();
+        if (k + 1 < ntiles) load_tile(k + 1);
+        const uint32_t steps = S - 16 * k < 16 ? S - 16 * k : 16;
+        for (uint32_t s4 = 0; s4 < steps; s4 += 4) {
+            float4 hq[4], wq[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                hq[i] = *reinterpret_cast<const float4 *>(&hl[tg + i][c][s4]);
+                wq[i] = *reinterpret_cast<const float4 *>(&wl[rg + i][c][s4]);
+            }
+            const uint32_t ns = steps - s4 < 4 ? steps - s4 : 4;
+#pragma unroll
+            for (uint32_t u = 0; u < 4; ++u) {
+                if (u >= ns) break;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float hu = u == 0 ? hq[i].x : u == 1 ? hq[i].y : u == 2 ? hq[i].z : hq[i].w;
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const float wu = u == 0 ? wq[j].x : u == 1 ? wq[j].y : u == 2 ? wq[j].z : wq[j].w;
+                        acc[i][j] = fma_rn(wu, hu, acc[i][j]);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    const bool tail8 = H - n16 >= 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = t0 + tg + i;
+        const float *hr = h + static_cast<uint64_t>(t < tokens ? t : tokens - 1) * H;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t r = r0 + rg + j;
+            const float *wr = a.router + static_cast<uint64_t>(r < E ? r : E - 1) * H;
+            float v = acc[i][j];
+            if (tail8 && c < 8) v = fma_rn(wr[n16 + c], hr[n16 + c], v);
+            const float tt = v + lane_xor(v, 8);
+            float total = hsum8_lanes(tt);
+            for (uint32_t kk = tail8 ? n16 + 8 : n16; kk < H; ++kk) total = fma_rn(wr[kk], hr[kk], total);
+            if (c == 0 && t < tokens && r < E)
+                logits[static_cast<uint64_t>(t) * E + r] = a.router_bias ? total + a.router_bias[r] : total;
+        }
     }
 }
 
@@ -669,9 +813,34 @@ int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, flo
     return FMX_OK;
 }
 
+// Batched routing: RMSNorm once per token into h, then the router logits in
+// tiles of 16 tokens x 16 rows (a workgroup per router row and token would
+// redo each token's RMSNorm once per expert).
+int launch_route_batched(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
+                         hipStream_t s) {
+    if (a.hidden > kMaxHidden || a.hidden % 4 || a.experts == 0) return FMX_ERR_SHAPE_MISMATCH;
+    const size_t lds = static_cast<size_t>(a.hidden) * sizeof(float);
+    if (a.hidden <= 16 * 256) {
+        auto k = rmsnorm_kernel<256>;
+        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+        hipLaunchKernelGGL(k, dim3(tokens), dim3(256), lds, s, a, x, h);
+    } else {
+        auto k = rmsnorm_kernel<1024>;
+        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+        hipLaunchKernelGGL(k, dim3(tokens), dim3(1024), lds, s, a, x, h);
+    }
+    FMX_LAUNCH_CHECK();
+    hipLaunchKernelGGL(router_tile_kernel, dim3(div_up(tokens, 16), div_up(a.experts, 16)), dim3(256), 0, s, a, h,
+                       tokens, logits);
+    FMX_LAUNCH_CHECK();
+    return FMX_OK;
+}
+
 int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                  uint32_t *ids, float *weights, uint32_t *status, hipStream_t s) {
-    if (int rc = launch_route_logits(a, x, tokens, h, logits, s)) return rc;
+    if (int rc = h && tokens > 1 ? launch_route_batched(a, x, tokens, h, logits, s)
+                                 : launch_route_logits(a, x, tokens, h, logits, s))
+        return rc;
     hipLaunchKernelGGL(route_finish_kernel, dim3(tokens), dim3(64), 0, s, a, logits, ids, weights, status);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
