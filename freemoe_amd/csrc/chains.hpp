@@ -117,6 +117,11 @@ struct Q40 {
         k.s = ld16(w.scales + static_cast<uint64_t>(c) * 16);
         return k;
     }
+    // The row's pointers moved n chunks on.
+    __device__ static void advance(Row &w, uint32_t n) {
+        w.quants += static_cast<uint64_t>(n) * 128;
+        w.scales += static_cast<uint64_t>(n) * 16;
+    }
 
     // The x values of half a chunk (4 blocks) from LDS: per block the lane's
     // float4 and its 8 * sum.
@@ -238,6 +243,10 @@ struct Q80 {
         k.s = ld8(w.scales + static_cast<uint64_t>(c) * 8);
         return k;
     }
+    __device__ static void advance(Row &w, uint32_t n) {
+        w.quants += static_cast<uint64_t>(n) * 128;
+        w.scales += static_cast<uint64_t>(n) * 8;
+    }
 
     __device__ static float sbyte(uint32_t w, int k) {
         return static_cast<float>(static_cast<int32_t>(w << (24 - 8 * k)) >> 24);
@@ -329,6 +338,10 @@ struct Q4K {
         k.h = ld16(w.header + static_cast<uint64_t>(c) * 16);
         return k;
     }
+    __device__ static void advance(Row &w, uint32_t n) {
+        w.quants += static_cast<uint64_t>(n) * 128;
+        w.header += static_cast<uint64_t>(n) * 16;
+    }
 
     template <int NR, bool FULL = false>
     __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t nb_tile,
@@ -419,14 +432,20 @@ __device__ __forceinline__ void run_chunks_pf(const typename T::Row (&rows)[NR],
 // The chunks live in a ring of kSlots = PF + 1 register slots: the load for
 // chunk c + PF goes into the slot chunk c - 1 just left, before chunk c is
 // consumed, with every slot index a compile-time constant. Every load is
-// issued unconditionally (past the row's last chunk it re-reads that chunk,
-// which the caches hold): a load under a branch makes the compiler's wait
-// counts conservative, and it then waits for every load in flight before
-// each chunk, which removes the prefetch. Every tile must start at a multiple
-// of kSlots chunks.
-// The compiler's wait counts are conservative at a loop's head: the first
-// chunk of every pass through the steady-state loop waits for every load in
-// flight. U rings per pass (U * kSlots chunks) make that wait rare.
+// issued unconditionally (past the row's last chunk the steady state reads on
+// into the next row or the layout's tail and the last partial ring re-reads
+// the last chunk): a load under a branch makes the compiler's wait counts
+// conservative, and it then waits for every load in flight before each chunk,
+// which removes the prefetch. Every tile must start at a multiple of kSlots
+// chunks.
+// In the steady state every load is addressed from row pointers that move
+// one ring on per pass, with the chunk's distance from them a compile-time
+// constant (an instruction offset): no address is computed per load, and the
+// prefetch reads up to PF chunks past a row's last chunk, which the packed
+// layout's tail keeps inside the matrix's allocation. (Address temporaries
+// computed per load made the compiler reuse registers of loads still in
+// flight, and wait for all of them at the top of every pass.) U rings per pass
+// (U * kSlots chunks) make the loop-head wait rare where it remains.
 // kPipe (types with XHalf / read_half / compute_half): in the steady state
 // the LDS reads of the next half chunk are in flight during the arithmetic of
 // the current one, for kernels with too few wavefronts per SIMD to hide LDS
@@ -435,17 +454,20 @@ template <class T, int NR, int PF, int U = 1, bool kPipe = false>
 struct ChunkStream {
     static constexpr int kSlots = PF + 1;
     typename T::Chunk buf[kSlots][NR];
+    // the rows' pointers at the stream's position (the first chunk run() has
+    // not consumed yet)
+    typename T::Row at[NR];
 
     // One full chunk `cc` from `cur`, with `xa` holding its first half's x
-    // values on entry and the next chunk's (chunk cn) on return; requests
-    // chunk `nxt` into `dst` first.
+    // values on entry and the next chunk's (chunk cn) on return; first
+    // requests the chunk `rel` chunks past the stream position into `dst`.
     template <class XH>
-    __device__ __forceinline__ void pipe_step(const typename T::Row (&rows)[NR], const typename T::Chunk (&cur)[NR],
-                                              typename T::Chunk (&dst)[NR], uint32_t nxt, uint32_t cc,
-                                              uint32_t cn, const float *lds, uint32_t nb_tile, uint32_t tile_b0,
-                                              uint32_t l, float (&t)[NR], XH &xa, XH &xb) {
+    __device__ __forceinline__ void pipe_step(const typename T::Chunk (&cur)[NR], typename T::Chunk (&dst)[NR],
+                                              uint32_t rel, uint32_t cc, uint32_t cn, const float *lds,
+                                              uint32_t nb_tile, uint32_t tile_b0, uint32_t l, float (&t)[NR],
+                                              XH &xa, XH &xb) {
 #pragma unroll
-        for (int i = 0; i < NR; ++i) dst[i] = T::load(rows[i], nxt);
+        for (int i = 0; i < NR; ++i) dst[i] = T::load(at[i], rel);
         __builtin_amdgcn_sched_barrier(0);
         T::read_half(xb, lds, nb_tile, cc * T::kPerChunk - tile_b0, 1, l);
         __builtin_amdgcn_sched_barrier(0);
@@ -455,19 +477,29 @@ struct ChunkStream {
         T::template compute_half<NR, true>(cur, xb, 1, 4, t);
     }
 
+    __device__ __forceinline__ void advance(uint32_t n) {
+#pragma unroll
+        for (int i = 0; i < NR; ++i) T::advance(at[i], n);
+    }
+
+    // Starts the stream at chunk 0 of `rows`.
     __device__ __forceinline__ void prime(const typename T::Row (&rows)[NR], uint32_t c_end) {
         const uint32_t last = c_end - 1;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) at[i] = rows[i];
 #pragma unroll
         for (int p = 0; p < PF; ++p) {
             const uint32_t c = static_cast<uint32_t>(p) < last ? static_cast<uint32_t>(p) : last;
 #pragma unroll
-            for (int i = 0; i < NR; ++i) buf[p][i] = T::load(rows[i], c);
+            for (int i = 0; i < NR; ++i) buf[p][i] = T::load(at[i], c);
         }
     }
 
-    __device__ __forceinline__ void run(const typename T::Row (&rows)[NR], uint32_t c0, uint32_t c1,
-                                        uint32_t c_end, uint32_t blocks, uint32_t tile_b0,
-                                        uint32_t nb_tile, const float *lds, uint32_t l, float (&t)[NR]) {
+    // Chunks [c0, c1) against the LDS tile that starts at block tile_b0; c0
+    // is the stream's position.
+    __device__ __forceinline__ void run(uint32_t c0, uint32_t c1, uint32_t c_end, uint32_t blocks,
+                                        uint32_t tile_b0, uint32_t nb_tile, const float *lds, uint32_t l,
+                                        float (&t)[NR]) {
         const uint32_t full_end = blocks / T::kPerChunk; // chunks [0, full_end) hold kPerChunk blocks
         const uint32_t last = c_end - 1;
         const uint32_t cf = c1 < full_end ? c1 : full_end;
@@ -482,22 +514,21 @@ struct ChunkStream {
 #pragma unroll
                         for (int p = 0; p < kSlots; ++p) {
                             const uint32_t cc = c + u * kSlots + p;
-                            const uint32_t nxt = cc + PF < last ? cc + PF : last;
                             const uint32_t cn = cc + 1 < cf ? cc + 1 : cc;
-                            pipe_step(rows, buf[p], buf[(p + PF) % kSlots], nxt, cc, cn, lds, nb_tile, tile_b0, l,
-                                      t, xa, xb);
+                            pipe_step(buf[p], buf[(p + PF) % kSlots], u * kSlots + p + PF, cc, cn, lds, nb_tile,
+                                      tile_b0, l, t, xa, xb);
                         }
                     }
+                    advance(kSlots * U);
                 }
             for (; c + kSlots <= cf; c += kSlots) {
 #pragma unroll
                 for (int p = 0; p < kSlots; ++p) {
                     const uint32_t cc = c + p;
-                    const uint32_t nxt = cc + PF < last ? cc + PF : last;
                     const uint32_t cn = cc + 1 < cf ? cc + 1 : cc;
-                    pipe_step(rows, buf[p], buf[(p + PF) % kSlots], nxt, cc, cn, lds, nb_tile, tile_b0, l, t, xa,
-                              xb);
+                    pipe_step(buf[p], buf[(p + PF) % kSlots], p + PF, cc, cn, lds, nb_tile, tile_b0, l, t, xa, xb);
                 }
+                advance(kSlots);
             }
         }
         // steady state: U whole rings of full chunks per pass, one basic block
@@ -508,42 +539,45 @@ struct ChunkStream {
 #pragma unroll
                     for (int p = 0; p < kSlots; ++p) {
                         const uint32_t cc = c + u * kSlots + p;
-                        const uint32_t nxt = cc + PF < last ? cc + PF : last;
 #pragma unroll
-                        for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(rows[i], nxt);
+                        for (int i = 0; i < NR; ++i)
+                            buf[(p + PF) % kSlots][i] = T::load(at[i], u * kSlots + p + PF);
                         __builtin_amdgcn_sched_barrier(0);
                         T::template step<NR, true>(buf[p], lds, nb_tile, cc * T::kPerChunk - tile_b0,
                                                    T::kPerChunk, l, t);
                     }
                 }
+                advance(kSlots * U);
             }
         for (; !kPipe && c + kSlots <= cf; c += kSlots) {
 #pragma unroll
             for (int p = 0; p < kSlots; ++p) {
                 const uint32_t cc = c + p;
-                const uint32_t nxt = cc + PF < last ? cc + PF : last;
 #pragma unroll
-                for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(rows[i], nxt);
+                for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(at[i], p + PF);
                 // the scheduler would otherwise sink loads whose data is used
                 // late in a step down to that use, emptying the prefetch ring
                 __builtin_amdgcn_sched_barrier(0);
                 T::template step<NR, true>(buf[p], lds, nb_tile, cc * T::kPerChunk - tile_b0, T::kPerChunk, l, t);
             }
+            advance(kSlots);
         }
-        // the rest of the tile (fewer than kSlots chunks, the last may be partial)
+        // the rest of the tile (fewer than kSlots chunks, the last may be
+        // partial); its requests stop at the row's last chunk
 #pragma unroll
         for (int p = 0; p < kSlots; ++p) {
             const uint32_t cc = c + p;
             if (cc >= c1) break;
             const uint32_t nxt = cc + PF < last ? cc + PF : last;
 #pragma unroll
-            for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(rows[i], nxt);
+            for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(at[i], nxt - c);
             const uint32_t b = cc * T::kPerChunk;
             if (cc < full_end)
                 T::template step<NR, true>(buf[p], lds, nb_tile, b - tile_b0, T::kPerChunk, l, t);
             else
                 T::template step<NR, false>(buf[p], lds, nb_tile, b - tile_b0, blocks - b, l, t);
         }
+        if (c1 > c) advance(c1 - c);
     }
 };
 

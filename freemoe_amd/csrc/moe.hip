@@ -563,7 +563,7 @@ __device__ inline float swiglu(float gate, float up) {
 // Four wavefronts per SIMD (at most 128 VGPRs): the whole grid of a Mixtral
 // expert pair is then resident at once.
 template <class T, int RJ, int PF>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void gate_up_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4 / RJ))) void gate_up_kernel(
     ExpertArgs a, const float *__restrict__ h, const float *__restrict__ logits, uint32_t *__restrict__ ids,
     float *__restrict__ w, float *__restrict__ act, uint32_t *__restrict__ status) {
     extern __shared__ __align__(16) float lds[];
@@ -601,8 +601,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         if (tb == 0) T::template stage<4, true>(h, tb, nb, lds, tid, kThreads, hb);
         else T::stage(h, tb, nb, lds, tid, kThreads);
         __syncthreads();
-        cs.run(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, c_end, blocks, tb, nb, lds, l,
-               t);
+        cs.run(tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, c_end, blocks, tb, nb, lds, l, t);
     }
 #pragma unroll
     for (int m = 0; m < RJ; ++m) {
@@ -667,7 +666,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
                                       kThreads);
         }
         __syncthreads();
-        cs.run(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, c_end, blocks, tb, nb,
+        cs.run(tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, c_end, blocks, tb, nb,
                lds + rank * tile_floats, l, t);
     }
     const float v = T::finish(t[0]);

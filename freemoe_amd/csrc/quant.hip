@@ -32,6 +32,11 @@ int raw_geometry(uint32_t type_id, uint32_t *block_size, uint32_t *block_bytes) 
 //   Q4_K  A: [rows][S][16 B] header (d, dmin, 12 B scales) B: [rows][S][lane][16 B]
 //         lane l's bytes 4g+k = qs[32g + 8k + l] (group g, k = 0..3).
 //   F32   raw row-major, no packing.
+// Block-type layouts end with kPackedTail spare bytes: the decode streams
+// request up to 8 chunks (1 KiB) past a row's last chunk before they know the
+// row has ended, and the last row's requests must stay inside the allocation.
+constexpr uint64_t kPackedTail = 4096;
+
 int packed_geometry(uint32_t type_id, uint32_t rows, uint32_t cols, PackedGeometry *g) {
     uint32_t bs, bb;
     int rc = raw_geometry(type_id, &bs, &bb);
@@ -57,7 +62,7 @@ int packed_geometry(uint32_t type_id, uint32_t rows, uint32_t cols, PackedGeomet
         p.scale_row_bytes = static_cast<uint64_t>(p.blocks_padded) * 2;
         p.scale_bytes = align_up(p.scale_row_bytes * rows, 256);
         p.quant_bytes = static_cast<uint64_t>(rows) * p.chunks * 128;
-        p.total = p.scale_bytes + align_up(p.quant_bytes, 256);
+        p.total = p.scale_bytes + align_up(p.quant_bytes, 256) + kPackedTail;
         break;
     }
     case FMX_TYPE_Q4_K:
@@ -66,7 +71,7 @@ int packed_geometry(uint32_t type_id, uint32_t rows, uint32_t cols, PackedGeomet
         p.scale_row_bytes = static_cast<uint64_t>(p.blocks) * 16;
         p.scale_bytes = align_up(p.scale_row_bytes * rows, 256);
         p.quant_bytes = static_cast<uint64_t>(rows) * p.chunks * 128;
-        p.total = p.scale_bytes + align_up(p.quant_bytes, 256);
+        p.total = p.scale_bytes + align_up(p.quant_bytes, 256) + kPackedTail;
         break;
     }
     *g = p;

@@ -6,6 +6,8 @@ is a pure permutation of the raw GGUF bytes (unpack(pack(raw)) == raw).
 import numpy as np
 
 Q4_0, Q8_0, Q4_K, F32 = 2, 8, 12, 0
+# zero bytes after a block-type layout (room for the decode streams' prefetch)
+PACKED_TAIL = 4096
 
 
 def _align(v, a=256):
@@ -36,7 +38,7 @@ def pack(type_id: int, raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
                 for k in range(4):
                     lanes[:, :, l, k::4] = qs[:, :, :, 8 * k + l]
         sbytes = _align(rows * bp * 2)
-        out = np.zeros(sbytes + _align(lanes.size), np.uint8)
+        out = np.zeros(sbytes + _align(lanes.size) + PACKED_TAIL, np.uint8)
         out[:rows * bp * 2] = scales.reshape(-1)
         out[sbytes:sbytes + lanes.size] = lanes.reshape(-1)
         return out
@@ -47,7 +49,7 @@ def pack(type_id: int, raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
         qs = blk[:, :, 16:].reshape(rows, nb, 4, 4, 8)  # [g][k][l]
         lanes = np.transpose(qs, (0, 1, 4, 2, 3)).reshape(rows, nb, 8, 16)  # [l][g*4+k]
         sbytes = _align(rows * nb * 16)
-        out = np.zeros(sbytes + _align(lanes.size), np.uint8)
+        out = np.zeros(sbytes + _align(lanes.size) + PACKED_TAIL, np.uint8)
         out[:rows * nb * 16] = hdr.reshape(-1)
         out[sbytes:sbytes + lanes.size] = lanes.reshape(-1)
         return out

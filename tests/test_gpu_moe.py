@@ -119,6 +119,38 @@ def test_route_and_decode_at_rmsnorm_near_ties(gpu):
     assert check_layer(gpu, lw, x) == 0
 
 
+def large_value_layer(gain_log2, gate_scale_bits):
+    """A Q4_0 layer whose h (or act) holds values of 2^70 .. 2^106: element 5
+    of h is about 2^gain_log2 (its RMSNorm gain; x[:, 5] = 1 and the router
+    ignores it), and block 0 of every gate / up row has nibble 15 at element 5
+    with scale 2^-24 (gate: `gate_scale_bits`), so gate, up and act grow with
+    it while every value stays finite."""
+    lw = wl.make_layer(256, 256, 4, 2, wl.Q4_0, 41)
+    lw.norm_weight[5] = np.float32(2.0 ** gain_log2)
+    lw.router[:, 5] = 0.0
+    for mats, bits16 in ((lw.gate, gate_scale_bits), (lw.up, 0x0001)):
+        for m in mats:
+            m[:, 0:2] = np.frombuffer(np.uint16(bits16).tobytes(), np.uint8)
+            m[:, 2 + 5] = (m[:, 2 + 5] & 0xF0) | 0x0F
+    x = wl.inputs(256, 4, 42)
+    x[:, 5] = 1.0
+    return lw, x
+
+
+@pytest.mark.parametrize("case", ["h_beyond_2^100", "act_beyond_2^100"])
+def test_decode_large_values(gpu, case):
+    """Values of magnitude 2^100 and more in h (gate/up) or in act (down),
+    with every product and sum still finite: the layer must match the oracle
+    bit for bit there too."""
+    if case == "h_beyond_2^100":
+        lw, x = large_value_layer(101, 0x0000)  # gate ignores element 5
+    else:
+        lw, x = large_value_layer(74, 0x0001)   # act ~ 2^105
+    want_out = host_layer(lw).forward_batch(x)[0]
+    assert np.isfinite(want_out).all() and np.abs(want_out).max() > 2.0 ** 60
+    assert check_layer(gpu, lw, x) == 0
+
+
 def test_decode_reports_nonfinite_scores(gpu):
     import torch
     lw = wl.make_layer(64, 128, 4, 2, wl.F32, 3)
