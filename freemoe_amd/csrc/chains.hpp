@@ -17,7 +17,15 @@
 namespace fmx {
 
 // ------------------------------------------------------------- staging --
-// One batch of a staging pass: N float4 per thread, in flight together. A
+// Staging copies a tile of x into LDS as "quads": quad s holds the four x
+// values that one lane of one block consumes, elements q, q + 8, q + 16 and
+// q + 24 of the tile for q = T::quad_base(s), and goes to LDS as one 16-byte
+// write at float4 s. A thread gathers its quads with four 4-byte loads each
+// (the lanes of a wavefront still read whole 32-byte runs), so that
+// consecutive lanes write consecutive 16-byte slots: spreading a float4 of
+// consecutive elements over four slots instead put every lane of a wavefront
+// on the same 8 LDS banks.
+// One batch of a staging pass: N quads per thread, in flight together. A
 // kernel may load the first batch ahead, to request x before it knows what
 // else it needs.
 template <int N>
@@ -25,44 +33,35 @@ struct XBatch {
     float4 v[N];
 };
 
-template <int N>
+// Quads s0 + u * nthreads (u < N) of the tile of n elements at x + e0.
+template <class T, int N>
 __device__ __forceinline__ void load_batch(XBatch<N> &b, const float *__restrict__ x, uint32_t e0, uint32_t n,
-                                           uint32_t i0, uint32_t nthreads) {
-    const float4 *src = reinterpret_cast<const float4 *>(x + e0);
-    const uint32_t n4 = n / 4;
+                                           uint32_t s0, uint32_t nthreads) {
+    const float *src = x + e0;
+    const uint32_t nq = n / 4;
 #pragma unroll
     for (int u = 0; u < N; ++u) {
-        const uint32_t i = i0 + u * nthreads;
-        b.v[u] = src[i < n4 ? i : n4 - 1];
+        const uint32_t s = s0 + u * nthreads;
+        const uint32_t q = T::quad_base(s < nq ? s : nq - 1);
+        b.v[u] = make_float4(src[q], src[q + 8], src[q + 16], src[q + 24]);
     }
 }
 
-// Copies elements [e0, e0 + n) of x (n a multiple of 4, x + e0 16-byte
-// aligned) into LDS in a lane-major order: element i goes to float
-// slot(i) * 4 + (i % 32) / 8, where a slot (16 bytes) holds the four elements
-// of a 32-element run that lane i % 8 consumes. A thread's global loads go in
-// batches of N float4; consecutive elements land in consecutive lanes' slots,
-// kLaneSlots slots apart. kPre: `pre` holds the first batch, loaded by
-// load_batch(pre, x, e0, n, tid, nthreads).
-template <uint32_t kLaneSlots, int N, bool kPre, class Slot>
-__device__ __forceinline__ void scatter_lanes(const float *__restrict__ x, uint32_t e0, uint32_t n, float *lds,
-                                              uint32_t tid, uint32_t nthreads, Slot slot, const XBatch<N> &pre) {
-    const uint32_t n4 = n / 4;
-    for (uint32_t i0 = tid; i0 < n4; i0 += N * nthreads) {
+// Every quad of the tile of n elements (n a multiple of 32) at x + e0, in
+// batches of N per thread, handed to put(s, quad). kPre: `pre` holds the
+// first batch, loaded by load_batch<T>(pre, x, e0, n, tid, nthreads).
+template <class T, int N, bool kPre, class Put>
+__device__ __forceinline__ void gather_quads(const float *__restrict__ x, uint32_t e0, uint32_t n, uint32_t tid,
+                                             uint32_t nthreads, const XBatch<N> &pre, Put put) {
+    const uint32_t nq = n / 4;
+    for (uint32_t s0 = tid; s0 < nq; s0 += N * nthreads) {
         XBatch<N> b;
-        if (kPre && i0 == tid) b = pre;
-        else load_batch(b, x, e0, n, i0, nthreads);
+        if (kPre && s0 == tid) b = pre;
+        else load_batch<T>(b, x, e0, n, s0, nthreads);
 #pragma unroll
         for (int u = 0; u < N; ++u) {
-            const uint32_t i = i0 + u * nthreads;
-            if (i < n4) {
-                const uint32_t e = 4 * i;
-                float *d = lds + slot(e) * 4 + ((e & 31) >> 3);
-                d[0] = b.v[u].x;
-                d[4 * kLaneSlots] = b.v[u].y;
-                d[8 * kLaneSlots] = b.v[u].z;
-                d[12 * kLaneSlots] = b.v[u].w;
-            }
+            const uint32_t s = s0 + u * nthreads;
+            if (s < nq) put(s, b.v[u]);
         }
     }
 }
@@ -77,21 +76,21 @@ struct Q40 {
     static constexpr uint32_t kLdsFloatsPerBlock = 40;
 
     // Stage blocks [b0, b0 + nb) of x into lds (xs: nb*32 floats, s8: nb*8):
+    // Quad s = 8 b + l: block b, lane l.
+    __device__ static uint32_t quad_base(uint32_t s) { return (s >> 3) * 32 + (s & 7); }
+
     // xs[b][l] = (x[l], x[8+l], x[16+l], x[24+l]) of block b, then per (b, l)
     // 8 * ((x[l] + x[8+l]) + (x[16+l] + x[24+l])) (the scaling is exact). The
-    // caller's barrier after stage() publishes the sums.
+    // caller's barrier after stage() publishes the tile.
     template <int N = 8, bool kPre = false>
     __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds, uint32_t tid,
                                  uint32_t nthreads, const XBatch<N> &pre = XBatch<N>()) {
-        scatter_lanes<1, N, kPre>(x, b0 * 32, nb * 32, lds, tid, nthreads,
-                               [](uint32_t e) { return (e >> 5) * 8 + (e & 7); }, pre);
-        __syncthreads();
-        const float4 *xs = reinterpret_cast<const float4 *>(lds);
+        float4 *xs = reinterpret_cast<float4 *>(lds);
         float *s8 = lds + nb * 32;
-        for (uint32_t e = tid; e < nb * 8; e += nthreads) {
-            const float4 v = xs[e];
-            s8[e] = 8.0f * ((v.x + v.y) + (v.z + v.w));
-        }
+        gather_quads<Q40, N, kPre>(x, b0 * 32, nb * 32, tid, nthreads, pre, [&](uint32_t q, float4 v) {
+            xs[q] = v;
+            s8[q] = 8.0f * ((v.x + v.y) + (v.z + v.w));
+        });
     }
 
     // Row base pointers for this lane: scales of the row, and the lane's
@@ -212,13 +211,15 @@ struct Q80 {
     static constexpr uint32_t kPerChunk = 4;
     static constexpr uint32_t kLdsFloatsPerBlock = 32;
 
+    __device__ static uint32_t quad_base(uint32_t s) { return (s >> 3) * 32 + (s & 7); }
+
     // xs[b][l] = (x[l], x[8+l], x[16+l], x[24+l]) of block b.
     template <int N = 8, bool kPre = false>
     __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds, uint32_t tid,
                                  uint32_t nthreads, const XBatch<N> &pre = XBatch<N>()) {
-        scatter_lanes<1, N, kPre>(x, b0 * 32, nb * 32, lds, tid, nthreads,
-                               [](uint32_t e) { return (e >> 5) * 8 + (e & 7); }, pre);
-        __syncthreads();
+        float4 *xs = reinterpret_cast<float4 *>(lds);
+        gather_quads<Q80, N, kPre>(x, b0 * 32, nb * 32, tid, nthreads, pre,
+                                   [&](uint32_t q, float4 v) { xs[q] = v; });
     }
 
     struct Row {
@@ -290,6 +291,9 @@ struct Q4K {
     static constexpr uint32_t kPerChunk = 1;
     static constexpr uint32_t kLdsFloatsPerBlock = 264;
 
+    // Quad s = ((4 * super-block + group) * 8 + l) * 2 + half.
+    __device__ static uint32_t quad_base(uint32_t s) { return (s >> 4) * 64 + (s & 1) * 32 + ((s >> 1) & 7); }
+
     // Per super-block and group g: slots (g, l, half) hold x[64g + 32 half + 8k + l],
     // k = 0..3; then per (super-block, g) the low and high 32-element sums in
     // the reference's order (per-lane sums of four, then the 8-lane tree). The
@@ -297,10 +301,9 @@ struct Q4K {
     template <int N = 8, bool kPre = false>
     __device__ static void stage(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds, uint32_t tid,
                                  uint32_t nthreads, const XBatch<N> &pre = XBatch<N>()) {
-        // element e of the tile: super-block e/256, group (e%256)/64, half (e%64)/32
-        scatter_lanes<2, N, kPre>(
-            x, b0 * 256, nb * 256, lds, tid, nthreads,
-            [](uint32_t e) { return (((e >> 6) * 8 + (e & 7)) * 2) + ((e >> 5) & 1); }, pre);
+        float4 *xw = reinterpret_cast<float4 *>(lds);
+        gather_quads<Q4K, N, kPre>(x, b0 * 256, nb * 256, tid, nthreads, pre,
+                                   [&](uint32_t q, float4 v) { xw[q] = v; });
         __syncthreads();
         const float4 *xs = reinterpret_cast<const float4 *>(lds);
         float *sums = lds + nb * 256;

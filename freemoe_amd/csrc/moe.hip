@@ -572,7 +572,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4 / RJ
     const uint32_t blocks = a.gu.blocks;
     // h's first tile is requested before the routing, whose loads it overlaps
     XBatch<4> hb;
-    load_batch(hb, h, 0, (blocks < a.gu_tile ? blocks : a.gu_tile) * T::kBlock, tid, kThreads);
+    load_batch<T>(hb, h, 0, (blocks < a.gu_tile ? blocks : a.gu_tile) * T::kBlock, tid, kThreads);
     const uint32_t e = expert_of_rank(a.route, logits, ids, rank, blockIdx.x == 0 && rank == 0, ids, w, status);
     if (e >= a.experts) {
         if (tid == 0 && blockIdx.x == 0) atomicOr(status, STATUS_BAD_EXPERT);
@@ -648,19 +648,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const uint32_t c_end = (blocks + T::kPerChunk - 1) / T::kPerChunk;
     const uint32_t tile_floats = a.dn_tile * T::kLdsFloatsPerBlock;
     ChunkStream<T, 1, PF, down_rings<T>(), T::kType == FMX_TYPE_Q4_0> cs;
-    cs.prime(rw, c_end);
     for (uint32_t tb = 0; tb < blocks; tb += a.dn_tile) {
         const uint32_t nb = blocks - tb < a.dn_tile ? blocks - tb : a.dn_tile;
         __syncthreads();
         const uint32_t tile_elems = nb * T::kBlock;
         if (K == 2 && tile_elems <= 16 * 4 * kThreads) {
-            // both ranks' activations requested together: one memory latency
+            // both ranks' activations requested together: one memory latency;
+            // the first weight chunks after them, so that staging (which
+            // waits for its loads in the order they were issued) does not
+            // wait for the weights as well
             XBatch<16> b0, b1;
-            load_batch(b0, act, tb * T::kBlock, tile_elems, tid, kThreads);
-            load_batch(b1, act + a.ffn, tb * T::kBlock, tile_elems, tid, kThreads);
+            load_batch<T>(b0, act, tb * T::kBlock, tile_elems, tid, kThreads);
+            load_batch<T>(b1, act + a.ffn, tb * T::kBlock, tile_elems, tid, kThreads);
+            if (tb == 0) cs.prime(rw, c_end);
             T::template stage<16, true>(act, tb, nb, lds, tid, kThreads, b0);
             T::template stage<16, true>(act + a.ffn, tb, nb, lds + tile_floats, tid, kThreads, b1);
         } else {
+            if (tb == 0) cs.prime(rw, c_end);
             for (uint32_t r = 0; r < K; ++r)
                 T::template stage<16>(act + static_cast<uint64_t>(r) * a.ffn, tb, nb, lds + r * tile_floats, tid,
                                       kThreads);
