@@ -95,6 +95,15 @@ __device__ __forceinline__ float ubyte3(uint32_t v) {
 
 __device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
+// Bytes 2w and 2w + 1 of a dword read as OCP E4M3 fp8 values (one
+// v_cvt_pk_f32_fp8). A byte below 16 is the fp8 value byte * 2^-9 exactly.
+template <bool kHighWord>
+__device__ __forceinline__ float2 fp8_pair(uint32_t v) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 r = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(v), kHighWord);
+    return make_float2(r.x, r.y);
+}
+
 // Value held by lane (lane ^ mask), mask < 8, inside a wavefront.
 __device__ __forceinline__ float lane_xor(float v, int mask) {
     return __shfl_xor(v, mask, 64);
