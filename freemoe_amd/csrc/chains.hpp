@@ -154,6 +154,19 @@ struct Q40 {
         float4 xv[4];
         float sx8[4];
     };
+    // read_half for a full chunk whose first block sits `kb` blocks past the
+    // blocks xs0 / s80 point at (xs0 = tile's float4s + 8 b + l, s80 = tile's
+    // sums + 8 b + l for a base block b): with kb a compile-time constant the
+    // reads carry it as an instruction offset.
+    __device__ static void read_half_at(XHalf &xh, const float4 *xs0, const float *s80, uint32_t kb,
+                                        uint32_t half) {
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t j = kb + 4 * half + q;
+            xh.xv[q] = xs0[j * 8];
+            xh.sx8[q] = s80[j * 8];
+        }
+    }
     // Blocks 4 * half .. 4 * half + 3 of the chunk whose first block sits at
     // tile block tb0 (blocks past nblk read block 0 instead).
     __device__ static void read_half(XHalf &xh, const float *lds, uint32_t nb_tile, uint32_t tb0, uint32_t half,
@@ -509,21 +522,22 @@ struct ChunkStream {
     // not consumed yet)
     typename T::Row at[NR];
 
-    // One full chunk `cc` from `cur`, with `xa` holding its first half's x
-    // values on entry and the next chunk's (chunk cn) on return; first
-    // requests the chunk `rel` chunks past the stream position into `dst`.
+    // One full chunk from `cur`, with `xa` holding its first half's x values
+    // on entry and the next chunk's on return; first requests the chunk `rel`
+    // chunks past the stream position into `dst`. The chunk's and the next
+    // chunk's first blocks sit kb and kn blocks past the blocks xs0 / s80
+    // point at (read_half_at).
     template <bool kScaled, class XH>
     __device__ __forceinline__ void pipe_step(const typename T::Chunk (&cur)[NR], typename T::Chunk (&dst)[NR],
-                                              uint32_t rel, uint32_t cc, uint32_t cn, const float *lds,
-                                              uint32_t nb_tile, uint32_t tile_b0, uint32_t l, float (&t)[NR],
-                                              XH &xa, XH &xb) {
+                                              uint32_t rel, const float4 *xs0, const float *s80, uint32_t kb,
+                                              uint32_t kn, float (&t)[NR], XH &xa, XH &xb) {
 #pragma unroll
         for (int i = 0; i < NR; ++i) dst[i] = T::load(at[i], rel);
         __builtin_amdgcn_sched_barrier(0);
-        T::read_half(xb, lds, nb_tile, cc * T::kPerChunk - tile_b0, 1, l);
+        T::read_half_at(xb, xs0, s80, kb, 1);
         __builtin_amdgcn_sched_barrier(0);
         T::template compute_half<NR, true, kScaled>(cur, xa, 0, 4, t);
-        T::read_half(xa, lds, nb_tile, cn * T::kPerChunk - tile_b0, 0, l);
+        T::read_half_at(xa, xs0, s80, kn, 0);
         __builtin_amdgcn_sched_barrier(0);
         T::template compute_half<NR, true, kScaled>(cur, xb, 1, 4, t);
     }
@@ -560,26 +574,38 @@ struct ChunkStream {
         if constexpr (kPipe) {
             typename T::XHalf xa, xb;
             if (c + kSlots <= cf) T::read_half(xa, lds, nb_tile, c * T::kPerChunk - tile_b0, 0, l);
+            // LDS reads relative to the pass's first block; the pass's last
+            // chunk reads the next chunk's first half only when one follows
+            const float4 *xst = reinterpret_cast<const float4 *>(lds) + l;
+            const float *s8t = lds + nb_tile * 32 + l;
             if (U > 1)
                 for (; c + kSlots * U <= cf; c += kSlots * U) {
+                    const uint32_t b = c * T::kPerChunk - tile_b0;
+                    const float4 *xs0 = xst + b * 8;
+                    const float *s80 = s8t + b * 8;
+                    const uint32_t kend = c + kSlots * U < cf ? kSlots * U * T::kPerChunk : (kSlots * U - 1) * T::kPerChunk;
 #pragma unroll
                     for (int u = 0; u < U; ++u) {
 #pragma unroll
                         for (int p = 0; p < kSlots; ++p) {
-                            const uint32_t cc = c + u * kSlots + p;
-                            const uint32_t cn = cc + 1 < cf ? cc + 1 : cc;
-                            pipe_step<kScaled>(buf[p], buf[(p + PF) % kSlots], u * kSlots + p + PF, cc, cn, lds, nb_tile,
-                                      tile_b0, l, t, xa, xb);
+                            const uint32_t k = u * kSlots + p;
+                            const uint32_t kn = k + 1 < kSlots * U ? (k + 1) * T::kPerChunk : kend;
+                            pipe_step<kScaled>(buf[p], buf[(p + PF) % kSlots], k + PF, xs0, s80, k * T::kPerChunk, kn,
+                                               t, xa, xb);
                         }
                     }
                     advance(kSlots * U);
                 }
             for (; c + kSlots <= cf; c += kSlots) {
+                const uint32_t b = c * T::kPerChunk - tile_b0;
+                const float4 *xs0 = xst + b * 8;
+                const float *s80 = s8t + b * 8;
+                const uint32_t kend = c + kSlots < cf ? kSlots * T::kPerChunk : (kSlots - 1) * T::kPerChunk;
 #pragma unroll
                 for (int p = 0; p < kSlots; ++p) {
-                    const uint32_t cc = c + p;
-                    const uint32_t cn = cc + 1 < cf ? cc + 1 : cc;
-                    pipe_step<kScaled>(buf[p], buf[(p + PF) % kSlots], p + PF, cc, cn, lds, nb_tile, tile_b0, l, t, xa, xb);
+                    const uint32_t kn = p + 1 < kSlots ? (p + 1) * T::kPerChunk : kend;
+                    pipe_step<kScaled>(buf[p], buf[(p + PF) % kSlots], p + PF, xs0, s80, p * T::kPerChunk, kn, t, xa,
+                                       xb);
                 }
                 advance(kSlots);
             }
