@@ -191,18 +191,19 @@ struct GQ4K {
 
 // ------------------------------------------------------------ the GEMMs --
 //
-// One workgroup (4 wavefronts, one per SIMD) multiplies a row tile of one
-// expert (up to 192 token-expert pairs = 6 blocks of 32) by 128 weight
-// columns; wavefront w owns two 32-column blocks (gate/up: gate and up of the
-// same 32 ffn rows, so SwiGLU pairs meet in one lane; down: 64 rows).
+// One workgroup (8 wavefronts, two per SIMD, so one wavefront's dequantising
+// overlaps the other's MFMAs) multiplies a row tile of one expert (up to 192
+// token-expert pairs = 6 blocks of 32) by 128 (gate/up) or 256 (down) weight
+// columns; wavefront w owns one 32-column block (gate/up: wavefronts 0-3 the
+// gate rows, 4-7 the up rows of the same 128 ffn rows; down: 32 rows each).
 //
-// Weights never touch LDS: each lane loads its own two rows' packed bytes for
+// Weights never touch LDS: each lane loads its own row's packed bytes for
 // a K step (128 packed positions; lanes 0-31 take positions 0-63, lanes 32-63
 // positions 64-127) from HBM into registers, two steps ahead, and dequantises
 // 8 positions (one MFMA K slice) at a time as the B operand. Each weight byte
 // is read once per row tile, and a row tile holds all of an expert's pairs up
 // to 192. Activations: the tile's rows for the next step are loaded during
-// this one and stored to the other of two LDS buffers, where all four
+// this one and stored to the other of two LDS buffers, where all eight
 // wavefronts read their A operands.
 //
 // v_mfma_f32_32x32x16_bf16: A lane l = tile row 32 mb + l % 32, B lane l =
@@ -210,7 +211,8 @@ struct GQ4K {
 // may contract over K in any order, as long as A and B agree); C element r of
 // lane l = row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
 
-constexpr uint32_t kGThreads = 256;
+constexpr uint32_t kGThreads = 512;                           // 8 wavefronts, two per SIMD
+constexpr uint32_t kGStageRows = kPrefillTileRows / (kGThreads / 16); // tile rows a thread stages
 constexpr uint32_t kGBlocks = kPrefillTileRows / 32;         // 6 row blocks of 32
 constexpr uint32_t kGStepK = 128;                             // packed positions per K step
 constexpr uint32_t kGRowBytes = kGStepK * 2;                  // 256 bytes of a tile row
@@ -237,25 +239,27 @@ __device__ inline bool row_tile(const uint32_t *tiles, uint32_t mt, uint32_t exp
 // this thread's share of the next activation step, the accumulators of NMB
 // row blocks (the kernels instantiate one per possible block count, so no
 // MFMA sits under a branch).
-// Thread t stages granule t % 16 of tile rows t / 16 + 16 i (i < 12); the
+// Thread t stages granule t % 16 of tile rows t / 16 + 32 i (i < 6); the
 // activation matrix has at least 192 readable rows past every tile's first
 // row (the workspace pads it), and rows past the tile only feed output rows
 // that are never written.
 template <class T, uint32_t NMB>
 struct GemmWave {
-    typename T::WStep w[3][2];
-    uint4 xv[kPrefillTileRows / 16];
-    f32x16 acc[NMB][2];
+    static constexpr uint32_t kRowStride = kGThreads / 16; // tile rows between a thread's staged rows
+    typename T::WStep w[3];
+    uint4 xv[kGStageRows];
+    f32x16 acc[NMB];
 
     __device__ __forceinline__ void load_x(const __bf16 *src, uint64_t ld, uint32_t k0) {
 #pragma unroll
-        for (uint32_t i = 0; i < kPrefillTileRows / 16; ++i) xv[i] = ld16(src + static_cast<uint64_t>(16 * i) * ld + k0);
+        for (uint32_t i = 0; i < kGStageRows; ++i)
+            xv[i] = ld16(src + static_cast<uint64_t>(kRowStride * i) * ld + k0);
     }
     // st: byte address of this thread's granule in row t / 16 of the buffer
     __device__ __forceinline__ void store_x(char *st) const {
 #pragma unroll
-        for (uint32_t i = 0; i < kPrefillTileRows / 16; ++i)
-            *reinterpret_cast<uint4 *>(st + i * 16 * kGRowBytes) = xv[i];
+        for (uint32_t i = 0; i < kGStageRows; ++i)
+            *reinterpret_cast<uint4 *>(st + i * kRowStride * kGRowBytes) = xv[i];
     }
 
     // The MFMAs of one K step from ring slot `slot`; a_kk[kk]: byte address of
@@ -264,12 +268,11 @@ struct GemmWave {
     // operands (dequantised weights) of slice kk + 1 are prepared while the
     // MFMAs of slice kk run, so the VALU work overlaps the matrix unit.
     __device__ __forceinline__ void multiply(int slot, const char *const (&a_kk)[8]) {
-        bf16x8 av[2][NMB], bv[2][2];
+        bf16x8 av[2][NMB], bv[2];
 #pragma unroll
         for (uint32_t mb = 0; mb < NMB; ++mb)
             av[0][mb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(a_kk[0] + mb * 32 * kGRowBytes));
-        bv[0][0] = T::dequant_kk(w[slot][0], 0);
-        bv[0][1] = T::dequant_kk(w[slot][1], 0);
+        bv[0] = T::dequant_kk(w[slot], 0);
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
             const int c = kk & 1, n = c ^ 1;
@@ -278,14 +281,11 @@ struct GemmWave {
                 for (uint32_t mb = 0; mb < NMB; ++mb)
                     av[n][mb] = __builtin_bit_cast(
                         bf16x8, *reinterpret_cast<const uint4 *>(a_kk[kk + 1] + mb * 32 * kGRowBytes));
-                bv[n][0] = T::dequant_kk(w[slot][0], kk + 1);
-                bv[n][1] = T::dequant_kk(w[slot][1], kk + 1);
+                bv[n] = T::dequant_kk(w[slot], kk + 1);
             }
 #pragma unroll
-            for (uint32_t mb = 0; mb < NMB; ++mb) {
-                acc[mb][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[c][mb], bv[c][0], acc[mb][0], 0, 0, 0);
-                acc[mb][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[c][mb], bv[c][1], acc[mb][1], 0, 0, 0);
-            }
+            for (uint32_t mb = 0; mb < NMB; ++mb)
+                acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[c][mb], bv[c], acc[mb], 0, 0, 0);
         }
     }
 
@@ -293,11 +293,10 @@ struct GemmWave {
     // (ring slot `slot`, LDS buffer `buf`), stage the next step's activations
     // into the other buffer, request the activations of step `nx`.
     __device__ __forceinline__ void step(int slot, int slot_next, uint32_t buf, uint32_t nw, uint32_t nx,
-                                         const uint8_t *m0, uint32_t r0, const uint8_t *m1, uint32_t r1,
-                                         const PackedGeometry &g, const __bf16 *xsrc, uint64_t ldx, char *lds,
-                                         uint32_t aoff0, uint32_t stoff, uint32_t h) {
-        T::load_step(w[slot_next][0], m0, g, r0, nw, h);
-        T::load_step(w[slot_next][1], m1, g, r1, nw, h);
+                                         const uint8_t *m0, uint32_t r0, const PackedGeometry &g,
+                                         const __bf16 *xsrc, uint64_t ldx, char *lds, uint32_t aoff0, uint32_t stoff,
+                                         uint32_t h) {
+        T::load_step(w[slot_next], m0, g, r0, nw, h);
         __builtin_amdgcn_sched_barrier(0);
         const char *a_kk[8];
 #pragma unroll
@@ -308,10 +307,9 @@ struct GemmWave {
         __syncthreads();
     }
 
-    // K steps [s0, s0 + steps) against weight rows (m0, r0) and (m1, r1).
-    __device__ __forceinline__ void run(const uint8_t *m0, uint32_t r0, const uint8_t *m1, uint32_t r1,
-                                        const PackedGeometry &g, const __bf16 *xsrc, uint64_t ldx, uint32_t s0,
-                                        uint32_t steps, char *lds) {
+    // K steps [s0, s0 + steps) against weight row (m0, r0).
+    __device__ __forceinline__ void run(const uint8_t *m0, uint32_t r0, const PackedGeometry &g,
+                                        const __bf16 *xsrc, uint64_t ldx, uint32_t s0, uint32_t steps, char *lds) {
         const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
         const uint32_t last = s0 + steps - 1;
         // A operand of slice kk: row lane % 32 of the block, granule 8 h + kk
@@ -324,15 +322,12 @@ struct GemmWave {
 #pragma unroll
         for (uint32_t mb = 0; mb < NMB; ++mb)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[mb][j][i] = 0.0f;
+            for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
         // prologue: weights of steps s0, s0 + 1; activations of s0 into buffer 0
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
             const uint32_t st = s0 + p < last ? s0 + p : last;
-            T::load_step(w[p][0], m0, g, r0, st, h);
-            T::load_step(w[p][1], m1, g, r1, st, h);
+            T::load_step(w[p], m0, g, r0, st, h);
         }
         load_x(xsrc, ldx, s0 * kGStepK);
         store_x(lds + stoff);
@@ -345,7 +340,7 @@ struct GemmWave {
             for (int u = 0; u < 3; ++u) {
                 const uint32_t st = s0 + s + u;
                 const uint32_t nxt = st + 2 < last ? st + 2 : last;
-                step(u, (u + 2) % 3, (s + u) & 1, nxt, nxt, m0, r0, m1, r1, g, xsrc, ldx, lds, aoff0, stoff, h);
+                step(u, (u + 2) % 3, (s + u) & 1, nxt, nxt, m0, r0, g, xsrc, ldx, lds, aoff0, stoff, h);
             }
         }
         // the remaining steps (fewer than three)
@@ -354,7 +349,7 @@ struct GemmWave {
             if (s + u >= steps) break;
             const uint32_t st = s0 + s + u;
             const uint32_t nxt = st + 2 < last ? st + 2 : last;
-            step(u, (u + 2) % 3, (s + u) & 1, nxt, nxt, m0, r0, m1, r1, g, xsrc, ldx, lds, aoff0, stoff, h);
+            step(u, (u + 2) % 3, (s + u) & 1, nxt, nxt, m0, r0, g, xsrc, ldx, lds, aoff0, stoff, h);
         }
     }
 };
@@ -383,14 +378,29 @@ __global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ h
 // Gate and up of 128 ffn rows (32 per wavefront) for one row tile of NMB row
 // blocks, SwiGLU, and the activations written as bf16 in the down
 // projection's packed K order.
+// Wavefronts 0-3 take the gate rows, 4-7 the up rows of the same 128 ffn
+// rows; after the K loop the gate wavefronts hand their results through LDS
+// (the activation buffers, free by then) to the up wavefronts of the same
+// columns, which apply SwiGLU.
 template <class T, class TD, uint32_t NMB>
 __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, uint32_t row0, uint32_t rows,
                              const __bf16 *__restrict__ x, __bf16 *__restrict__ act, char *lds) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t f = blockIdx.y * 128 + 32 * wave + (lane & 31);
+    const uint32_t f = blockIdx.y * 128 + 32 * (wave & 3) + (lane & 31);
+    const bool is_up = wave >= 4;
     GemmWave<T, NMB> gw;
-    gw.run(static_cast<const uint8_t *>(a.gate[e]), f, static_cast<const uint8_t *>(a.up[e]), f, a.gu,
+    gw.run(static_cast<const uint8_t *>(is_up ? a.up[e] : a.gate[e]), f, a.gu,
            x + static_cast<uint64_t>(row0) * a.hidden, a.hidden, 0, a.hidden / kGStepK, lds);
+    // the K loop ended with a barrier after every wavefront's last LDS read
+    float *xc = reinterpret_cast<float *>(lds) + (wave & 3) * NMB * 16 * 64 + lane;
+    if (!is_up) {
+#pragma unroll
+        for (uint32_t mb = 0; mb < NMB; ++mb)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xc[(mb * 16 + r) * 64] = gw.acc[mb][r];
+    }
+    __syncthreads();
+    if (!is_up) return;
     const uint32_t F = a.ffn;
     const uint32_t col = f / TD::kChunkK * TD::kChunkK + TD::pos(f % TD::kChunkK);
 #pragma unroll
@@ -399,7 +409,7 @@ __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, ui
         for (int r = 0; r < 16; ++r) {
             const uint32_t m = 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (m >= rows) continue;
-            const float gv = gw.acc[mb][0][r], uv = gw.acc[mb][1][r];
+            const float gv = xc[(mb * 16 + r) * 64], uv = gw.acc[mb][r];
             act[static_cast<uint64_t>(row0 + m) * F + col] = static_cast<__bf16>(gv / (1.0f + expf(-gv)) * uv);
         }
     }
@@ -407,7 +417,7 @@ __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, ui
 
 // grid: (max row tiles, ffn / 128).
 template <class T, class TD>
-__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void gate_up_gemm_kernel(
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gate_up_gemm_kernel(
     ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, const __bf16 *__restrict__ x,
     __bf16 *__restrict__ act) {
     extern __shared__ __align__(16) char xlds[];
@@ -423,18 +433,17 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     }
 }
 
-// Down rows [256 blockIdx.y, +256) (64 per wavefront) for one row tile of NMB
+// Down rows [256 blockIdx.y, +256) (32 per wavefront) for one row tile of NMB
 // row blocks, over K steps [blockIdx.z * steps, +steps), into D[blockIdx.z]
 // [pairs x hidden] f32.
 template <class T, uint32_t NMB>
 __device__ __forceinline__ void down_tile(const ExpertArgs &a, uint32_t e, uint32_t row0, uint32_t rows, uint32_t pairs,
                           const __bf16 *__restrict__ act, uint32_t steps, float *__restrict__ dn, char *lds) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t n = blockIdx.y * 256 + 64 * wave + (lane & 31);
+    const uint32_t n = blockIdx.y * 256 + 32 * wave + (lane & 31);
     const uint8_t *wd = static_cast<const uint8_t *>(a.down[e]);
     GemmWave<T, NMB> gw;
-    gw.run(wd, n, wd, n + 32, a.dn, act + static_cast<uint64_t>(row0) * a.ffn, a.ffn, blockIdx.z * steps, steps,
-           lds);
+    gw.run(wd, n, a.dn, act + static_cast<uint64_t>(row0) * a.ffn, a.ffn, blockIdx.z * steps, steps, lds);
     const uint32_t H = a.hidden;
     float *dst = dn + static_cast<uint64_t>(blockIdx.z) * pairs * H;
 #pragma unroll
@@ -443,16 +452,14 @@ __device__ __forceinline__ void down_tile(const ExpertArgs &a, uint32_t e, uint3
         for (int r = 0; r < 16; ++r) {
             const uint32_t m = 32 * mb + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
             if (m >= rows) continue;
-            float *o = dst + static_cast<uint64_t>(row0 + m) * H + n;
-            o[0] = gw.acc[mb][0][r];
-            o[32] = gw.acc[mb][1][r];
+            dst[static_cast<uint64_t>(row0 + m) * H + n] = gw.acc[mb][r];
         }
     }
 }
 
 // grid: (max row tiles, hidden / 256, K splits).
 template <class T>
-__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void down_gemm_kernel(
+__global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void down_gemm_kernel(
     ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, const __bf16 *__restrict__ act,
     uint32_t steps, float *__restrict__ dn) {
     extern __shared__ __align__(16) char xlds[];
