@@ -31,6 +31,7 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     uint32_t *count = sm;                  // [E]
     uint32_t *base = count + E;            // [E]
     uint32_t *mask = base + E;             // [E][kWords]
+    uint32_t *below = mask + E * kWords;   // [E][kWords]: chosen tokens in the expert's earlier words
     __shared__ uint32_t bad;
     const uint32_t tid = threadIdx.x;
     if (tid == 0) bad = 0;
@@ -50,25 +51,49 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
         }
         return;
     }
-    // exclusive prefix sum over experts (E <= kBucketThreads), one lane;
-    // with `tiles`, also the list of row tiles (expert, first row, rows) of
-    // at most tile_rows rows each, experts ascending: tiles[0] = count, then
-    // 3 words per tile
-    if (tid == 0) {
-        uint32_t run = 0, nt = 0;
-        for (uint32_t e = 0; e < E; ++e) {
+    // exclusive prefix sums over experts (E <= kBucketMaxExperts), one
+    // wavefront, kPerLane consecutive experts per lane: entry offsets and,
+    // with `tiles`, the list of row tiles (expert, first row, rows) of at most
+    // tile_rows rows each, experts ascending: tiles[0] = count, then 3 words
+    // per tile
+    if (tid < 64) {
+        constexpr uint32_t kPerLane = kBucketMaxExperts / 64;
+        uint32_t rows = 0, nts = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < kPerLane; ++j) {
+            const uint32_t e = tid * kPerLane + j;
+            const uint32_t c = e < E ? count[e] : 0;
+            rows += c;
+            if (tiles) nts += (c + tile_rows - 1) / tile_rows;
+        }
+        uint32_t rincl = rows, tincl = nts;
+#pragma unroll
+        for (uint32_t d = 1; d < 64; d <<= 1) {
+            const uint32_t rv = __shfl_up(rincl, d), tv = __shfl_up(tincl, d);
+            if (tid >= d) {
+                rincl += rv;
+                tincl += tv;
+            }
+        }
+        uint32_t run = rincl - rows, nt = tincl - nts;
+        for (uint32_t j = 0; j < kPerLane; ++j) {
+            const uint32_t e = tid * kPerLane + j;
+            if (e >= E) break;
+            const uint32_t c = count[e];
             base[e] = run;
             offsets[e] = run;
             if (tiles)
-                for (uint32_t r = 0; r < count[e]; r += tile_rows, ++nt) {
+                for (uint32_t r = 0; r < c; r += tile_rows, ++nt) {
                     tiles[1 + 3 * nt] = e;
                     tiles[2 + 3 * nt] = run + r;
-                    tiles[3 + 3 * nt] = count[e] - r < tile_rows ? count[e] - r : tile_rows;
+                    tiles[3 + 3 * nt] = c - r < tile_rows ? c - r : tile_rows;
                 }
-            run += count[e];
+            run += c;
         }
-        offsets[E] = run;
-        if (tiles) tiles[0] = nt;
+        if (tid == 63) {
+            offsets[E] = rincl;
+            if (tiles) tiles[0] = tincl;
+        }
     }
     __syncthreads();
     for (uint32_t t0 = 0; t0 < tokens; t0 += kBucketThreads) {
@@ -82,24 +107,32 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
                 atomicOr(&mask[e * kWords + (tid >> 5)], 1u << (tid & 31));
             }
         __syncthreads();
+        // per expert, the exclusive prefix of its words' popcounts: one
+        // 32-lane half-wavefront per expert at a time (kWords = 32)
+        for (uint32_t i = tid; i < E * kWords; i += kBucketThreads) {
+            const uint32_t c = __builtin_popcount(mask[i]), q = i & (kWords - 1);
+            uint32_t incl = c;
+#pragma unroll
+            for (uint32_t d = 1; d < kWords; d <<= 1) {
+                const uint32_t v = __shfl_up(incl, d, kWords);
+                if (q >= d) incl += v;
+            }
+            below[i] = incl - c;
+        }
+        __syncthreads();
         if (live)
             for (uint32_t r = 0; r < K; ++r) {
                 const uint32_t e = ids[static_cast<uint64_t>(t) * K + r];
                 const uint32_t w = tid >> 5;
-                uint32_t before = 0;
-                for (uint32_t q = 0; q < w; ++q) before += __builtin_popcount(mask[e * kWords + q]);
-                const uint32_t below = mask[e * kWords + w] & ((1u << (tid & 31)) - 1u);
-                const uint32_t pos = base[e] + before + __builtin_popcount(below);
+                const uint32_t lower = mask[e * kWords + w] & ((1u << (tid & 31)) - 1u);
+                const uint32_t pos = base[e] + below[e * kWords + w] + __builtin_popcount(lower);
                 token_list[pos] = t;
                 rank_list[pos] = r;
                 if (slot_of) slot_of[static_cast<uint64_t>(t) * K + r] = pos;
             }
         __syncthreads();
-        for (uint32_t i = tid; i < E; i += kBucketThreads) {
-            uint32_t chosen = 0;
-            for (uint32_t q = 0; q < kWords; ++q) chosen += __builtin_popcount(mask[i * kWords + q]);
-            base[i] += chosen;
-        }
+        for (uint32_t i = tid; i < E; i += kBucketThreads)
+            base[i] += below[i * kWords + kWords - 1] + __builtin_popcount(mask[i * kWords + kWords - 1]);
         __syncthreads();
     }
 }
@@ -107,13 +140,14 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
 } // namespace
 
 size_t bucket_lds_bytes(uint32_t experts) {
-    return (2ull * experts + static_cast<uint64_t>(experts) * kWords) * sizeof(uint32_t);
+    return (2ull * experts + 2ull * experts * kWords) * sizeof(uint32_t);
 }
 
 int launch_bucket(const uint32_t *ids, uint32_t tokens, uint32_t K, uint32_t E, uint32_t *offsets,
                   uint32_t *token_list, uint32_t *rank_list, uint32_t *slot_of, uint32_t *status,
                   hipStream_t s, uint32_t *tiles, uint32_t tile_rows) {
     if (tiles && tile_rows == 0) return FMX_ERR_INVALID_ARGUMENT;
+    if (int rc = allow_lds(reinterpret_cast<const void *>(bucket_kernel), bucket_lds_bytes(E))) return rc;
     hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(kBucketThreads), bucket_lds_bytes(E), s, ids, tokens, K,
                        E, offsets, token_list, rank_list, slot_of, status, tiles, tile_rows);
     FMX_LAUNCH_CHECK();
