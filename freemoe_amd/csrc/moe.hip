@@ -34,6 +34,10 @@ namespace fmx {
 namespace {
 
 constexpr uint32_t kMaxHidden = 16384; // hidden sizes the routing kernels accept
+// Code alignment of the decode kernels: each starts on its own 4 KiB
+// boundary, so that where their loops fall in the instruction cache does not
+// move with the size of the kernels placed before them.
+constexpr int kHotAlign = 4096;
 // Dynamic LDS these kernels request at most: a gfx950 workgroup may hold
 // 160 KiB, of which 1 KiB is left for the kernels' static LDS.
 constexpr size_t kMaxLds = 159 * 1024;
@@ -196,9 +200,12 @@ __device__ Routing wave_route(const RouteArgs &a, const float *__restrict__ logi
 // farther from a float rounding boundary than the worst-case difference
 // between the two sums can move it; only when one is that close does one lane
 // redo the sum in the reference's order, from a copy of x in `scratch` (LDS,
-// at least hidden floats, 16-byte aligned). Either way hv is the reference's h
-// bit for bit. Every thread of the workgroup calls it; it ends after a barrier.
-template <uint32_t NT, uint32_t P>
+// at least hidden floats, 16-byte aligned), or with kSquares from the squares
+// (exact in double) written there (at least 2 hidden floats), the one lane
+// then running nothing but the chain of adds. Either way hv is the
+// reference's h bit for bit. Every thread of the workgroup calls it; it ends
+// after a barrier.
+template <uint32_t NT, uint32_t P, bool kSquares = false>
 __device__ __forceinline__ void token_rmsnorm(const RouteArgs &a, const float4 (&xv)[P], const float4 (&gv)[P],
                                               bool has_gain, float (&hv)[4 * P], float *scratch) {
     __shared__ double wave_part[NT / 64];
@@ -245,6 +252,56 @@ __device__ __forceinline__ void token_rmsnorm(const RouteArgs &a, const float4 (
         if (__any(unsafe) && (tid & 63) == 0) unsafe_s = 1;
         __syncthreads();
         if (!unsafe_s) break;
+        if (kSquares) {
+            // every thread writes its squares into LDS, then one lane adds
+            // them in order, its operands requested one batch (16 adds) ahead
+            double2 *tl = reinterpret_cast<double2 *>(scratch);
+#pragma unroll
+            for (uint32_t i = 0; i < P; ++i) {
+                const uint32_t q = tid + i * NT;
+                if (q < H4) {
+                    tl[2 * q] = make_double2(static_cast<double>(xv[i].x) * static_cast<double>(xv[i].x),
+                                             static_cast<double>(xv[i].y) * static_cast<double>(xv[i].y));
+                    tl[2 * q + 1] = make_double2(static_cast<double>(xv[i].z) * static_cast<double>(xv[i].z),
+                                                 static_cast<double>(xv[i].w) * static_cast<double>(xv[i].w));
+                }
+            }
+            __syncthreads();
+            if (tid == 0) {
+                constexpr uint32_t kB = 8; // double2 per batch
+                const uint32_t n2 = 2 * H4, nb = n2 / kB;
+                double2 buf[2][kB];
+                double s = 0.0;
+                if (nb > 0) {
+#pragma unroll
+                    for (uint32_t q = 0; q < kB; ++q) buf[0][q] = tl[q];
+                }
+                for (uint32_t bi = 0; bi < nb; bi += 2) {
+#pragma unroll
+                    for (uint32_t half = 0; half < 2; ++half) {
+                        const uint32_t b = bi + half;
+                        if (b >= nb) break;
+                        const uint32_t nx = (b + 1 < nb ? b + 1 : b) * kB;
+#pragma unroll
+                        for (uint32_t q = 0; q < kB; ++q) buf[half ^ 1][q] = tl[nx + q];
+#pragma unroll
+                        for (uint32_t q = 0; q < kB; ++q) {
+                            s += buf[half][q].x;
+                            s += buf[half][q].y;
+                        }
+                    }
+                }
+                for (uint32_t q = nb * kB; q < n2; ++q) {
+                    const double2 v = tl[q];
+                    s += v.x;
+                    s += v.y;
+                }
+                ss_s = s;
+            }
+            __syncthreads();
+            ss = ss_s;
+            continue;
+        }
         // the reference's order: x into LDS, one lane sums it
         float4 *xl = reinterpret_cast<float4 *>(scratch);
 #pragma unroll
@@ -291,7 +348,7 @@ __host__ __device__ inline uint32_t route_chain_stride(uint32_t hidden) {
 // does one lane redo the sum in the reference's order. Either way h is the
 // reference's h bit for bit.
 template <uint32_t NT>
-__global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float *__restrict__ x,
+__global__ __launch_bounds__(NT) __attribute__((aligned(kHotAlign))) void route_rows_kernel(RouteArgs a, const float *__restrict__ x,
                                                         float *__restrict__ h_out, float *__restrict__ logits) {
     constexpr uint32_t P = 4;
     extern __shared__ __align__(16) float lds[];
@@ -388,7 +445,7 @@ __global__ __launch_bounds__(NT) void route_rows_kernel(RouteArgs a, const float
 }
 
 // RMSNorm of token blockIdx.x into h (batched routing). NT threads, 4 float4
-// per thread (hidden <= 16 NT); LDS: hidden floats for the in-order fallback.
+// per thread (hidden <= 16 NT); LDS: 2 hidden floats for the in-order fallback.
 template <uint32_t NT>
 __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *__restrict__ x,
                                                      float *__restrict__ h) {
@@ -406,7 +463,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *_
         gv[i] = g4 ? g4[qc] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
     }
     float hv[4 * P];
-    token_rmsnorm<NT, P>(a, xv, gv, g4 != nullptr, hv, lds);
+    token_rmsnorm<NT, P, true>(a, xv, gv, g4 != nullptr, hv, lds);
     float4 *h4 = reinterpret_cast<float4 *>(h + static_cast<uint64_t>(t) * H);
 #pragma unroll
     for (uint32_t i = 0; i < P; ++i) {
@@ -563,7 +620,7 @@ __device__ inline float swiglu(float gate, float up) {
 // Four wavefronts per SIMD (at most 128 VGPRs): the whole grid of a Mixtral
 // expert pair is then resident at once.
 template <class T, int RJ, int PF>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4 / RJ))) void gate_up_kernel(
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4 / RJ), aligned(kHotAlign))) void gate_up_kernel(
     ExpertArgs a, const float *__restrict__ h, const float *__restrict__ logits, uint32_t *__restrict__ ids,
     float *__restrict__ w, float *__restrict__ act, uint32_t *__restrict__ status) {
     extern __shared__ __align__(16) float lds[];
@@ -620,7 +677,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4 / RJ
 // runs per CU: the wavefront may use every register, which holds a deep
 // prefetch ring.
 template <class T, int PF>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void down_kernel(ExpertArgs a, const float *__restrict__ x,
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1), aligned(kHotAlign))) void down_kernel(ExpertArgs a, const float *__restrict__ x,
                                                         const float *__restrict__ act,
                                                         const uint32_t *__restrict__ ids,
                                                         const float *__restrict__ w,
@@ -839,7 +896,7 @@ int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, flo
 int launch_route_batched(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                          hipStream_t s) {
     if (a.hidden > kMaxHidden || a.hidden % 4 || a.experts == 0) return FMX_ERR_SHAPE_MISMATCH;
-    const size_t lds = static_cast<size_t>(a.hidden) * sizeof(float);
+    const size_t lds = 2ull * a.hidden * sizeof(float);
     if (a.hidden <= 16 * 256) {
         auto k = rmsnorm_kernel<256>;
         if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
