@@ -212,7 +212,6 @@ struct GQ4K {
 // lane l = row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
 
 constexpr uint32_t kGThreads = 512;                           // 8 wavefronts, two per SIMD
-constexpr uint32_t kGStageRows = kPrefillTileRows / (kGThreads / 16); // tile rows a thread stages
 constexpr uint32_t kGBlocks = kPrefillTileRows / 32;         // 6 row blocks of 32
 constexpr uint32_t kGStepK = 128;                             // packed positions per K step
 constexpr uint32_t kGRowBytes = kGStepK * 2;                  // 256 bytes of a tile row
@@ -239,26 +238,29 @@ __device__ inline bool row_tile(const uint32_t *tiles, uint32_t mt, uint32_t exp
 // this thread's share of the next activation step, the accumulators of NMB
 // row blocks (the kernels instantiate one per possible block count, so no
 // MFMA sits under a branch).
-// Thread t stages granule t % 16 of tile rows t / 16 + 32 i (i < 6); the
+// Thread t stages granule t % 16 of tile rows t / 16 + 32 i (i < NMB); the
 // activation matrix has at least 192 readable rows past every tile's first
-// row (the workspace pads it), and rows past the tile only feed output rows
-// that are never written.
+// row (the workspace pads it), and rows past the tile (up to 32 NMB) only
+// feed output rows that are never written.
 template <class T, uint32_t NMB>
 struct GemmWave {
     static constexpr uint32_t kRowStride = kGThreads / 16; // tile rows between a thread's staged rows
     typename T::WStep w[3];
-    uint4 xv[kGStageRows];
+    uint4 xv[NMB];
     f32x16 acc[NMB];
 
+    // rows of the tile's NMB row blocks only (kRowStride = 32: one row per
+    // block)
+    static_assert(kRowStride == 32, "one staged row per row block");
     __device__ __forceinline__ void load_x(const __bf16 *src, uint64_t ld, uint32_t k0) {
 #pragma unroll
-        for (uint32_t i = 0; i < kGStageRows; ++i)
+        for (uint32_t i = 0; i < NMB; ++i)
             xv[i] = ld16(src + static_cast<uint64_t>(kRowStride * i) * ld + k0);
     }
     // st: byte address of this thread's granule in row t / 16 of the buffer
     __device__ __forceinline__ void store_x(char *st) const {
 #pragma unroll
-        for (uint32_t i = 0; i < kGStageRows; ++i)
+        for (uint32_t i = 0; i < NMB; ++i)
             *reinterpret_cast<uint4 *>(st + i * kRowStride * kGRowBytes) = xv[i];
     }
 
