@@ -479,23 +479,27 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 
 // out[t] = x[t] + ((0 + w_0 D_0) + w_1 D_1 ...) in rank order (engine.cpp:1517,
 // 1770, 813-816), each D the sum of the K splits' partial products in split
-// order. grid: (ceil(hidden / 256), tokens).
+// order. V consecutive elements per thread (hidden % V == 0, x and out
+// V-float aligned). grid: (ceil(hidden / (256 V)), tokens).
+template <uint32_t V>
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ x, const float *__restrict__ dn,
                                                       uint32_t splits, uint64_t split_stride,
                                                       const uint32_t *__restrict__ slot_of,
                                                       const float *__restrict__ w, uint32_t hidden, uint32_t K,
                                                       float *__restrict__ out) {
-    const uint32_t t = blockIdx.y, j = blockIdx.x * 256 + threadIdx.x;
+    typedef float fv __attribute__((ext_vector_type(V)));
+    const uint32_t t = blockIdx.y, j = (blockIdx.x * 256 + threadIdx.x) * V;
     if (j >= hidden) return;
-    float ffn = 0.0f;
+    fv ffn = 0.0f;
     for (uint32_t r = 0; r < K; ++r) {
         const uint64_t i = static_cast<uint64_t>(t) * K + r;
         const float *d = dn + static_cast<uint64_t>(slot_of[i]) * hidden + j;
-        float v = d[0];
-        for (uint32_t sp = 1; sp < splits; ++sp) v += d[sp * split_stride];
+        fv v = *reinterpret_cast<const fv *>(d);
+        for (uint32_t sp = 1; sp < splits; ++sp) v += *reinterpret_cast<const fv *>(d + sp * split_stride);
         ffn = ffn + w[i] * v;
     }
-    out[static_cast<uint64_t>(t) * hidden + j] = x[static_cast<uint64_t>(t) * hidden + j] + ffn;
+    const uint64_t o = static_cast<uint64_t>(t) * hidden + j;
+    *reinterpret_cast<fv *>(out + o) = *reinterpret_cast<const fv *>(x + o) + ffn;
 }
 
 // ---------------------------------------------------------------- launchers --
@@ -581,8 +585,13 @@ uint32_t prefill_down_splits(uint32_t experts, uint32_t ffn) {
 
 int launch_combine(const float *x, const float *dn, uint32_t splits, uint32_t pairs, const uint32_t *slot_of,
                    const float *w, uint32_t hidden, uint32_t K, uint32_t tokens, float *out, hipStream_t s) {
-    hipLaunchKernelGGL(combine_kernel, dim3(div_up(hidden, 256), tokens), dim3(256), 0, s, x, dn, splits,
-                       static_cast<uint64_t>(pairs) * hidden, slot_of, w, hidden, K, out);
+    const uint64_t stride = static_cast<uint64_t>(pairs) * hidden;
+    if (hidden % 4 == 0 && (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) % 16 == 0)
+        hipLaunchKernelGGL(combine_kernel<4>, dim3(div_up(hidden, 1024), tokens), dim3(256), 0, s, x, dn, splits,
+                           stride, slot_of, w, hidden, K, out);
+    else
+        hipLaunchKernelGGL(combine_kernel<1>, dim3(div_up(hidden, 256), tokens), dim3(256), 0, s, x, dn, splits,
+                           stride, slot_of, w, hidden, K, out);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
