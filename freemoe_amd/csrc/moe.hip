@@ -472,56 +472,67 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *_
     }
 }
 
-// Router logits of 16 tokens x 16 router rows per workgroup (batched
-// routing): every (token, row) pair runs the 16 FMA chains of the reference's
-// gemv_avx2_row order (chain c takes elements 16 s + c, s = 0, 1, ...), lane c
-// of a 16-lane group owning chain c of a 4 x 4 block of pairs (16 independent
-// chains per lane). h and the router rows pass through LDS 256 elements (16
-// steps of every chain) at a time, the next tile requested during this one's
-// FMAs; then the lane tree, the sequential tail and the logit bias, as in
-// f32_row_chains. grid: (ceil(tokens / 16), ceil(experts / 16)).
+// Router logits of a tile of TT = GT PT tokens x TR = (16 / GT) PR router
+// rows per workgroup (batched routing): every (token, row) pair runs the 16
+// FMA chains of the reference's gemv_avx2_row order (chain c takes elements
+// 16 s + c, s = 0, 1, ...), lane c of a 16-lane group owning chain c of a
+// PT x PR block of pairs (PT PR independent chains per lane). h and the
+// router rows pass through LDS 256 elements (16 steps of every chain) at a
+// time, the next tile requested during this one's FMAs; then the lane tree,
+// the sequential tail and the logit bias, as in f32_row_chains. Few experts
+// take small tiles (2 tokens x 8 or 16 rows) so that the grid still covers
+// the device; many take 16 x 16. grid: (ceil(tokens / TT), ceil(experts / TR)).
 constexpr uint32_t kRtPad = 20; // floats per (token or row, chain) in LDS: 16 steps + 4
+template <uint32_t PT, uint32_t PR, uint32_t GT>
 __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const float *__restrict__ h,
                                                           uint32_t tokens, float *__restrict__ logits) {
-    __shared__ __align__(16) float hl[16][16][kRtPad];
-    __shared__ __align__(16) float wl[16][16][kRtPad];
+    constexpr uint32_t GR = 16 / GT, TT = GT * PT, TR = GR * PR;
+    __shared__ __align__(16) float hl[TT][16][kRtPad];
+    __shared__ __align__(16) float wl[TR][16][kRtPad];
     const uint32_t H = a.hidden, E = a.experts, tid = threadIdx.x;
     const uint32_t c = tid & 15, g = tid >> 4;
-    const uint32_t tg = (g & 3) * 4, rg = (g >> 2) * 4;
-    const uint32_t t0 = blockIdx.x * 16, r0 = blockIdx.y * 16;
+    const uint32_t tg = (g % GT) * PT, rg = (g / GT) * PR;
+    const uint32_t t0 = blockIdx.x * TT, r0 = blockIdx.y * TR;
     const uint32_t S = H / 16, n16 = S * 16, ntiles = (S + 15) / 16;
-    // staging: thread -> token / row tid / 16, float4 q = tid % 16 + 16 i of the tile
-    const uint32_t st = tid >> 4, sq = tid & 15;
-    const float *hsrc = h + static_cast<uint64_t>(t0 + st < tokens ? t0 + st : tokens - 1) * H;
-    const float *wsrc = a.router + static_cast<uint64_t>(r0 + st < E ? r0 + st : E - 1) * H;
-    float4 hv[4], wv[4];
+    // staging: the tile's TT + TR rows of 64 float4 each, item q = tid + 256 i
+    // -> row q / 64, float4 q % 64 of the row's 256 elements
+    constexpr uint32_t kItems = (TT + TR) * 64, kPer = (kItems + 255) / 256;
+    const float *src[kPer];
+#pragma unroll
+    for (uint32_t i = 0; i < kPer; ++i) {
+        const uint32_t q = tid + 256 * i, row = q / 64 < TT + TR ? q / 64 : 0;
+        src[i] = row < TT ? h + static_cast<uint64_t>(t0 + row < tokens ? t0 + row : tokens - 1) * H
+                          : a.router + static_cast<uint64_t>(r0 + row - TT < E ? r0 + row - TT : E - 1) * H;
+    }
+    float4 sv[kPer];
     auto load_tile = [&](uint32_t k) {
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t e = 256 * k + 4 * (sq + 16 * i);
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t q = tid + 256 * i;
+            if (kItems % 256 != 0 && q >= kItems) break;
+            const uint32_t e = 256 * k + 4 * (q % 64);
             const uint32_t ec = e + 4 <= n16 ? e : 0; // past the chains' elements: unused
-            hv[i] = *reinterpret_cast<const float4 *>(hsrc + ec);
-            wv[i] = *reinterpret_cast<const float4 *>(wsrc + ec);
+            sv[i] = *reinterpret_cast<const float4 *>(src[i] + ec);
         }
     };
     auto store_tile = [&]() {
 #pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t q = sq + 16 * i, s0 = q >> 2, c0 = 4 * (q & 3);
-            const float hh[4] = {hv[i].x, hv[i].y, hv[i].z, hv[i].w};
-            const float ww[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
-#pragma unroll
-            for (uint32_t j = 0; j < 4; ++j) {
-                hl[st][c0 + j][s0] = hh[j];
-                wl[st][c0 + j][s0] = ww[j];
-            }
+        for (uint32_t i = 0; i < kPer; ++i) {
+            const uint32_t q = tid + 256 * i;
+            if (kItems % 256 != 0 && q >= kItems) break;
+            const uint32_t row = q / 64, f = q % 64, s0 = f >> 2, c0 = 4 * (f & 3);
+            float(*dst)[kRtPad] = row < TT ? hl[row] : wl[row - TT];
+            dst[c0][s0] = sv[i].x;
+            dst[c0 + 1][s0] = sv[i].y;
+            dst[c0 + 2][s0] = sv[i].z;
+            dst[c0 + 3][s0] = sv[i].w;
         }
     };
-    float acc[4][4];
+    float acc[PT][PR];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (uint32_t i = 0; i < PT; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+        for (uint32_t j = 0; j < PR; ++j) acc[i][j] = 0.0f;
     if (ntiles > 0) load_tile(0);
     for (uint32_t k = 0; k < ntiles; ++k) {
         store_tile();
@@ -529,21 +540,20 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
         if (k + 1 < ntiles) load_tile(k + 1);
         const uint32_t steps = S - 16 * k < 16 ? S - 16 * k : 16;
         for (uint32_t s4 = 0; s4 < steps; s4 += 4) {
-            float4 hq[4], wq[4];
+            float4 hq[PT], wq[PR];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                hq[i] = *reinterpret_cast<const float4 *>(&hl[tg + i][c][s4]);
-                wq[i] = *reinterpret_cast<const float4 *>(&wl[rg + i][c][s4]);
-            }
+            for (uint32_t i = 0; i < PT; ++i) hq[i] = *reinterpret_cast<const float4 *>(&hl[tg + i][c][s4]);
+#pragma unroll
+            for (uint32_t j = 0; j < PR; ++j) wq[j] = *reinterpret_cast<const float4 *>(&wl[rg + j][c][s4]);
             const uint32_t ns = steps - s4 < 4 ? steps - s4 : 4;
 #pragma unroll
             for (uint32_t u = 0; u < 4; ++u) {
                 if (u >= ns) break;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
+                for (uint32_t i = 0; i < PT; ++i) {
                     const float hu = u == 0 ? hq[i].x : u == 1 ? hq[i].y : u == 2 ? hq[i].z : hq[i].w;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
+                    for (uint32_t j = 0; j < PR; ++j) {
                         const float wu = u == 0 ? wq[j].x : u == 1 ? wq[j].y : u == 2 ? wq[j].z : wq[j].w;
                         acc[i][j] = fma_rn(wu, hu, acc[i][j]);
                     }
@@ -554,11 +564,11 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
     }
     const bool tail8 = H - n16 >= 8;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (uint32_t i = 0; i < PT; ++i) {
         const uint32_t t = t0 + tg + i;
         const float *hr = h + static_cast<uint64_t>(t < tokens ? t : tokens - 1) * H;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (uint32_t j = 0; j < PR; ++j) {
             const uint32_t r = r0 + rg + j;
             const float *wr = a.router + static_cast<uint64_t>(r < E ? r : E - 1) * H;
             float v = acc[i][j];
@@ -907,8 +917,15 @@ int launch_route_batched(const RouteArgs &a, const float *x, uint32_t tokens, fl
         hipLaunchKernelGGL(k, dim3(tokens), dim3(1024), lds, s, a, x, h);
     }
     FMX_LAUNCH_CHECK();
-    hipLaunchKernelGGL(router_tile_kernel, dim3(div_up(tokens, 16), div_up(a.experts, 16)), dim3(256), 0, s, a, h,
-                       tokens, logits);
+    if (a.experts <= 8)
+        hipLaunchKernelGGL((router_tile_kernel<1, 1, 2>), dim3(div_up(tokens, 2), div_up(a.experts, 8)), dim3(256), 0,
+                           s, a, h, tokens, logits);
+    else if (a.experts <= 16)
+        hipLaunchKernelGGL((router_tile_kernel<1, 2, 2>), dim3(div_up(tokens, 2), div_up(a.experts, 16)), dim3(256), 0,
+                           s, a, h, tokens, logits);
+    else
+        hipLaunchKernelGGL((router_tile_kernel<4, 4, 4>), dim3(div_up(tokens, 16), div_up(a.experts, 16)), dim3(256),
+                           0, s, a, h, tokens, logits);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
