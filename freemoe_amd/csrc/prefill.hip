@@ -235,33 +235,44 @@ __device__ inline bool row_tile(const uint32_t *tiles, uint32_t mt, uint32_t exp
 }
 
 // One GEMM of a workgroup: weight steps in a ring of three register slots,
-// this thread's share of the next activation step, the accumulators of NMB
-// row blocks (the kernels instantiate one per possible block count, so no
-// MFMA sits under a branch).
+// this thread's share of the activation steps to come (kXBufs register
+// buffers), the accumulators of NMB row blocks (the kernels instantiate one
+// per possible block count, so no MFMA sits under a branch).
 // Thread t stages granule t % 16 of tile rows t / 16 + 32 i (i < NMB); the
 // activation matrix has at least 192 readable rows past every tile's first
 // row (the workspace pads it), and rows past the tile (up to 32 NMB) only
 // feed output rows that are never written.
+//
+// Request order and the in-order vector memory counter: step st requests the
+// weights of step st + 2 first and, at its end, the activations of step
+// st + 1 + kXBufs. Waiting for the activations that step st stores (those of
+// st + 1) also waits for everything requested before them; with two register
+// buffers those were requested two steps earlier and only weights up to step
+// st + 1 precede them, so the weights keep two steps in flight. With one
+// buffer (tiles of more than four row blocks, for the registers) the
+// activations have one step.
 template <class T, uint32_t NMB>
 struct GemmWave {
     static constexpr uint32_t kRowStride = kGThreads / 16; // tile rows between a thread's staged rows
+    static constexpr uint32_t kXBufs = NMB <= 4 ? 2 : 1;
+    static constexpr uint32_t kPass = 3 * kXBufs; // steps per pass: ring slots and buffers both turn
     typename T::WStep w[3];
-    uint4 xv[NMB];
+    uint4 xv[kXBufs][NMB];
     f32x16 acc[NMB];
 
     // rows of the tile's NMB row blocks only (kRowStride = 32: one row per
     // block)
     static_assert(kRowStride == 32, "one staged row per row block");
-    __device__ __forceinline__ void load_x(const __bf16 *src, uint64_t ld, uint32_t k0) {
+    __device__ __forceinline__ void load_x(uint32_t b, const __bf16 *src, uint64_t ld, uint32_t k0) {
 #pragma unroll
         for (uint32_t i = 0; i < NMB; ++i)
-            xv[i] = ld16(src + static_cast<uint64_t>(kRowStride * i) * ld + k0);
+            xv[b][i] = ld16(src + static_cast<uint64_t>(kRowStride * i) * ld + k0);
     }
     // st: byte address of this thread's granule in row t / 16 of the buffer
-    __device__ __forceinline__ void store_x(char *st) const {
+    __device__ __forceinline__ void store_x(uint32_t b, char *st) const {
 #pragma unroll
         for (uint32_t i = 0; i < NMB; ++i)
-            *reinterpret_cast<uint4 *>(st + i * kRowStride * kGRowBytes) = xv[i];
+            *reinterpret_cast<uint4 *>(st + i * kRowStride * kGRowBytes) = xv[b][i];
     }
 
     // The MFMAs of one K step from ring slot `slot`; a_kk[kk]: byte address of
@@ -293,9 +304,10 @@ struct GemmWave {
 
     // One step: request weights of step `nw` into `slot_next`, multiply step
     // (ring slot `slot`, LDS buffer `buf`), stage the next step's activations
-    // into the other buffer, request the activations of step `nx`.
-    __device__ __forceinline__ void step(int slot, int slot_next, uint32_t buf, uint32_t nw, uint32_t nx,
-                                         const uint8_t *m0, uint32_t r0, const PackedGeometry &g,
+    // (register buffer `xb`) into the other LDS buffer, request the
+    // activations of step `nx` into `xb`.
+    __device__ __forceinline__ void step(int slot, int slot_next, uint32_t buf, uint32_t xb, uint32_t nw,
+                                         uint32_t nx, const uint8_t *m0, uint32_t r0, const PackedGeometry &g,
                                          const __bf16 *xsrc, uint64_t ldx, char *lds, uint32_t aoff0, uint32_t stoff,
                                          uint32_t h) {
         T::load_step(w[slot_next], m0, g, r0, nw, h);
@@ -304,8 +316,8 @@ struct GemmWave {
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) a_kk[kk] = lds + buf * kGBufBytes + (aoff0 ^ (kk << 4));
         multiply(slot, a_kk);
-        store_x(lds + (buf ^ 1) * kGBufBytes + stoff);
-        load_x(xsrc, ldx, nx * kGStepK);
+        store_x(xb, lds + (buf ^ 1) * kGBufBytes + stoff);
+        load_x(xb, xsrc, ldx, nx * kGStepK);
         __syncthreads();
     }
 
@@ -314,6 +326,7 @@ struct GemmWave {
                                         const __bf16 *xsrc, uint64_t ldx, uint32_t s0, uint32_t steps, char *lds) {
         const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
         const uint32_t last = s0 + steps - 1;
+        auto clampk = [last](uint32_t k) { return k < last ? k : last; };
         // A operand of slice kk: row lane % 32 of the block, granule 8 h + kk
         const uint32_t ar = lane & 31;
         const uint32_t aoff0 = ar * kGRowBytes + (((8 * h) ^ xswz(ar)) << 4);
@@ -325,33 +338,35 @@ struct GemmWave {
         for (uint32_t mb = 0; mb < NMB; ++mb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
-        // prologue: weights of steps s0, s0 + 1; activations of s0 into buffer 0
+        // prologue: weights of steps s0, s0 + 1; activations of s0 into LDS
+        // buffer 0; those of s0 + 1 (.. s0 + kXBufs) into the register
+        // buffers (step s0 + i is held by buffer (i + kXBufs - 1) % kXBufs ...
+        // step i stores buffer (i + 1) % kXBufs)
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            const uint32_t st = s0 + p < last ? s0 + p : last;
-            T::load_step(w[p], m0, g, r0, st, h);
-        }
-        load_x(xsrc, ldx, s0 * kGStepK);
-        store_x(lds + stoff);
-        load_x(xsrc, ldx, (s0 + 1 < last ? s0 + 1 : last) * kGStepK);
+        for (int p = 0; p < 2; ++p) T::load_step(w[p], m0, g, r0, clampk(s0 + p), h);
+        load_x(0, xsrc, ldx, s0 * kGStepK);
+        store_x(0, lds + stoff);
+#pragma unroll
+        for (uint32_t b = 1; b <= kXBufs; ++b) load_x(b % kXBufs, xsrc, ldx, clampk(s0 + b) * kGStepK);
         __syncthreads();
         uint32_t s = 0;
-        // steady state: three steps (one turn of the ring) per pass
-        for (; s + 3 <= steps; s += 3) {
+        // steady state: kPass steps (whole turns of the weight ring and the
+        // register buffers) per pass
+        for (; s + kPass <= steps; s += kPass) {
 #pragma unroll
-            for (int u = 0; u < 3; ++u) {
+            for (uint32_t u = 0; u < kPass; ++u) {
                 const uint32_t st = s0 + s + u;
-                const uint32_t nxt = st + 2 < last ? st + 2 : last;
-                step(u, (u + 2) % 3, (s + u) & 1, nxt, nxt, m0, r0, g, xsrc, ldx, lds, aoff0, stoff, h);
+                step(u % 3, (u + 2) % 3, (s + u) & 1, (u + 1) % kXBufs, clampk(st + 2), clampk(st + 1 + kXBufs), m0,
+                     r0, g, xsrc, ldx, lds, aoff0, stoff, h);
             }
         }
-        // the remaining steps (fewer than three)
+        // the remaining steps (fewer than kPass)
 #pragma unroll
-        for (int u = 0; u < 3; ++u) {
+        for (uint32_t u = 0; u < kPass; ++u) {
             if (s + u >= steps) break;
             const uint32_t st = s0 + s + u;
-            const uint32_t nxt = st + 2 < last ? st + 2 : last;
-            step(u, (u + 2) % 3, (s + u) & 1, nxt, nxt, m0, r0, g, xsrc, ldx, lds, aoff0, stoff, h);
+            step(u % 3, (u + 2) % 3, (s + u) & 1, (u + 1) % kXBufs, clampk(st + 2), clampk(st + 1 + kXBufs), m0, r0,
+                 g, xsrc, ldx, lds, aoff0, stoff, h);
         }
     }
 };
