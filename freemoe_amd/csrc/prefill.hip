@@ -403,7 +403,7 @@ template <class T, class TD, uint32_t NMB>
 __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, uint32_t row0, uint32_t rows,
                              const __bf16 *__restrict__ x, __bf16 *__restrict__ act, char *lds) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t f = blockIdx.y * 128 + 32 * (wave & 3) + (lane & 31);
+    const uint32_t f = blockIdx.x * 128 + 32 * (wave & 3) + (lane & 31);
     const bool is_up = wave >= 4;
     GemmWave<T, NMB> gw;
     gw.run(static_cast<const uint8_t *>(is_up ? a.up[e] : a.gate[e]), f, a.gu,
@@ -432,14 +432,15 @@ __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, ui
     }
 }
 
-// grid: (max row tiles, ffn / 128).
+// grid: (ffn / 128, max row tiles): the row tiles past the bucketing's count
+// (their workgroups return at once) come last in dispatch order.
 template <class T, class TD>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gate_up_gemm_kernel(
     ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, const __bf16 *__restrict__ x,
     __bf16 *__restrict__ act) {
     extern __shared__ __align__(16) char xlds[];
     uint32_t e, row0, rows;
-    if (!row_tile(tiles, blockIdx.x, a.experts, pairs, e, row0, rows)) return;
+    if (!row_tile(tiles, blockIdx.y, a.experts, pairs, e, row0, rows)) return;
     switch ((rows + 31) / 32) {
     case 1: gate_up_tile<T, TD, 1>(a, e, row0, rows, x, act, xlds); break;
     case 2: gate_up_tile<T, TD, 2>(a, e, row0, rows, x, act, xlds); break;
@@ -450,19 +451,19 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     }
 }
 
-// Down rows [256 blockIdx.y, +256) (32 per wavefront) for one row tile of NMB
-// row blocks, over K steps [blockIdx.z * steps, +steps), into D[blockIdx.z]
+// Down rows [256 blockIdx.x, +256) (32 per wavefront) for one row tile of NMB
+// row blocks, over K steps [blockIdx.y * steps, +steps), into D[blockIdx.y]
 // [pairs x hidden] f32.
 template <class T, uint32_t NMB>
 __device__ __forceinline__ void down_tile(const ExpertArgs &a, uint32_t e, uint32_t row0, uint32_t rows, uint32_t pairs,
                           const __bf16 *__restrict__ act, uint32_t steps, float *__restrict__ dn, char *lds) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t n = blockIdx.y * 256 + 32 * wave + (lane & 31);
+    const uint32_t n = blockIdx.x * 256 + 32 * wave + (lane & 31);
     const uint8_t *wd = static_cast<const uint8_t *>(a.down[e]);
     GemmWave<T, NMB> gw;
-    gw.run(wd, n, a.dn, act + static_cast<uint64_t>(row0) * a.ffn, a.ffn, blockIdx.z * steps, steps, lds);
+    gw.run(wd, n, a.dn, act + static_cast<uint64_t>(row0) * a.ffn, a.ffn, blockIdx.y * steps, steps, lds);
     const uint32_t H = a.hidden;
-    float *dst = dn + static_cast<uint64_t>(blockIdx.z) * pairs * H;
+    float *dst = dn + static_cast<uint64_t>(blockIdx.y) * pairs * H;
 #pragma unroll
     for (uint32_t mb = 0; mb < NMB; ++mb) {
 #pragma unroll
@@ -474,14 +475,14 @@ __device__ __forceinline__ void down_tile(const ExpertArgs &a, uint32_t e, uint3
     }
 }
 
-// grid: (max row tiles, hidden / 256, K splits).
+// grid: (hidden / 256, K splits, max row tiles).
 template <class T>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void down_gemm_kernel(
     ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, const __bf16 *__restrict__ act,
     uint32_t steps, float *__restrict__ dn) {
     extern __shared__ __align__(16) char xlds[];
     uint32_t e, row0, rows;
-    if (!row_tile(tiles, blockIdx.x, a.experts, pairs, e, row0, rows)) return;
+    if (!row_tile(tiles, blockIdx.z, a.experts, pairs, e, row0, rows)) return;
     switch ((rows + 31) / 32) {
     case 1: down_tile<T, 1>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
     case 2: down_tile<T, 2>(a, e, row0, rows, pairs, act, steps, dn, xlds); break;
@@ -537,10 +538,10 @@ int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tile
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds)) return rc;
     if (b.pairs == 0) return FMX_OK;
     if (int rc = launch_gather<T>(b.h, a.hidden, b.tokens, b.token_list, b.pairs, b.x, s)) return rc;
-    hipLaunchKernelGGL(gu, dim3(max_tiles, a.ffn / 128), dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.x, b.act);
+    hipLaunchKernelGGL(gu, dim3(a.ffn / 128, max_tiles), dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.x, b.act);
     FMX_LAUNCH_CHECK();
     const uint32_t steps = a.ffn / kGStepK / b.splits;
-    hipLaunchKernelGGL(dn, dim3(max_tiles, a.hidden / 256, b.splits), dim3(kGThreads), lds, s, a, b.tiles, b.pairs,
+    hipLaunchKernelGGL(dn, dim3(a.hidden / 256, b.splits, max_tiles), dim3(kGThreads), lds, s, a, b.tiles, b.pairs,
                        b.act, steps, b.dn);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
