@@ -18,6 +18,11 @@ ROUTE_CASES = {
     "mixtral_router": (4096, 256, 8, 2, wl.Q4_0, 200, None),
     "finegrained_router": (2048, 256, 128, 8, wl.Q4_K, 128, 1.2),
     "odd_hidden": (200, 64, 5, 3, wl.F32, 40, None),
+    # the batched router's tile shapes: 2 tokens x 16 rows (9-16 experts),
+    # 16 x 32 (more), with partial token and row tiles and a 4-element tail
+    "sixteen_experts_odd_tokens": (256, 64, 16, 4, wl.F32, 37, None),
+    "twelve_experts": (128, 64, 12, 3, wl.F32, 21, None),
+    "forty_experts_partial_tiles": (260, 64, 40, 6, wl.F32, 45, 1.2),
 }
 
 
