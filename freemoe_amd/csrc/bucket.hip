@@ -5,7 +5,8 @@
 // that chose it; this pass inverts the routing record (engine.cpp:1707) into
 // CSR form: offsets[E+1], and for expert e the entries offsets[e]..offsets[e+1]-1
 // of token_list / rank_list hold the tokens, ascending, and the rank at which
-// they chose e. `slot_of[t*K + r]` receives the entry index of (t, r).
+// they chose e. `slot_of[t*K + r]` receives the entry index of (t, r); when it
+// is given, a second, many-workgroup pass writes the two lists from it.
 //
 // Deterministic by construction: counts are order-independent integer adds,
 // and the position of (t, r) inside expert e's list is the number of earlier
@@ -21,6 +22,11 @@ namespace {
 
 constexpr uint32_t kBucketThreads = 1024;
 constexpr uint32_t kWords = kBucketThreads / 32; // bitmask words per expert
+// Ids are read into registers in batches (their loads overlap; one workgroup
+// is latency-bound): kCountBatch per thread when counting, and a token's
+// first kIdRegs ids once per chunk.
+constexpr uint32_t kCountBatch = 8;
+constexpr uint32_t kIdRegs = 16;
 
 __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     const uint32_t *__restrict__ ids, uint32_t tokens, uint32_t K, uint32_t E,
@@ -38,10 +44,19 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
     for (uint32_t e = tid; e < E; e += kBucketThreads) count[e] = 0;
     __syncthreads();
     const uint64_t n = static_cast<uint64_t>(tokens) * K;
-    for (uint64_t i = tid; i < n; i += kBucketThreads) {
-        const uint32_t e = ids[i];
-        if (e < E) atomicAdd(&count[e], 1u);
-        else atomicOr(&bad, 1u);
+    for (uint64_t i0 = tid; i0 < n; i0 += kCountBatch * kBucketThreads) {
+        uint32_t eb[kCountBatch];
+#pragma unroll
+        for (uint32_t j = 0; j < kCountBatch; ++j) {
+            const uint64_t i = i0 + j * kBucketThreads;
+            eb[j] = i < n ? ids[i] : 0;
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < kCountBatch; ++j) {
+            if (i0 + j * kBucketThreads >= n) break;
+            if (eb[j] < E) atomicAdd(&count[eb[j]], 1u);
+            else atomicOr(&bad, 1u);
+        }
     }
     __syncthreads();
     if (bad) {
@@ -101,11 +116,16 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
         __syncthreads();
         const uint32_t t = t0 + tid;
         const bool live = t < tokens;
-        if (live)
-            for (uint32_t r = 0; r < K; ++r) {
-                const uint32_t e = ids[static_cast<uint64_t>(t) * K + r];
-                atomicOr(&mask[e * kWords + (tid >> 5)], 1u << (tid & 31));
-            }
+        const uint32_t *tid_ids = ids + static_cast<uint64_t>(live ? t : 0) * K;
+        uint32_t ev[kIdRegs];
+#pragma unroll
+        for (uint32_t r = 0; r < kIdRegs; ++r) ev[r] = live && r < K ? tid_ids[r] : 0;
+        if (live) {
+#pragma unroll
+            for (uint32_t r = 0; r < kIdRegs; ++r)
+                if (r < K) atomicOr(&mask[ev[r] * kWords + (tid >> 5)], 1u << (tid & 31));
+            for (uint32_t r = kIdRegs; r < K; ++r) atomicOr(&mask[tid_ids[r] * kWords + (tid >> 5)], 1u << (tid & 31));
+        }
         __syncthreads();
         // per expert, the exclusive prefix of its words' popcounts: one
         // 32-lane half-wavefront per expert at a time (kWords = 32)
@@ -120,21 +140,42 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
             below[i] = incl - c;
         }
         __syncthreads();
-        if (live)
-            for (uint32_t r = 0; r < K; ++r) {
-                const uint32_t e = ids[static_cast<uint64_t>(t) * K + r];
-                const uint32_t w = tid >> 5;
-                const uint32_t lower = mask[e * kWords + w] & ((1u << (tid & 31)) - 1u);
-                const uint32_t pos = base[e] + below[e * kWords + w] + __builtin_popcount(lower);
-                token_list[pos] = t;
-                rank_list[pos] = r;
-                if (slot_of) slot_of[static_cast<uint64_t>(t) * K + r] = pos;
-            }
+        if (live) {
+            const uint32_t w = tid >> 5, lowbits = (1u << (tid & 31)) - 1u;
+            // with slot_of, invert_slots_kernel writes the lists from it:
+            // their scattered stores would all pass through this one CU
+            auto place = [&](uint32_t r, uint32_t e) {
+                const uint32_t pos = base[e] + below[e * kWords + w] + __builtin_popcount(mask[e * kWords + w] & lowbits);
+                if (slot_of) {
+                    slot_of[static_cast<uint64_t>(t) * K + r] = pos;
+                } else {
+                    token_list[pos] = t;
+                    rank_list[pos] = r;
+                }
+            };
+#pragma unroll
+            for (uint32_t r = 0; r < kIdRegs; ++r)
+                if (r < K) place(r, ev[r]);
+            for (uint32_t r = kIdRegs; r < K; ++r) place(r, tid_ids[r]);
+        }
         __syncthreads();
         for (uint32_t i = tid; i < E; i += kBucketThreads)
             base[i] += below[i * kWords + kWords - 1] + __builtin_popcount(mask[i * kWords + kWords - 1]);
         __syncthreads();
     }
+}
+
+// token_list / rank_list from slot_of: entry slot_of[i] = (i / K, i % K).
+// Positions outside [0, n) (a table the bucketing rejected) are skipped.
+__global__ __launch_bounds__(256) void invert_slots_kernel(const uint32_t *__restrict__ slot_of, uint32_t n,
+                                                           uint32_t K, uint32_t *__restrict__ token_list,
+                                                           uint32_t *__restrict__ rank_list) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t pos = slot_of[i];
+    if (pos >= n) return;
+    token_list[pos] = i / K;
+    rank_list[pos] = i % K;
 }
 
 } // namespace
@@ -151,6 +192,12 @@ int launch_bucket(const uint32_t *ids, uint32_t tokens, uint32_t K, uint32_t E, 
     hipLaunchKernelGGL(bucket_kernel, dim3(1), dim3(kBucketThreads), bucket_lds_bytes(E), s, ids, tokens, K,
                        E, offsets, token_list, rank_list, slot_of, status, tiles, tile_rows);
     FMX_LAUNCH_CHECK();
+    const uint64_t n = static_cast<uint64_t>(tokens) * K;
+    if (slot_of && n > 0) {
+        hipLaunchKernelGGL(invert_slots_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, slot_of,
+                           static_cast<uint32_t>(n), K, token_list, rank_list);
+        FMX_LAUNCH_CHECK();
+    }
     return FMX_OK;
 }
 
