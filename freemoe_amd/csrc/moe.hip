@@ -481,7 +481,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *_
 // time, the next tile requested during this one's FMAs; then the lane tree,
 // the sequential tail and the logit bias, as in f32_row_chains. Few experts
 // take small tiles (2 tokens x 8 or 16 rows) so that the grid still covers
-// the device; many take 16 x 32 (8 x 4 pairs per lane). grid:
+// the device; many take 16 x 32 (4 x 8 pairs per lane). grid:
 // (ceil(tokens / TT), ceil(experts / TR)).
 constexpr uint32_t kRtPad = 20; // floats per (token or row, chain) in LDS: 16 steps + 4
 template <uint32_t PT, uint32_t PR, uint32_t GT>
@@ -925,7 +925,7 @@ int launch_route_batched(const RouteArgs &a, const float *x, uint32_t tokens, fl
         hipLaunchKernelGGL((router_tile_kernel<1, 2, 2>), dim3(div_up(tokens, 2), div_up(a.experts, 16)), dim3(256), 0,
                            s, a, h, tokens, logits);
     else
-        hipLaunchKernelGGL((router_tile_kernel<8, 4, 2>), dim3(div_up(tokens, 16), div_up(a.experts, 32)), dim3(256),
+        hipLaunchKernelGGL((router_tile_kernel<4, 8, 4>), dim3(div_up(tokens, 16), div_up(a.experts, 32)), dim3(256),
                            0, s, a, h, tokens, logits);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
