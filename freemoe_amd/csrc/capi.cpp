@@ -482,6 +482,8 @@ int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t
     PrefillBuffers b;
     b.h = h;
     b.token_list = reinterpret_cast<uint32_t *>(base + ws.token_list);
+    b.slot_of = slot_of;
+    b.top_k = L->top_k;
     b.tiles = reinterpret_cast<uint32_t *>(base + ws.tiles);
     b.tokens = tokens;
     b.pairs = ws.pairs;

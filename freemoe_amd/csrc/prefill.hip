@@ -373,23 +373,34 @@ struct GemmWave {
 
 // ------------------------------------------------------------------ kernels --
 
-// X[s][p] = bf16(h[token_list[s]][element at packed position p]), 8 positions
-// per thread. grid: (ceil(hidden / 8 / 256), pairs).
+// X[slot_of[t K + r]][p] = bf16(h[t][element at packed position p]) for
+// every rank r of token t: one workgroup per (2048-element segment, token),
+// so each h row is read once (16-byte loads into LDS) and its packed bf16
+// segment written to the token's K pair rows; 8 positions per thread.
+// Positions at or past `pairs` (a routing table the bucketing rejected) are
+// skipped. grid: (ceil(hidden / 2048), tokens).
+constexpr uint32_t kGatherSeg = 2048;
 template <class T>
-__global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ h, uint32_t hidden, uint32_t tokens,
-                                                     const uint32_t *__restrict__ token_list,
+__global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ h, uint32_t hidden, uint32_t K,
+                                                     const uint32_t *__restrict__ slot_of, uint32_t pairs,
                                                      __bf16 *__restrict__ x) {
-    const uint32_t s = blockIdx.y;
-    const uint32_t p0 = (blockIdx.x * 256 + threadIdx.x) * 8;
-    if (p0 >= hidden) return;
-    const uint32_t tok = token_list[s];
-    const float *src = h + static_cast<uint64_t>(tok < tokens ? tok : tokens - 1) * hidden;
-    const uint32_t cbase = p0 / T::kChunkK * T::kChunkK, pc = p0 % T::kChunkK;
+    __shared__ __align__(16) float seg[kGatherSeg];
+    const uint32_t t = blockIdx.y, e0 = blockIdx.x * kGatherSeg, tid = threadIdx.x;
+    const uint32_t n = hidden - e0 < kGatherSeg ? hidden - e0 : kGatherSeg;
+    const float4 *src = reinterpret_cast<const float4 *>(h + static_cast<uint64_t>(t) * hidden + e0);
+    for (uint32_t q = tid; q < n / 4; q += 256) reinterpret_cast<float4 *>(seg)[q] = src[q];
+    __syncthreads();
+    const uint32_t p = tid * 8;
+    if (p >= n) return;
+    const uint32_t cb = p / T::kChunkK * T::kChunkK, pc = p % T::kChunkK;
     uint32_t v[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        v[i] = pack_bf16x2(src[cbase + T::elem(pc + 2 * i)], src[cbase + T::elem(pc + 2 * i + 1)]);
-    *reinterpret_cast<uint4 *>(x + static_cast<uint64_t>(s) * hidden + p0) = make_uint4(v[0], v[1], v[2], v[3]);
+    for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(seg[cb + T::elem(pc + 2 * i)], seg[cb + T::elem(pc + 2 * i + 1)]);
+    const uint4 packed = make_uint4(v[0], v[1], v[2], v[3]);
+    for (uint32_t r = 0; r < K; ++r) {
+        const uint32_t pos = slot_of[static_cast<uint64_t>(t) * K + r];
+        if (pos < pairs) *reinterpret_cast<uint4 *>(x + static_cast<uint64_t>(pos) * hidden + e0 + p) = packed;
+    }
 }
 
 // Gate and up of 128 ffn rows (32 per wavefront) for one row tile of NMB row
@@ -521,10 +532,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 // ---------------------------------------------------------------- launchers --
 
 template <class T>
-int launch_gather(const float *h, uint32_t hidden, uint32_t tokens, const uint32_t *token_list, uint32_t pairs,
-                  __bf16 *x, hipStream_t s) {
-    hipLaunchKernelGGL(gather_kernel<T>, dim3(div_up(hidden / 8, 256), pairs), dim3(256), 0, s, h, hidden, tokens,
-                       token_list, x);
+int launch_gather(const float *h, uint32_t hidden, uint32_t tokens, uint32_t K, const uint32_t *slot_of,
+                  uint32_t pairs, __bf16 *x, hipStream_t s) {
+    if (tokens == 0) return FMX_OK;
+    hipLaunchKernelGGL(gather_kernel<T>, dim3(div_up(hidden, kGatherSeg), tokens), dim3(256), 0, s, h, hidden, K,
+                       slot_of, pairs, x);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
@@ -537,7 +549,7 @@ int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tile
     if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds)) return rc;
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds)) return rc;
     if (b.pairs == 0) return FMX_OK;
-    if (int rc = launch_gather<T>(b.h, a.hidden, b.tokens, b.token_list, b.pairs, b.x, s)) return rc;
+    if (int rc = launch_gather<T>(b.h, a.hidden, b.tokens, b.top_k, b.slot_of, b.pairs, b.x, s)) return rc;
     hipLaunchKernelGGL(gu, dim3(a.ffn / 128, max_tiles), dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.x, b.act);
     FMX_LAUNCH_CHECK();
     const uint32_t steps = a.ffn / kGStepK / b.splits;

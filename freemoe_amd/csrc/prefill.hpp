@@ -9,6 +9,8 @@ namespace fmx {
 struct PrefillBuffers {
     const float *h;              // [tokens x hidden] RMSNorm output
     const uint32_t *token_list;  // [pairs] token of each bucketed (token, expert) pair
+    const uint32_t *slot_of;     // [tokens x top_k] pair row of each (token, rank)
+    uint32_t top_k;
     const uint32_t *tiles;       // row tiles of the bucketing (count, then expert / first row / rows)
     uint32_t tokens;
     uint32_t pairs;              // tokens * top_k
