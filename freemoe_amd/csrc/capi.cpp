@@ -404,9 +404,10 @@ int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uin
     sc.act = reinterpret_cast<float *>(base + ws.act);
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
     FMX_LAUNCH_CHECK();
-    // events in batches: [token][route start, route end = experts start, gate/up end, down end]
+    // events in batches: [token][route start, route end, then the gate/up and
+    // the down kernels' start and end, recorded by their launches]
     constexpr uint32_t kBatch = 64;
-    hipEvent_t ev[kBatch][4];
+    hipEvent_t ev[kBatch][6];
     for (auto &row : ev)
         for (auto &e : row) FMX_HIP_TRY(hipEventCreate(&e));
     int rc = FMX_OK;
@@ -420,15 +421,14 @@ int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uin
             (void)hipEventRecord(ev[i][1], s);
             if (rc == FMX_OK)
                 rc = launch_experts(ea, x + t * H, h, lg, ids + t * K, weights + t * K, sc, out + t * H, status,
-                                    s, ev[i][2]);
-            (void)hipEventRecord(ev[i][3], s);
+                                    s, &ev[i][2]);
         }
         if (hipStreamSynchronize(s) != hipSuccess) rc = FMX_ERR_LAUNCH_FAILED;
         for (uint32_t i = 0; i < n && rc == FMX_OK; ++i) {
             float a = 0, b = 0, c = 0;
             if (hipEventElapsedTime(&a, ev[i][0], ev[i][1]) != hipSuccess ||
-                hipEventElapsedTime(&b, ev[i][1], ev[i][2]) != hipSuccess ||
-                hipEventElapsedTime(&c, ev[i][2], ev[i][3]) != hipSuccess)
+                hipEventElapsedTime(&b, ev[i][2], ev[i][3]) != hipSuccess ||
+                hipEventElapsedTime(&c, ev[i][4], ev[i][5]) != hipSuccess)
                 rc = FMX_ERR_LAUNCH_FAILED;
             kernel_ms[0] += a;
             kernel_ms[1] += b;

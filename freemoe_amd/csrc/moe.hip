@@ -26,6 +26,8 @@
 #include "matvec.hpp"
 #include "moe.hpp"
 
+#include <hip/hip_ext.h>
+
 #include <mutex>
 #include <vector>
 
@@ -837,7 +839,7 @@ constexpr int kDownPF = 7;
 template <class T>
 int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
                      float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
-                     hipEvent_t mid) {
+                     const hipEvent_t *kev) {
     constexpr int RJ = 1;
     const size_t lds_gu = static_cast<size_t>(a.gu_tile) * T::kLdsFloatsPerBlock * sizeof(float);
     const size_t lds_dn = static_cast<size_t>(a.dn_tile) * T::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
@@ -846,13 +848,20 @@ int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const 
     auto dn = down_kernel<T, kDownPF>;
     if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds_gu)) return rc;
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds_dn)) return rc;
-    hipLaunchKernelGGL(gu, dim3(div_up(a.ffn, (kThreads / 8) * RJ), a.top_k), dim3(kThreads), lds_gu, s, a, h,
-                       logits, ids, w, ws.act, status);
+    const dim3 gu_grid(div_up(a.ffn, (kThreads / 8) * RJ), a.top_k);
+    if (kev)
+        hipExtLaunchKernelGGL(gu, gu_grid, dim3(kThreads), lds_gu, s, kev[0], kev[1], 0, a, h, logits, ids, w, ws.act,
+                              status);
+    else
+        hipLaunchKernelGGL(gu, gu_grid, dim3(kThreads), lds_gu, s, a, h, logits, ids, w, ws.act, status);
     FMX_LAUNCH_CHECK();
-    if (mid) FMX_HIP_TRY(hipEventRecord(mid, s));
     const uint32_t jpw = (kThreads / 8) / a.top_k;
-    hipLaunchKernelGGL(dn, dim3(div_up(a.hidden, jpw)), dim3(kThreads), lds_dn, s, a, x, ws.act, ids, w, out,
-                       status);
+    const dim3 dn_grid(div_up(a.hidden, jpw));
+    if (kev)
+        hipExtLaunchKernelGGL(dn, dn_grid, dim3(kThreads), lds_dn, s, kev[2], kev[3], 0, a, x, ws.act, ids, w, out,
+                              status);
+    else
+        hipLaunchKernelGGL(dn, dn_grid, dim3(kThreads), lds_dn, s, a, x, ws.act, ids, w, out, status);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
@@ -979,27 +988,30 @@ int prepare_expert_args(const fmx_moe_layer *L, const RouteArgs &route, ExpertAr
 
 int launch_experts(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
                    float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
-                   hipEvent_t mid) {
+                   const hipEvent_t *kev) {
     float *act = ws.act;
     if (a.type_gu == FMX_TYPE_F32) {
         if (a.top_k > kThreads / 16 || a.type_dn != FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+        if (kev) FMX_HIP_TRY(hipEventRecord(kev[0], s));
         hipLaunchKernelGGL(gate_up_f32_kernel, dim3(div_up(a.ffn, kThreads / 16), a.top_k), dim3(kThreads), 0, s,
                            a, h, logits, ids, w, act, status);
         FMX_LAUNCH_CHECK();
-        if (mid) FMX_HIP_TRY(hipEventRecord(mid, s));
+        if (kev) FMX_HIP_TRY(hipEventRecord(kev[1], s));
     }
     if (a.type_gu == FMX_TYPE_F32 && a.type_dn == FMX_TYPE_F32) {
         const uint32_t jpw = (kThreads / 16) / a.top_k;
+        if (kev) FMX_HIP_TRY(hipEventRecord(kev[2], s));
         hipLaunchKernelGGL(down_f32_kernel, dim3(div_up(a.hidden, jpw)), dim3(kThreads), 0, s, a, x, act, ids,
                            w, out, status);
         FMX_LAUNCH_CHECK();
+        if (kev) FMX_HIP_TRY(hipEventRecord(kev[3], s));
         return FMX_OK;
     }
     if (a.type_gu != a.type_dn) return FMX_ERR_UNSUPPORTED_QUANTISATION;
     switch (a.type_gu) {
-    case FMX_TYPE_Q4_0: return launch_experts_q<Q40>(a, x, h, logits, ids, w, ws, out, status, s, mid);
-    case FMX_TYPE_Q8_0: return launch_experts_q<Q80>(a, x, h, logits, ids, w, ws, out, status, s, mid);
-    case FMX_TYPE_Q4_K: return launch_experts_q<Q4K>(a, x, h, logits, ids, w, ws, out, status, s, mid);
+    case FMX_TYPE_Q4_0: return launch_experts_q<Q40>(a, x, h, logits, ids, w, ws, out, status, s, kev);
+    case FMX_TYPE_Q8_0: return launch_experts_q<Q80>(a, x, h, logits, ids, w, ws, out, status, s, kev);
+    case FMX_TYPE_Q4_K: return launch_experts_q<Q4K>(a, x, h, logits, ids, w, ws, out, status, s, kev);
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }

@@ -47,9 +47,11 @@ int prepare_expert_args(const fmx_moe_layer *L, const RouteArgs &route, ExpertAr
 // With `logits` ([experts]), the gate/up kernel computes the token's routing
 // from them and stores it into ids / w (top_k each) for the down kernel and
 // the caller; without, ids / w hold the routing already.
-// `mid`, when given, is recorded between the gate/up and the down launch.
+// `kev`, when given, holds four events: the gate/up kernel's start and end
+// and the down kernel's start and end, recorded by the launches themselves
+// (hipExtLaunchKernelGGL), so that they bracket each kernel's execution.
 int launch_experts(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
                    float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
-                   hipEvent_t mid = nullptr);
+                   const hipEvent_t *kev = nullptr);
 
 } // namespace fmx

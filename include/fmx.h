@@ -178,9 +178,12 @@ int fmx_moe_decode(const fmx_moe_layer *layer, const float *x, float *out, uint3
                    void *stream);
 
 /* Instrumented fmx_moe_decode (no reference counterpart; for measurement):
- * the same launches, with a HIP event pair recorded around each kernel on
- * `stream`. kernel_ms[0..2] receive the summed durations in milliseconds of the
- * routing, gate/up and down kernels over all tokens. Synchronises the stream. */
+ * the same launches on `stream`, timed with HIP events: kernel_ms[0] sums the
+ * interval between events recorded before and after each routing launch;
+ * kernel_ms[1] and kernel_ms[2] sum the gate/up and down kernels' own
+ * execution, between events their launches record at kernel start and end
+ * (hipExtLaunchKernelGGL). Milliseconds over all tokens. Synchronises the
+ * stream. */
 int fmx_moe_decode_timed(const fmx_moe_layer *layer, const float *x, float *out, uint32_t tokens,
                          uint32_t *ids, float *weights, void *workspace, uint64_t workspace_bytes,
                          void *stream, double *kernel_ms);
