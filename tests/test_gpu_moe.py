@@ -207,3 +207,28 @@ def test_bucket_rejects_out_of_range_ids(gpu):
     fmx.call("fmx_moe_bucket", ids.data_ptr(), 2, 2, 4, off.data_ptr(), tl.data_ptr(), rl.data_ptr(),
              ws.data_ptr(), ws.numel(), fmx.stream_handle())
     assert fmx.lib().fmx_moe_status(ws.data_ptr(), fmx.stream_handle()) == 1
+
+
+@pytest.mark.parametrize("type_id", [wl.Q4_0, wl.F32])
+def test_decode_timed_matches_decode(gpu, type_id):
+    """The instrumented decode (launch-recorded events) gives the plain
+    decode's outputs bit for bit and positive kernel times."""
+    import ctypes
+    import torch
+    lw = wl.make_layer(256, 512, 4, 2, type_id, 51)
+    x = torch.from_numpy(wl.inputs(256, 5, 52)).to(gpu)
+    dl = DeviceLayer(lw, gpu)
+    out1, ids1, w1 = dl.decode(x)
+    out2 = torch.empty_like(x)
+    ids2 = torch.empty_like(ids1)
+    w2 = torch.empty_like(w1)
+    ws = dl.ensure_workspace(x.shape[0])
+    ms = (ctypes.c_double * 3)()
+    fmx.call("fmx_moe_decode_timed", ctypes.byref(dl.desc), x.data_ptr(), out2.data_ptr(), x.shape[0],
+             ids2.data_ptr(), w2.data_ptr(), ws.data_ptr(), ws.numel(), fmx.stream_handle(), ms)
+    torch.cuda.synchronize()
+    assert dl.status() == 0
+    assert np.array_equal(bits(to_np(out1)), bits(to_np(out2)))
+    assert np.array_equal(to_np(ids1), to_np(ids2))
+    assert np.array_equal(bits(to_np(w1)), bits(to_np(w2)))
+    assert all(v > 0.0 for v in ms)
