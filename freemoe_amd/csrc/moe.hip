@@ -911,8 +911,8 @@ int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, flo
 }
 
 // Batched routing: RMSNorm once per token into h, then the router logits in
-// tiles of 16 tokens x 16 rows (a workgroup per router row and token would
-// redo each token's RMSNorm once per expert).
+// token x row tiles shaped by the expert count (a workgroup per router row and
+// token would redo each token's RMSNorm once per expert).
 int launch_route_batched(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                          hipStream_t s) {
     if (a.hidden > kMaxHidden || a.hidden % 4 || a.experts == 0) return FMX_ERR_SHAPE_MISMATCH;
