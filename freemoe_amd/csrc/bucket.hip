@@ -64,6 +64,9 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
             atomicOr(status, STATUS_BAD_EXPERT);
             if (tiles) tiles[0] = 0; // nothing downstream runs on these lists
         }
+        // every position out of range: the gather and the combine skip them
+        if (slot_of)
+            for (uint64_t i = tid; i < n; i += kBucketThreads) slot_of[i] = 0xFFFFFFFFu;
         return;
     }
     // exclusive prefix sums over experts (E <= kBucketMaxExperts), one
@@ -159,10 +162,17 @@ __global__ __launch_bounds__(kBucketThreads) void bucket_kernel(
             for (uint32_t r = kIdRegs; r < K; ++r) place(r, tid_ids[r]);
         }
         __syncthreads();
-        for (uint32_t i = tid; i < E; i += kBucketThreads)
-            base[i] += below[i * kWords + kWords - 1] + __builtin_popcount(mask[i * kWords + kWords - 1]);
+        for (uint32_t i = tid; i < E; i += kBucketThreads) {
+            const uint32_t chosen = below[i * kWords + kWords - 1] + __builtin_popcount(mask[i * kWords + kWords - 1]);
+            base[i] += chosen;
+            count[i] -= chosen;
+        }
         __syncthreads();
     }
+    // a token that lists one expert twice sets one mask bit for two counts:
+    // its expert's count is then not used up, and the lists hold a gap
+    for (uint32_t e = tid; e < E; e += kBucketThreads)
+        if (count[e] != 0) atomicOr(status, STATUS_BAD_EXPERT);
 }
 
 // token_list / rank_list from slot_of: entry slot_of[i] = (i / K, i % K).

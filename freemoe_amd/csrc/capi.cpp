@@ -96,25 +96,10 @@ int validate_layer(const fmx_moe_layer *L) {
     if (!L->router || !L->gate || !L->up || !L->down) return FMX_ERR_INVALID_ARGUMENT;
     // the routing kernels read x, the router rows and the norm gains as float4
     if (!aligned16(L->router) || (L->norm_weight && !aligned16(L->norm_weight))) return FMX_ERR_INVALID_ARGUMENT;
-    if (L->router_type != FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    if (L->router_type != FMX_TYPE_F32 && L->router_type != FMX_TYPE_Q4_0 && L->router_type != FMX_TYPE_Q8_0 &&
+        L->router_type != FMX_TYPE_Q4_K)
+        return FMX_ERR_UNSUPPORTED_QUANTISATION;
     return FMX_OK;
-}
-
-RouteArgs route_args(const fmx_moe_layer *L) {
-    RouteArgs a;
-    a.hidden = L->hidden;
-    a.experts = L->experts;
-    a.top_k = L->top_k;
-    a.norm_weight = L->norm_weight;
-    a.rms_eps = L->rms_eps;
-    a.norm_bias = L->norm_bias;
-    a.router = static_cast<const float *>(L->router);
-    a.router_bias = L->router_bias;
-    a.weights_norm = L->weights_norm;
-    a.epsilon_additive = L->epsilon_additive;
-    a.weights_epsilon = L->weights_epsilon;
-    a.weights_scale = L->weights_scale;
-    return a;
 }
 
 } // namespace
@@ -345,9 +330,20 @@ int fmx_moe_route(const fmx_moe_layer *L, const float *x, uint32_t tokens, float
     uint8_t *base = static_cast<uint8_t *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(base);
     float *lg = logits ? logits : reinterpret_cast<float *>(base + ws.logits);
+    RouteArgs ra;
+    if (int rc = prepare_route_args(L, &ra)) return rc;
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
     FMX_LAUNCH_CHECK();
-    return launch_route(route_args(L), x, tokens, h, lg, ids, weights, status, s);
+    if (h || ra.router_type == FMX_TYPE_F32) return launch_route(ra, x, tokens, h, lg, ids, weights, status, s);
+    // a block-type router needs h: one token at a time through the
+    // workspace's h
+    if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
+    float *hw = reinterpret_cast<float *>(base + ws.h);
+    const uint64_t H = L->hidden, E = L->experts, K = L->top_k;
+    for (uint32_t t = 0; t < tokens; ++t)
+        if (int rc = launch_route(ra, x + t * H, 1, hw, lg + t * E, ids + t * K, weights + t * K, status, s))
+            return rc;
+    return FMX_OK;
 }
 
 int fmx_moe_decode(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
@@ -359,9 +355,10 @@ int fmx_moe_decode(const fmx_moe_layer *L, const float *x, float *out, uint32_t 
     if (!aligned16(x) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
     const DecodeWorkspace ws = decode_workspace(L, 1);
     if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
+    RouteArgs ra;
+    if (int rc = prepare_route_args(L, &ra)) return rc;
     ExpertArgs ea;
-    if (int rc = prepare_expert_args(L, route_args(L), &ea)) return rc;
-    const RouteArgs ra = route_args(L);
+    if (int rc = prepare_expert_args(L, ra, &ea)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint8_t *base = static_cast<uint8_t *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(base);
@@ -391,9 +388,10 @@ int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uin
     if (!x || !out || !ids || !weights || !workspace) return FMX_ERR_INVALID_ARGUMENT;
     const DecodeWorkspace ws = decode_workspace(L, 1);
     if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
+    RouteArgs ra;
+    if (int rc = prepare_route_args(L, &ra)) return rc;
     ExpertArgs ea;
-    if (int rc = prepare_expert_args(L, route_args(L), &ea)) return rc;
-    const RouteArgs ra = route_args(L);
+    if (int rc = prepare_expert_args(L, ra, &ea)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (!aligned16(x) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
     uint8_t *base = static_cast<uint8_t *>(workspace);
@@ -454,9 +452,10 @@ int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t
     if (!aligned16(x) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
     const PrefillWorkspace ws = prefill_workspace(L, tokens);
     if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
+    RouteArgs ra;
+    if (int rc = prepare_route_args(L, &ra)) return rc;
     ExpertArgs ea;
-    if (int rc = prepare_expert_args(L, route_args(L), &ea)) return rc;
-    const RouteArgs ra = route_args(L);
+    if (int rc = prepare_expert_args(L, ra, &ea)) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
     uint8_t *base = static_cast<uint8_t *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(base);

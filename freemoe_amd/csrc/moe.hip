@@ -600,6 +600,35 @@ __global__ __launch_bounds__(64) void route_finish_kernel(RouteArgs a, const flo
     if (bad && lane == 0) atomicOr(status, STATUS_NONFINITE_SCORE);
 }
 
+// Router logits of a block-type router (the reference's quantised branch,
+// engine.cpp:358-366 -> gemv_quant, kernels.cpp:846-878): every row runs the
+// lane chains of the experts' rows, so a logit is the reference's bit for
+// bit; then the logit bias (engine.cpp:1611-1616). 32 router rows per
+// workgroup, token blockIdx.x's h staged in LDS tiles of a.rtile blocks.
+// grid: (tokens, ceil(experts / 32)).
+template <class T>
+__global__ __launch_bounds__(kThreads) void router_quant_kernel(RouteArgs a, const float *__restrict__ h,
+                                                                float *__restrict__ logits) {
+    extern __shared__ __align__(16) float lds[];
+    const uint32_t tid = threadIdx.x, l = tid & 7, slot = tid >> 3;
+    const uint32_t t = blockIdx.x, r = blockIdx.y * (kThreads / 8) + slot, E = a.experts;
+    const PackedGeometry &g = a.rg;
+    typename T::Row rw[1] = {T::row(static_cast<const uint8_t *>(a.router_packed), g.scale_bytes, g.blocks_padded,
+                                    g.chunks, r < E ? r : E - 1, l)};
+    float acc[1] = {0.0f};
+    const float *x = h + static_cast<uint64_t>(t) * a.hidden;
+    for (uint32_t tb = 0; tb < g.blocks; tb += a.rtile) {
+        const uint32_t nb = g.blocks - tb < a.rtile ? g.blocks - tb : a.rtile;
+        __syncthreads();
+        T::stage(x, tb, nb, lds, tid, kThreads);
+        __syncthreads();
+        run_chunks_pf<T, 1, 2>(rw, tb / T::kPerChunk, (tb + nb + T::kPerChunk - 1) / T::kPerChunk, g.blocks, tb, nb,
+                               lds, l, acc);
+    }
+    const float v = T::finish(acc[0]);
+    if (l == 0 && r < E) logits[static_cast<uint64_t>(t) * E + r] = a.router_bias ? v + a.router_bias[r] : v;
+}
+
 // The expert of rank `rank` for an expert kernel: from the routing computed
 // in this wavefront when `logits` is given (the first workgroup also stores
 // ids, weights and the error flag for the kernels after it), else from ids.
@@ -836,16 +865,17 @@ __global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const 
 constexpr int kGateUpPF = 1;
 constexpr int kDownPF = 7;
 
-template <class T>
+// Gate/up rows in block type TG, down rows in TD.
+template <class TG, class TD>
 int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
                      float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
                      const hipEvent_t *kev) {
     constexpr int RJ = 1;
-    const size_t lds_gu = static_cast<size_t>(a.gu_tile) * T::kLdsFloatsPerBlock * sizeof(float);
-    const size_t lds_dn = static_cast<size_t>(a.dn_tile) * T::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
+    const size_t lds_gu = static_cast<size_t>(a.gu_tile) * TG::kLdsFloatsPerBlock * sizeof(float);
+    const size_t lds_dn = static_cast<size_t>(a.dn_tile) * TD::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
     if (lds_gu > kMaxLds || lds_dn > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
-    auto gu = gate_up_kernel<T, RJ, kGateUpPF>;
-    auto dn = down_kernel<T, kDownPF>;
+    auto gu = gate_up_kernel<TG, RJ, kGateUpPF>;
+    auto dn = down_kernel<TD, kDownPF>;
     if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds_gu)) return rc;
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds_dn)) return rc;
     const dim3 gu_grid(div_up(a.ffn, (kThreads / 8) * RJ), a.top_k);
@@ -864,6 +894,20 @@ int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const 
         hipLaunchKernelGGL(dn, dn_grid, dim3(kThreads), lds_dn, s, a, x, ws.act, ids, w, out, status);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
+}
+
+// The down block type for gate/up in TG (they may differ, as in the
+// reference's Q4_K gate/up with Q6_K down experts).
+template <class TG>
+int launch_experts_gu(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
+                      float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
+                      const hipEvent_t *kev) {
+    switch (a.type_dn) {
+    case FMX_TYPE_Q4_0: return launch_experts_q<TG, Q40>(a, x, h, logits, ids, w, ws, out, status, s, kev);
+    case FMX_TYPE_Q8_0: return launch_experts_q<TG, Q80>(a, x, h, logits, ids, w, ws, out, status, s, kev);
+    case FMX_TYPE_Q4_K: return launch_experts_q<TG, Q4K>(a, x, h, logits, ids, w, ws, out, status, s, kev);
+    }
+    return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }
 
 } // namespace
@@ -889,11 +933,53 @@ int allow_lds(const void *fn, size_t bytes) {
 
 size_t route_lds_bytes(uint32_t hidden) { return 2ull * 16 * route_chain_stride(hidden) * sizeof(float); }
 
+// RMSNorm of `tokens` rows of x into h: one workgroup per token.
+int launch_rmsnorm(const RouteArgs &a, const float *x, uint32_t tokens, float *h, hipStream_t s) {
+    const size_t lds = 2ull * a.hidden * sizeof(float);
+    if (a.hidden <= 16 * 256) {
+        auto k = rmsnorm_kernel<256>;
+        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+        hipLaunchKernelGGL(k, dim3(tokens), dim3(256), lds, s, a, x, h);
+    } else {
+        auto k = rmsnorm_kernel<1024>;
+        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+        hipLaunchKernelGGL(k, dim3(tokens), dim3(1024), lds, s, a, x, h);
+    }
+    FMX_LAUNCH_CHECK();
+    return FMX_OK;
+}
+
+template <class T>
+int launch_router_quant_t(const RouteArgs &a, const float *h, uint32_t tokens, float *logits, hipStream_t s) {
+    const size_t lds = static_cast<size_t>(a.rtile) * T::kLdsFloatsPerBlock * sizeof(float);
+    auto k = router_quant_kernel<T>;
+    if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+    hipLaunchKernelGGL(k, dim3(tokens, div_up(a.experts, kThreads / 8)), dim3(kThreads), lds, s, a, h, logits);
+    FMX_LAUNCH_CHECK();
+    return FMX_OK;
+}
+
+// Logits of a block-type router from h ([tokens x hidden]).
+int launch_router_quant(const RouteArgs &a, const float *h, uint32_t tokens, float *logits, hipStream_t s) {
+    switch (a.router_type) {
+    case FMX_TYPE_Q4_0: return launch_router_quant_t<Q40>(a, h, tokens, logits, s);
+    case FMX_TYPE_Q8_0: return launch_router_quant_t<Q80>(a, h, tokens, logits, s);
+    case FMX_TYPE_Q4_K: return launch_router_quant_t<Q4K>(a, h, tokens, logits, s);
+    }
+    return FMX_ERR_UNSUPPORTED_QUANTISATION;
+}
+
 // One workgroup per (token, router row): 256 threads up to hidden 4096, 1024
-// beyond (each thread holds 16 elements of the token).
+// beyond (each thread holds 16 elements of the token). A block-type router
+// takes RMSNorm into h (which it then needs) and the router rows after it.
 int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                         hipStream_t s) {
     if (a.hidden > kMaxHidden || a.hidden % 4 || a.experts == 0) return FMX_ERR_SHAPE_MISMATCH;
+    if (a.router_type != FMX_TYPE_F32) {
+        if (!h) return FMX_ERR_INVALID_ARGUMENT;
+        if (int rc = launch_rmsnorm(a, x, tokens, h, s)) return rc;
+        return launch_router_quant(a, h, tokens, logits, s);
+    }
     const size_t lds = route_lds_bytes(a.hidden);
     if (lds > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
     const dim3 grid(tokens, a.experts);
@@ -916,17 +1002,8 @@ int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, flo
 int launch_route_batched(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                          hipStream_t s) {
     if (a.hidden > kMaxHidden || a.hidden % 4 || a.experts == 0) return FMX_ERR_SHAPE_MISMATCH;
-    const size_t lds = 2ull * a.hidden * sizeof(float);
-    if (a.hidden <= 16 * 256) {
-        auto k = rmsnorm_kernel<256>;
-        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
-        hipLaunchKernelGGL(k, dim3(tokens), dim3(256), lds, s, a, x, h);
-    } else {
-        auto k = rmsnorm_kernel<1024>;
-        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
-        hipLaunchKernelGGL(k, dim3(tokens), dim3(1024), lds, s, a, x, h);
-    }
-    FMX_LAUNCH_CHECK();
+    if (int rc = launch_rmsnorm(a, x, tokens, h, s)) return rc;
+    if (a.router_type != FMX_TYPE_F32) return launch_router_quant(a, h, tokens, logits, s);
     if (a.experts <= 8)
         hipLaunchKernelGGL((router_tile_kernel<1, 1, 2>), dim3(div_up(tokens, 2), div_up(a.experts, 8)), dim3(256), 0,
                            s, a, h, tokens, logits);
@@ -947,6 +1024,42 @@ int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, 
         return rc;
     hipLaunchKernelGGL(route_finish_kernel, dim3(tokens), dim3(64), 0, s, a, logits, ids, weights, status);
     FMX_LAUNCH_CHECK();
+    return FMX_OK;
+}
+
+int prepare_route_args(const fmx_moe_layer *L, RouteArgs *out) {
+    RouteArgs a;
+    a.hidden = L->hidden;
+    a.experts = L->experts;
+    a.top_k = L->top_k;
+    a.norm_weight = L->norm_weight;
+    a.rms_eps = L->rms_eps;
+    a.norm_bias = L->norm_bias;
+    a.router_type = L->router_type;
+    a.router = nullptr;
+    a.router_packed = nullptr;
+    a.rtile = 0;
+    switch (L->router_type) {
+    case FMX_TYPE_F32: a.router = static_cast<const float *>(L->router); break;
+    case FMX_TYPE_Q4_0:
+    case FMX_TYPE_Q8_0:
+    case FMX_TYPE_Q4_K: {
+        if (int rc = packed_geometry(L->router_type, L->experts, L->hidden, &a.rg)) return rc;
+        a.router_packed = L->router;
+        constexpr uint32_t kBudget = 8 * 1024; // floats of h per LDS tile
+        a.rtile = L->router_type == FMX_TYPE_Q4_0   ? tile_blocks_for<Q40>(a.rg.blocks, kBudget)
+                  : L->router_type == FMX_TYPE_Q8_0 ? tile_blocks_for<Q80>(a.rg.blocks, kBudget)
+                                                    : tile_blocks_for<Q4K>(a.rg.blocks, kBudget);
+        break;
+    }
+    default: return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    }
+    a.router_bias = L->router_bias;
+    a.weights_norm = L->weights_norm;
+    a.epsilon_additive = L->epsilon_additive;
+    a.weights_epsilon = L->weights_epsilon;
+    a.weights_scale = L->weights_scale;
+    *out = a;
     return FMX_OK;
 }
 
@@ -1007,11 +1120,11 @@ int launch_experts(const ExpertArgs &a, const float *x, const float *h, const fl
         if (kev) FMX_HIP_TRY(hipEventRecord(kev[3], s));
         return FMX_OK;
     }
-    if (a.type_gu != a.type_dn) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    if (a.type_gu == FMX_TYPE_F32 || a.type_dn == FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
     switch (a.type_gu) {
-    case FMX_TYPE_Q4_0: return launch_experts_q<Q40>(a, x, h, logits, ids, w, ws, out, status, s, kev);
-    case FMX_TYPE_Q8_0: return launch_experts_q<Q80>(a, x, h, logits, ids, w, ws, out, status, s, kev);
-    case FMX_TYPE_Q4_K: return launch_experts_q<Q4K>(a, x, h, logits, ids, w, ws, out, status, s, kev);
+    case FMX_TYPE_Q4_0: return launch_experts_gu<Q40>(a, x, h, logits, ids, w, ws, out, status, s, kev);
+    case FMX_TYPE_Q8_0: return launch_experts_gu<Q80>(a, x, h, logits, ids, w, ws, out, status, s, kev);
+    case FMX_TYPE_Q4_K: return launch_experts_gu<Q4K>(a, x, h, logits, ids, w, ws, out, status, s, kev);
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }

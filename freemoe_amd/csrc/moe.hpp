@@ -5,12 +5,18 @@
 
 namespace fmx {
 
-// Routing arguments (device pointers); F32 router only.
+// Routing arguments (device pointers). An F32 router is raw row-major
+// (`router`); a block-type router is packed (`router_packed`, geometry `rg`,
+// LDS tile of `rtile` blocks) and its rows run the experts' lane chains.
 struct RouteArgs {
     uint32_t hidden, experts, top_k;
     const float *norm_weight;
     double rms_eps, norm_bias;
+    uint32_t router_type;
     const float *router;
+    const void *router_packed;
+    PackedGeometry rg;
+    uint32_t rtile;
     const float *router_bias;
     int32_t weights_norm, epsilon_additive;
     double weights_epsilon, weights_scale;
@@ -42,6 +48,8 @@ int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, flo
 int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                  uint32_t *ids, float *weights, uint32_t *status, hipStream_t s);
 int prepare_expert_args(const fmx_moe_layer *L, const RouteArgs &route, ExpertArgs *a);
+// Routing arguments of a layer (geometry and LDS tile of a block-type router).
+int prepare_route_args(const fmx_moe_layer *L, RouteArgs *a);
 // Decode experts for one token: gate/up + SwiGLU into act[top_k x ffn], then
 // down + combine + residual into out[hidden].
 // With `logits` ([experts]), the gate/up kernel computes the token's routing

@@ -507,11 +507,13 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
 // out[t] = x[t] + ((0 + w_0 D_0) + w_1 D_1 ...) in rank order (engine.cpp:1517,
 // 1770, 813-816), each D the sum of the K splits' partial products in split
 // order. V consecutive elements per thread (hidden % V == 0, x and out
-// V-float aligned). grid: (ceil(hidden / (256 V)), tokens).
+// V-float aligned). A rank whose position is at or past `pairs` (a routing
+// table the bucketing rejected, which reported it) adds nothing. grid:
+// (ceil(hidden / (256 V)), tokens).
 template <uint32_t V>
 __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ x, const float *__restrict__ dn,
                                                       uint32_t splits, uint64_t split_stride,
-                                                      const uint32_t *__restrict__ slot_of,
+                                                      const uint32_t *__restrict__ slot_of, uint32_t pairs,
                                                       const float *__restrict__ w, uint32_t hidden, uint32_t K,
                                                       float *__restrict__ out) {
     typedef float fv __attribute__((ext_vector_type(V)));
@@ -520,7 +522,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
     fv ffn = 0.0f;
     for (uint32_t r = 0; r < K; ++r) {
         const uint64_t i = static_cast<uint64_t>(t) * K + r;
-        const float *d = dn + static_cast<uint64_t>(slot_of[i]) * hidden + j;
+        const uint32_t pos = slot_of[i];
+        if (pos >= pairs) continue;
+        const float *d = dn + static_cast<uint64_t>(pos) * hidden + j;
         fv v = *reinterpret_cast<const fv *>(d);
         for (uint32_t sp = 1; sp < splits; ++sp) v += *reinterpret_cast<const fv *>(d + sp * split_stride);
         ffn = ffn + w[i] * v;
@@ -616,10 +620,10 @@ int launch_combine(const float *x, const float *dn, uint32_t splits, uint32_t pa
     const uint64_t stride = static_cast<uint64_t>(pairs) * hidden;
     if (hidden % 4 == 0 && (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) % 16 == 0)
         hipLaunchKernelGGL(combine_kernel<4>, dim3(div_up(hidden, 1024), tokens), dim3(256), 0, s, x, dn, splits,
-                           stride, slot_of, w, hidden, K, out);
+                           stride, slot_of, pairs, w, hidden, K, out);
     else
         hipLaunchKernelGGL(combine_kernel<1>, dim3(div_up(hidden, 256), tokens), dim3(256), 0, s, x, dn, splits,
-                           stride, slot_of, w, hidden, K, out);
+                           stride, slot_of, pairs, w, hidden, K, out);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }

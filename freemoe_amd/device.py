@@ -34,7 +34,9 @@ class DeviceLayer:
         self.device = torch.device(device)
         H, F, E = lw.hidden, lw.ffn, lw.experts
         self.norm = to_device(lw.norm_weight, self.device)
-        self.router = to_device(lw.router, self.device)
+        self.router = to_device(lw.router_bytes, self.device)
+        if lw.router_type != fmx.FMX_TYPE_F32:
+            self.router = pack(lw.router_type, self.router, E, H, stream)
         self.router_bias = None if lw.router_bias is None else to_device(lw.router_bias, self.device)
         self.gate, self.up, self.down = [], [], []
         for e in range(E):
@@ -44,9 +46,10 @@ class DeviceLayer:
         self.slots = torch.tensor([[t.data_ptr() for t in arr] for arr in (self.gate, self.up, self.down)],
                                   dtype=torch.int64, device=self.device)
         self.desc = fmx.MoELayer(
-            H, F, E, lw.top_k, self.norm.data_ptr(), lw.rms_eps, 0.0, fmx.FMX_TYPE_F32, self.router.data_ptr(),
-            fmx.ptr(self.router_bias), int(lw.weights_norm), 0, 6.103515625e-5, 1.0, lw.gate_type, lw.up_type,
-            lw.down_type, self.slots[0].data_ptr(), self.slots[1].data_ptr(), self.slots[2].data_ptr())
+            H, F, E, lw.top_k, self.norm.data_ptr(), lw.rms_eps, lw.norm_bias, lw.router_type,
+            self.router.data_ptr(), fmx.ptr(self.router_bias), int(lw.weights_norm), int(lw.epsilon_additive),
+            lw.weights_epsilon, lw.weights_scale, lw.gate_type, lw.up_type, lw.down_type,
+            self.slots[0].data_ptr(), self.slots[1].data_ptr(), self.slots[2].data_ptr())
         self.workspace = None
         self.prefill_workspace = None
 

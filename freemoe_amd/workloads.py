@@ -72,18 +72,36 @@ class LayerWeights:
     weights_norm: bool = True
     seed: int = 0
     notes: dict = field(default_factory=dict)
+    down_type: int | None = None       # None: gate_type
+    router_type: int = F32             # the router's block type (raw rows in `router_raw`)
+    router_raw: np.ndarray | None = None
+    norm_bias: float = 0.0             # 1.0 for zero-centred norm gains
+    epsilon_additive: bool = False     # expert_weights_epsilon_additive
+    weights_epsilon: float = 6.103515625e-5
+    weights_scale: float = 1.0
+
+    def __post_init__(self):
+        if self.down_type is None:
+            self.down_type = self.gate_type
 
     @property
     def up_type(self):
         return self.gate_type
 
     @property
-    def down_type(self):
-        return self.gate_type
+    def router_bytes(self) -> np.ndarray:
+        """The router as raw GGUF rows [experts x row_bytes(hidden)]."""
+        if self.router_type == F32:
+            return np.ascontiguousarray(self.router).view(np.uint8)
+        return self.router_raw
 
 
 def make_layer(hidden: int, ffn: int, experts: int, top_k: int, type_id: int, seed: int,
-               zipf_s: float | None = None) -> LayerWeights:
+               zipf_s: float | None = None, down_type: int | None = None,
+               router_type: int = F32) -> LayerWeights:
+    """A seeded layer; gate/up in `type_id`, down in `down_type` (default the
+    same). A block-type router holds rows of quants uniform as the experts'
+    with scales f16(|N(0, 1/hidden)|), so that logits keep a unit scale."""
     rng = np.random.default_rng(seed)
     norm = (1.0 + rng.standard_normal(hidden) * 0.02).astype(np.float32)
     router = (rng.standard_normal((experts, hidden)) / np.sqrt(hidden)).astype(np.float32)
@@ -93,13 +111,19 @@ def make_layer(hidden: int, ffn: int, experts: int, top_k: int, type_id: int, se
         ranks = rng.permutation(experts) + 1
         bias = (-zipf_s * np.log(ranks)).astype(np.float32)
         notes["router_bias"] = f"-{zipf_s}*ln(rank), ranks a seeded permutation of 1..{experts}"
+    dt = type_id if down_type is None else down_type
     gate, up, down = [], [], []
     for _ in range(experts):
         gate.append(matrix(type_id, rng, ffn, hidden))
         up.append(matrix(type_id, rng, ffn, hidden))
-        down.append(matrix(type_id, rng, hidden, ffn))
+        down.append(matrix(dt, rng, hidden, ffn))
+    router_raw = None
+    if router_type != F32:
+        router_raw = matrix(router_type, np.random.default_rng(seed + 7919), experts, hidden,
+                            sigma=float(1.0 / hidden))
     return LayerWeights(hidden, ffn, experts, top_k, type_id, norm, router, gate, up, down, bias,
-                        seed=seed, notes=notes)
+                        seed=seed, notes=notes, down_type=dt, router_type=router_type,
+                        router_raw=router_raw)
 
 
 def inputs(hidden: int, tokens: int, seed: int) -> np.ndarray:

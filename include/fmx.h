@@ -140,12 +140,16 @@ int fmx_matvec(uint32_t type_id, const void *packed, const float *x, float *y,
  * arrays of device pointers (the hot expert slot table), so the kernels find the
  * routed experts without a host round trip. */
 typedef struct fmx_moe_layer {
+    /* gate/up and down may hold different block types (e.g. Q4_K gate/up with
+     * Q8_0 down); gate and up share one. */
     uint32_t hidden, ffn, experts, top_k;
     const float *norm_weight;     /* [hidden] RMSNorm gain, NULL = unit gain (16-byte aligned) */
     double rms_eps;               /* ModelConfig::rms_eps */
     double norm_bias;             /* 1.0 when norm weights are zero-centred */
-    uint32_t router_type;         /* FMX_TYPE_F32 */
-    const void *router;           /* [experts x hidden] raw row-major (16-byte aligned) */
+    uint32_t router_type;         /* FMX_TYPE_F32, _Q4_0, _Q8_0 or _Q4_K */
+    const void *router;           /* [experts x hidden], 16-byte aligned: F32 raw row-major;
+                                     a block type packed (fmx_pack), its logits then the
+                                     gemv_quant row dots (engine.cpp:358-366) */
     const float *router_bias;     /* [experts] logit bias (ffn_gate_inp.bias) or NULL */
     int32_t weights_norm;         /* expert_weights_norm */
     int32_t epsilon_additive;     /* expert_weights_epsilon_additive */
@@ -191,9 +195,10 @@ int fmx_moe_decode_timed(const fmx_moe_layer *layer, const float *x, float *out,
 /* Prefill: the whole layer for `tokens` rows of x ([tokens x hidden]) at once.
  * Routing is bit-identical to fmx_moe_route (ids / weights [tokens x top_k]);
  * the experts run as grouped GEMMs on bf16 MFMA over per-expert token lists
- * (fmx_moe_bucket's order), with each expert's packed blocks dequantised into
- * LDS; outputs match the reference within 2e-2 relative (bf16 operands, f32
- * accumulation). The reference has no batched MoE path: it runs its decode
+ * (fmx_moe_bucket's order): each lane loads its weight row's packed blocks
+ * and dequantises them in registers into the MFMA's bf16 B operand, while the
+ * gathered activations pass through LDS; outputs match the reference within
+ * 2e-2 relative (bf16 operands, f32 accumulation). The reference has no batched MoE path: it runs its decode
  * step once per prompt token (engine.cpp:1870, 2395-2399); this replaces that
  * loop. Shapes the GEMMs do not tile (and F32 experts) run the decode expert
  * kernels token by token instead, on the GPU. */
@@ -210,8 +215,10 @@ int fmx_moe_status(void *workspace, void *stream);
  * offsets[experts+1], token_list/rank_list[tokens*top_k] as the reference's
  * routing record (engine.cpp:1707) inverted: tokens ascending within each
  * expert, with the rank at which each chose it. Deterministic (no atomic slot
- * grabs). experts <= 256. An id >= experts is reported by fmx_moe_status on the
- * same workspace (>= 256 bytes). */
+ * grabs). experts <= 256. A token's ids must be distinct, as top-k makes them
+ * (engine.cpp:395-411). An id >= experts, or a token that lists one expert
+ * twice, is reported as FMX_ERR_INVALID_ARGUMENT by fmx_moe_status on the same
+ * workspace (>= 256 bytes); the lists are then not meaningful. */
 int fmx_moe_bucket(const uint32_t *ids, uint32_t tokens, uint32_t top_k, uint32_t experts,
                    uint32_t *offsets, uint32_t *token_list, uint32_t *rank_list, void *workspace,
                    uint64_t workspace_bytes, void *stream);

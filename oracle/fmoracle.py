@@ -215,15 +215,31 @@ class HostLayer:
               "fmo_moe_layer")
         return out, ids, w, h, act
 
-    def forward_batch(self, x: np.ndarray, isa: int = ISA_AVX2):
+    def forward_batch(self, x: np.ndarray, isa: int = ISA_AVX2, threads: int = 1):
+        """Every row of x as its own token. `threads` > 1 splits the rows over
+        that many threads (the C calls release the GIL; each token's result
+        does not depend on the split)."""
         x = np.ascontiguousarray(x, np.float32).reshape(-1, self.hidden)
         t = x.shape[0]
         out = np.empty_like(x)
         ids = np.empty((t, self.top_k), np.uint32)
         w = np.empty((t, self.top_k), np.float32)
         L = self.struct()
-        check(oracle().fmo_moe_layer_batch(isa, ctypes.byref(L), _p(x), _p(out), _p(ids), _p(w), t),
-              "fmo_moe_layer_batch")
+
+        def run(a: int, b: int) -> int:
+            return oracle().fmo_moe_layer_batch(isa, ctypes.byref(L), _p(x[a:]), _p(out[a:]), _p(ids[a:]),
+                                                _p(w[a:]), b - a)
+
+        threads = max(1, min(threads, t))
+        if threads == 1:
+            check(run(0, t), "fmo_moe_layer_batch")
+            return out, ids, w
+        from concurrent.futures import ThreadPoolExecutor
+        cuts = [t * i // threads for i in range(threads + 1)]
+        with ThreadPoolExecutor(threads) as pool:
+            rcs = list(pool.map(lambda i: run(cuts[i], cuts[i + 1]), range(threads)))
+        for rc in rcs:
+            check(rc, "fmo_moe_layer_batch")
         return out, ids, w
 
     def ref_forward_batch(self, x: np.ndarray, isa: int = ISA_AVX2, threads: int = 0):
@@ -242,6 +258,9 @@ class HostLayer:
 def host_layer(lw) -> HostLayer:
     """HostLayer from freemoe_amd.workloads.LayerWeights (same arrays, no copies)."""
     return HostLayer(hidden=lw.hidden, ffn=lw.ffn, experts=lw.experts, top_k=lw.top_k,
-                     norm_weight=lw.norm_weight, rms_eps=lw.rms_eps, router=lw.router.view(np.uint8),
-                     router_bias=lw.router_bias, gate=lw.gate, up=lw.up, down=lw.down,
-                     gate_type=lw.gate_type, weights_norm=lw.weights_norm)
+                     norm_weight=lw.norm_weight, rms_eps=lw.rms_eps, router=lw.router_bytes,
+                     router_type=lw.router_type, router_bias=lw.router_bias, gate=lw.gate, up=lw.up,
+                     down=lw.down, gate_type=lw.gate_type, down_type=lw.down_type,
+                     norm_bias=lw.norm_bias, weights_norm=lw.weights_norm,
+                     epsilon_additive=lw.epsilon_additive, weights_epsilon=lw.weights_epsilon,
+                     weights_scale=lw.weights_scale)

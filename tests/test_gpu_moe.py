@@ -232,3 +232,124 @@ def test_decode_timed_matches_decode(gpu, type_id):
     assert np.array_equal(to_np(ids1), to_np(ids2))
     assert np.array_equal(bits(to_np(w1)), bits(to_np(w2)))
     assert all(v > 0.0 for v in ms)
+
+
+def check_route(gpu, lw, x):
+    """The device routing (h, logits, ids, weights) against the oracle, bit for
+    bit, on the batched route of all tokens and on the single-token route."""
+    import torch
+    dl = DeviceLayer(lw, gpu)
+    xd = torch.from_numpy(x).to(gpu)
+    hl = host_layer(lw)
+    for rows in (slice(0, len(x)), slice(0, 1)):
+        h, logits, ids, w = dl.route(xd[rows])
+        torch.cuda.synchronize()
+        assert dl.status() == 0
+        for i in range(rows.stop):
+            hh, lg, pr, ii, ww = hl.route(x[i])
+            assert np.array_equal(bits(to_np(h[i])), bits(hh)), f"h token {i}"
+            assert np.array_equal(bits(to_np(logits[i])), bits(lg)), f"logits token {i}"
+            assert np.array_equal(to_np(ids[i]).astype(np.uint32), ii), f"ids token {i}"
+            assert np.array_equal(bits(to_np(w[i])), bits(ww)), f"weights token {i}"
+
+
+BLOCK_ROUTER_CASES = {
+    # name: (hidden, ffn, experts, top_k, expert type, router type, tokens, zipf)
+    "q4_0_router": (512, 256, 8, 2, wl.Q4_0, wl.Q4_0, 24, None),
+    "q8_0_router": (256, 512, 4, 2, wl.Q8_0, wl.Q8_0, 24, None),
+    "q4_k_router_40_experts": (512, 256, 40, 4, wl.Q4_K, wl.Q4_K, 20, 1.2),
+    "q8_0_router_q4_0_experts": (4096, 256, 8, 2, wl.Q4_0, wl.Q8_0, 12, None),
+}
+
+
+@pytest.mark.parametrize("name", list(BLOCK_ROUTER_CASES))
+def test_block_type_router(gpu, name):
+    """A quantised router (the reference's quant fixtures quantise it): logits
+    are gemv_quant row dots, bit for bit, on the route, decode and prefill
+    paths."""
+    H, F, E, K, t, rt, T, z = BLOCK_ROUTER_CASES[name]
+    lw = wl.make_layer(H, F, E, K, t, 81, zipf_s=z, router_type=rt)
+    x = wl.inputs(H, T, 82)
+    check_route(gpu, lw, x)
+    assert check_layer(gpu, lw, x) == 0
+    import test_gpu_prefill as tp
+    tp.check_prefill(gpu, lw, x)
+
+
+@pytest.mark.parametrize("gate_type,down_type", [(wl.Q4_K, wl.Q8_0), (wl.Q8_0, wl.Q4_0), (wl.Q4_0, wl.Q4_K)])
+def test_decode_mixed_block_types(gpu, gate_type, down_type):
+    """Gate/up and down of different block types (the reference runs Q4_K
+    gate/up with Q6_K down, tests.cpp:1479-1544): each projection keeps its
+    own lane chains, the layer stays bit for bit."""
+    lw = wl.make_layer(512, 512, 6, 2, gate_type, 91, down_type=down_type)
+    x = wl.inputs(512, 8, 92)
+    assert check_layer(gpu, lw, x) == 0
+
+
+def test_route_exact_probability_ties(gpu):
+    """Router rows 1 and 4, and rows 2 and 6, are equal, so their logits and
+    probabilities are equal bit for bit: the stable top-k keeps the lower index
+    first (engine.cpp:395-411), on every path."""
+    lw = wl.make_layer(256, 256, 8, 3, wl.Q8_0, 93)
+    lw.router[4] = lw.router[1]
+    lw.router[6] = lw.router[2]
+    x = wl.inputs(256, 64, 94)
+    hl = host_layer(lw)
+    tied = 0
+    for i in range(len(x)):
+        _, _, pr, ii, _ = hl.route(x[i])
+        assert pr[1] == pr[4] and pr[2] == pr[6]
+        tied += int(1 in ii and 4 in ii) + int(2 in ii and 6 in ii)
+    assert tied > 0  # some tokens select both members of a tied pair
+    check_route(gpu, lw, x)
+    assert check_layer(gpu, lw, x) == 0
+    import test_gpu_prefill as tp
+    tp.check_prefill(gpu, lw, x)
+
+
+ROUTING_OPTION_CASES = {
+    # zero-centred norm gains (gain = 1 + w), weights scaled
+    "norm_bias_1_scale_2_5": dict(norm_bias=1.0, weights_scale=2.5),
+    # den = total + epsilon instead of max(total, epsilon)
+    "epsilon_additive": dict(epsilon_additive=True, weights_epsilon=0.25),
+    # raw probabilities, scaled
+    "no_renormalisation": dict(weights_norm=False, weights_scale=0.75),
+    # epsilon above every total: den = epsilon
+    "epsilon_floor": dict(weights_epsilon=1.5),
+}
+
+
+@pytest.mark.parametrize("name", list(ROUTING_OPTION_CASES))
+def test_routing_options(gpu, name):
+    """The routing options of ModelConfig (norm_bias, expert_weights_norm,
+    _epsilon, _epsilon_additive, _scale; engine.cpp:723-740, 1680-1702) on the
+    route, decode and prefill paths, against the oracle."""
+    lw = wl.make_layer(256, 256, 8, 2, wl.Q4_0, 95)
+    for k, v in ROUTING_OPTION_CASES[name].items():
+        setattr(lw, k, v)
+    if lw.norm_bias:
+        lw.norm_weight = (lw.norm_weight - np.float32(1.0)).astype(np.float32)
+    x = wl.inputs(256, 32, 96)
+    check_route(gpu, lw, x)
+    assert check_layer(gpu, lw, x) == 0
+    import test_gpu_prefill as tp
+    tp.check_prefill(gpu, lw, x)
+
+
+def test_bucket_rejects_duplicate_ids(gpu):
+    """A token that lists one expert twice is reported (status
+    INVALID_ARGUMENT), as an out-of-range id is."""
+    import torch
+    ws = torch.zeros(256, dtype=torch.uint8, device=gpu)
+    ids = torch.tensor([[0, 1], [2, 2], [3, 1]], dtype=torch.int32, device=gpu)
+    off = torch.empty(5, dtype=torch.int32, device=gpu)
+    tl = torch.empty(6, dtype=torch.int32, device=gpu)
+    rl = torch.empty(6, dtype=torch.int32, device=gpu)
+    fmx.call("fmx_moe_bucket", ids.data_ptr(), 3, 2, 4, off.data_ptr(), tl.data_ptr(), rl.data_ptr(),
+             ws.data_ptr(), ws.numel(), fmx.stream_handle())
+    assert fmx.lib().fmx_moe_status(ws.data_ptr(), fmx.stream_handle()) == 1
+    # a valid table on the same workspace afterwards reports nothing
+    ids = torch.tensor([[0, 1], [2, 3], [3, 1]], dtype=torch.int32, device=gpu)
+    fmx.call("fmx_moe_bucket", ids.data_ptr(), 3, 2, 4, off.data_ptr(), tl.data_ptr(), rl.data_ptr(),
+             ws.data_ptr(), ws.numel(), fmx.stream_handle())
+    assert fmx.lib().fmx_moe_status(ws.data_ptr(), fmx.stream_handle()) == 0

@@ -6,6 +6,8 @@ FFN contribution (out - x) is checked against the oracle's within 2e-2
 relative, both as a norm ratio and as max-abs over the largest reference
 value. Shapes the GEMMs do not tile run the decode kernels and stay
 bit-identical."""
+import os
+
 import numpy as np
 import pytest
 
@@ -24,7 +26,15 @@ CASES = {
     "q4_k_zipf": (512, 256, 8, 4, wl.Q4_K, 96, 1.2),
     "q8_0_tiles_over_256_rows": (256, 256, 2, 1, wl.Q8_0, 700, None),
     "q8_0_ragged_top8": (256, 256, 16, 8, wl.Q8_0, 40, 1.2),
+    # more than 16 experts: the single-split down GEMM and the 16 x 32 router
+    # tiles
+    "q8_0_32_experts": (256, 256, 32, 4, wl.Q8_0, 300, None),
+    "q4_0_24_experts_zipf": (512, 256, 24, 3, wl.Q4_0, 200, 1.2),
 }
+
+# the oracle runs the reference's per-token loop; large cases split it over
+# host threads (each token's result does not depend on the split)
+ORACLE_THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
 def to_np(t):
@@ -37,7 +47,7 @@ def check_prefill(gpu, lw, x):
     out, ids, w = dl.prefill(torch.from_numpy(x).to(gpu))
     torch.cuda.synchronize()
     assert dl.prefill_status() == 0
-    want_out, want_ids, want_w = host_layer(lw).forward_batch(x)
+    want_out, want_ids, want_w = host_layer(lw).forward_batch(x, threads=ORACLE_THREADS)
     assert np.array_equal(to_np(ids).astype(np.uint32), want_ids)
     assert np.array_equal(to_np(w).view(np.uint32), want_w.view(np.uint32))
     got = to_np(out).astype(np.float64) - x
@@ -64,6 +74,35 @@ def test_prefill_mixtral_shape_q8_0(gpu):
     lw = wl.make_layer(4096, 14336, 8, 2, wl.Q8_0, 1234)
     x = wl.inputs(4096, 48, 1235)
     check_prefill(gpu, lw, x)
+
+
+def test_prefill_mixtral_q8_0_512_tokens(gpu):
+    """The prefill benchmark workload itself: hidden 4096, ffn 14336, 8 experts,
+    top-2, Q8_0, 512 tokens, so each expert's row tiles hold about 128 pairs
+    (4 or more 32-row blocks)."""
+    lw, x = wl.workload("mixtral-q8_0")
+    norm_ratio, max_ratio = check_prefill(gpu, lw, x)
+    print(f"mixtral q8_0 512 tokens: norm ratio {norm_ratio:.3e}, max ratio {max_ratio:.3e}")
+
+
+def test_prefill_finegrained_q4_k_1100_tokens(gpu):
+    """The fine-grained layer's shape (hidden 2048, ffn 768, 128 experts, top-8,
+    Q4_K, Zipf(1.2) router bias) at 1100 tokens: the single-split down GEMM,
+    bucketing over two 1024-token chunks, and experts with no pair, one pair
+    and more than one 192-pair row tile."""
+    lw = wl.make_layer(2048, 768, 128, 8, wl.Q4_K, 41, zipf_s=1.2)
+    x = wl.inputs(2048, 1100, 42)
+    norm_ratio, max_ratio = check_prefill(gpu, lw, x)
+    print(f"finegrained q4_k 1100 tokens: norm ratio {norm_ratio:.3e}, max ratio {max_ratio:.3e}")
+
+
+def test_prefill_mixed_block_types(gpu):
+    """Gate/up and down in different block types (Q4_K gate/up with Q8_0 down,
+    Q8_0 gate/up with Q4_0 down)."""
+    for seed, (gt, dt) in enumerate(((wl.Q4_K, wl.Q8_0), (wl.Q8_0, wl.Q4_0))):
+        lw = wl.make_layer(512, 512, 8, 2, gt, 60 + seed, down_type=dt)
+        x = wl.inputs(512, 80, 70 + seed)
+        check_prefill(gpu, lw, x)
 
 
 def test_prefill_untiled_shape_runs_decode_kernels(gpu):
