@@ -8,6 +8,7 @@
 #include <atomic>
 #include <chrono>
 #include <cstdio>
+#include <mutex>
 #include <thread>
 
 namespace fmx {
@@ -99,6 +100,58 @@ int validate_layer(const fmx_moe_layer *L) {
     if (L->router_type != FMX_TYPE_F32 && L->router_type != FMX_TYPE_Q4_0 && L->router_type != FMX_TYPE_Q8_0 &&
         L->router_type != FMX_TYPE_Q4_K)
         return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    return FMX_OK;
+}
+
+// The decode sequence of fmx_moe_decode for `tokens` rows of x, with the
+// one-token workspace at `base` (layout of decode_workspace) and the error
+// word at `status`. Arguments are validated by the caller.
+int decode_tokens(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
+                  float *weights, uint8_t *base, uint32_t *status, hipStream_t s) {
+    RouteArgs ra;
+    if (int rc = prepare_route_args(L, &ra)) return rc;
+    ExpertArgs ea;
+    if (int rc = prepare_expert_args(L, ra, &ea)) return rc;
+    const DecodeWorkspace ws = decode_workspace(L, 1);
+    float *h = reinterpret_cast<float *>(base + ws.h);
+    float *lg = reinterpret_cast<float *>(base + ws.logits);
+    DecodeScratch sc;
+    sc.act = reinterpret_cast<float *>(base + ws.act);
+    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
+    FMX_LAUNCH_CHECK();
+    const uint64_t H = L->hidden, K = L->top_k;
+    for (uint32_t t = 0; t < tokens; ++t) {
+        if (int rc = launch_route_logits(ra, x + t * H, 1, h, lg, s)) return rc;
+        if (int rc = launch_experts(ea, x + t * H, h, lg, ids + t * K, weights + t * K, sc, out + t * H, status, s))
+            return rc;
+    }
+    return FMX_OK;
+}
+
+// The decode workspace of fmx_moe_decode_static: a device array of fixed size
+// that every call on one GPU shares. Each GPU holds its own copy at its own
+// address; host code uses that address (from hipGetSymbolAddress, looked up
+// once per device), never the array's name, which on the host is only a
+// stand-in.
+static __device__ __align__(256) uint8_t scratch[FMX_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+uint8_t *g_scratch_ptr[kMaxDevices];
+
+// `scratch` of the current device.
+int static_scratch(uint8_t **ptr) {
+    int dev = 0;
+    FMX_HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return FMX_ERR_NO_DEVICE;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        FMX_HIP_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return FMX_ERR_LAUNCH_FAILED;
+        g_scratch_ptr[dev] = static_cast<uint8_t *>(p);
+    }
+    *ptr = g_scratch_ptr[dev];
     return FMX_OK;
 }
 
@@ -353,28 +406,24 @@ int fmx_moe_decode(const fmx_moe_layer *L, const float *x, float *out, uint32_t 
     if (tokens == 0) return FMX_OK;
     if (!x || !out || !ids || !weights || !workspace) return FMX_ERR_INVALID_ARGUMENT;
     if (!aligned16(x) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
-    const DecodeWorkspace ws = decode_workspace(L, 1);
-    if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
-    RouteArgs ra;
-    if (int rc = prepare_route_args(L, &ra)) return rc;
-    ExpertArgs ea;
-    if (int rc = prepare_expert_args(L, ra, &ea)) return rc;
-    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (workspace_bytes < decode_workspace(L, 1).total) return FMX_ERR_INVALID_ARGUMENT;
     uint8_t *base = static_cast<uint8_t *>(workspace);
-    uint32_t *status = reinterpret_cast<uint32_t *>(base);
-    float *h = reinterpret_cast<float *>(base + ws.h);
-    float *lg = reinterpret_cast<float *>(base + ws.logits);
-    DecodeScratch sc;
-    sc.act = reinterpret_cast<float *>(base + ws.act);
-    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
-    FMX_LAUNCH_CHECK();
-    const uint64_t H = L->hidden, K = L->top_k;
-    for (uint32_t t = 0; t < tokens; ++t) {
-        if (int rc = launch_route_logits(ra, x + t * H, 1, h, lg, s)) return rc;
-        if (int rc = launch_experts(ea, x + t * H, h, lg, ids + t * K, weights + t * K, sc, out + t * H, status, s))
-            return rc;
-    }
-    return FMX_OK;
+    return decode_tokens(L, x, out, tokens, ids, weights, base, reinterpret_cast<uint32_t *>(base),
+                         static_cast<hipStream_t>(stream));
+}
+
+int fmx_moe_decode_static(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
+                          float *weights, uint32_t *status, void *stream) {
+    if (int rc = fault_gate()) return rc;
+    if (int rc = validate_layer(L)) return rc;
+    if (tokens == 0) return FMX_OK;
+    if (!x || !out || !ids || !weights) return FMX_ERR_INVALID_ARGUMENT;
+    if (!aligned16(x)) return FMX_ERR_INVALID_ARGUMENT;
+    if (decode_workspace(L, 1).total > FMX_STATIC_SCRATCH_BYTES) return FMX_ERR_SHAPE_MISMATCH;
+    uint8_t *base = nullptr;
+    if (int rc = static_scratch(&base)) return rc;
+    return decode_tokens(L, x, out, tokens, ids, weights, base, status ? status : reinterpret_cast<uint32_t *>(base),
+                         static_cast<hipStream_t>(stream));
 }
 
 int fmx_moe_decode_timed(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,

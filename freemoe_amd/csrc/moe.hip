@@ -29,7 +29,6 @@
 #include <hip/hip_ext.h>
 
 #include <mutex>
-#include <vector>
 
 namespace fmx {
 
@@ -914,20 +913,25 @@ int launch_experts_gu(const ExpertArgs &a, const float *x, const float *h, const
 
 // Raises the dynamic LDS limit of kernel `fn` (64 KiB by default) to `bytes`
 // when a launch needs more; the limit only grows, and each kernel's is kept.
+// The table is a fixed array (no allocation on a compute call); a kernel past
+// its capacity has its attribute set on every such launch instead.
 int allow_lds(const void *fn, size_t bytes) {
     if (bytes <= 64 * 1024) return FMX_OK;
+    constexpr int kKernels = 256;
     static std::mutex mu;
-    static std::vector<std::pair<const void *, size_t>> limits;
+    static const void *fns[kKernels];
+    static size_t limits[kKernels];
+    static int used = 0;
     std::lock_guard<std::mutex> lock(mu);
-    for (auto &f : limits)
-        if (f.first == fn) {
-            if (f.second >= bytes) return FMX_OK;
-            FMX_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
-            f.second = bytes;
-            return FMX_OK;
-        }
+    int i = 0;
+    while (i < used && fns[i] != fn) ++i;
+    if (i < used && limits[i] >= bytes) return FMX_OK;
     FMX_HIP_TRY(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes)));
-    limits.emplace_back(fn, bytes);
+    if (i == used && used < kKernels) ++used;
+    if (i < used) {
+        fns[i] = fn;
+        limits[i] = bytes;
+    }
     return FMX_OK;
 }
 

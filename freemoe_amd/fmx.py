@@ -71,6 +71,8 @@ _SIGNATURES = {
                               c_void_p, c_uint64, c_void_p]),
     "fmx_moe_decode": (c_int, [POINTER(MoELayer), c_void_p, c_void_p, c_uint32, c_void_p, c_void_p, c_void_p,
                                c_uint64, c_void_p]),
+    "fmx_moe_decode_static": (c_int, [POINTER(MoELayer), c_void_p, c_void_p, c_uint32, c_void_p, c_void_p,
+                                      c_void_p, c_void_p]),
     "fmx_moe_decode_timed": (c_int, [POINTER(MoELayer), c_void_p, c_void_p, c_uint32, c_void_p, c_void_p,
                                      c_void_p, c_uint64, c_void_p, POINTER(c_double)]),
     "fmx_moe_prefill_workspace_bytes": (c_uint64, [POINTER(MoELayer), c_uint32]),

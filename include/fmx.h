@@ -181,6 +181,23 @@ int fmx_moe_decode(const fmx_moe_layer *layer, const float *x, float *out, uint3
                    uint32_t *ids, float *weights, void *workspace, uint64_t workspace_bytes,
                    void *stream);
 
+/* fmx_moe_decode for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). No
+ * counterpart in the reference. It allocates nothing: its workspace is a
+ * device array of FMX_STATIC_SCRATCH_BYTES inside the library, one per GPU,
+ * held until the process ends. A layer whose decode workspace
+ * (fmx_moe_workspace_bytes(layer, 1)) exceeds that is refused with
+ * FMX_ERR_SHAPE_MISMATCH before anything is launched. `status` (device, 4
+ * bytes, may be NULL) receives the error word fmx_moe_status would read
+ * (cleared first; bit 0: a non-finite router score, INTERNAL_ERROR; bit 1: an
+ * expert id out of range, INVALID_ARGUMENT). Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (two streams, two threads)
+ * race and must be ordered by the caller. Results equal fmx_moe_decode's bit
+ * for bit. */
+#define FMX_STATIC_SCRATCH_BYTES (4u << 20)
+int fmx_moe_decode_static(const fmx_moe_layer *layer, const float *x, float *out, uint32_t tokens,
+                          uint32_t *ids, float *weights, uint32_t *status, void *stream);
+
 /* Instrumented fmx_moe_decode (no reference counterpart; for measurement):
  * the same launches on `stream`, timed with HIP events: kernel_ms[0] sums the
  * interval between events recorded before and after each routing launch;

@@ -99,3 +99,19 @@ def test_argument_checks_run_before_any_launch():
     desc.hidden, desc.ffn, desc.experts, desc.top_k = 64, 128, 4, 5   # top_k > experts
     assert lib.fmx_moe_decode(ctypes.byref(desc), None, None, 1, None, None, None, 0, None) == 1
     assert lib.fmx_moe_bucket(None, 4, 2, 300, None, None, None, None, 0, None) == 1  # > 256 experts
+
+
+def test_decode_static_refuses_oversized_layers():
+    """fmx_moe_decode_static checks its fixed workspace on the host, before
+    anything is launched: a layer whose one-token decode workspace exceeds
+    FMX_STATIC_SCRATCH_BYTES (4 MiB) is refused with SHAPE_MISMATCH."""
+    import ctypes
+    import numpy as np
+    from freemoe_amd import fmx
+    lib = fmx.lib()
+    buf = np.zeros(64, np.float32)  # any non-null, 16-byte aligned address; never read
+    p = buf.ctypes.data + (-buf.ctypes.data) % 16
+    layer = fmx.MoELayer(16384, 40000, 32, 32, 0, 1e-5, 0.0, 0, p, 0, 1, 0, 6.103515625e-5, 1.0, 2, 2, 2, p, p, p)
+    assert lib.fmx_moe_workspace_bytes(ctypes.byref(layer), 1) > (4 << 20)
+    rc = lib.fmx_moe_decode_static(ctypes.byref(layer), p, p, 1, p, p, 0, None)
+    assert rc == 3  # FMX_ERR_SHAPE_MISMATCH
