@@ -18,7 +18,10 @@ from .workloads import LayerWeights
 
 
 def to_device(a: np.ndarray, device) -> torch.Tensor:
-    return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    a = np.ascontiguousarray(a)
+    if not a.flags.writeable:  # a read-only memory map (a checkpoint's bytes)
+        a = a.copy()
+    return torch.from_numpy(a).to(device)
 
 
 def pack(type_id: int, raw: torch.Tensor, rows: int, cols: int, stream=None) -> torch.Tensor:

@@ -144,3 +144,32 @@ def workload(name: str, seed: int = 1234):
     tokens = w.pop("tokens")
     layer = make_layer(seed=seed, **w)
     return layer, inputs(layer.hidden, tokens, seed + 1)
+
+
+def tiny_checkpoint(seed: int = 2026):
+    """The freemoe-tiny-v1 end-to-end model as a GGUF file object
+    (freemoe_amd.gguf): 2 layers, hidden 64, 4 heads of dim 16, 4 experts with
+    top-2 routing, expert ffn 128, the 258-entry byte vocabulary, F32 weight
+    matrices ~N(0, 0.02) (norm gains 1 + N(0, 0.02)), seeded."""
+    from . import gguf
+
+    H, F, E, K, L = 64, 128, 4, 2, 2
+    rng = np.random.default_rng(seed)
+
+    def n(*shape):
+        return (rng.standard_normal(shape) * 0.02).astype(np.float32)
+
+    def gain():
+        return (1.0 + rng.standard_normal(H) * 0.02).astype(np.float32)
+
+    layers = []
+    for _ in range(L):
+        router = n(E, H)
+        gate = [n(F, H) for _ in range(E)]
+        up = [n(F, H) for _ in range(E)]
+        down = [n(H, F) for _ in range(E)]
+        layers.append(dict(attn_norm=gain(), attn_q=n(H, H), attn_k=n(H, H), attn_v=n(H, H), attn_output=n(H, H),
+                           ffn_norm=gain(), moe=gguf.MoEBlock(router, F32, gate, up, down, F32, F32)))
+    vocab = dict(token_embd=n(258, H), output_norm=gain(), output=n(258, H))
+    return gguf.freemoe_tiny(hidden=H, ffn=F, heads=4, experts=E, top_k=K, layers=layers, vocab_tensors=vocab,
+                             seed=seed, name="freemoe-tiny-v1 synthetic")

@@ -86,8 +86,80 @@ def ref() -> ctypes.CDLL:
                                             c_void_p, c_uint32]
         lib.fmr_resolved_threads.restype = c_uint32
         lib.fmr_resolved_threads.argtypes = [c_uint32]
+        lib.fmr_engine_open.restype = c_void_p
+        lib.fmr_engine_open.argtypes = [ctypes.c_char_p, c_int, c_uint32, ctypes.c_char_p, c_uint32]
+        lib.fmr_engine_close.restype = None
+        lib.fmr_engine_close.argtypes = [c_void_p]
+        lib.fmr_engine_prompt.restype = c_int
+        lib.fmr_engine_prompt.argtypes = [c_void_p, ctypes.c_char_p, c_uint32, c_uint32,
+                                          c_void_p, c_uint32, POINTER(c_uint32), c_void_p, c_uint32,
+                                          POINTER(c_uint32), c_void_p, c_uint32, POINTER(c_uint32),
+                                          c_void_p, c_uint32, c_uint32, POINTER(c_uint32),
+                                          ctypes.c_char_p, c_uint32]
+        lib.fmr_manifest_probe.restype = c_int
+        lib.fmr_manifest_probe.argtypes = [ctypes.c_char_p, c_void_p, c_void_p, c_void_p, c_uint32,
+                                           ctypes.c_char_p, c_uint32]
         _ref = lib
     return _ref
+
+
+def ref_manifest(path, cap: int = 4096) -> dict:
+    """The reference's parse_gguf + build_manifest on a checkpoint: its
+    layer / expert / top-k / hidden counts, slot and fixed-weight bytes, and
+    per expert record (layer, expert) and three extents (offset, bytes,
+    type)."""
+    info = np.zeros(9, np.uint32)
+    ext = np.zeros((cap, 3, 3), np.uint64)
+    who = np.zeros((cap, 2), np.uint32)
+    err = ctypes.create_string_buffer(512)
+    rc = ref().fmr_manifest_probe(str(path).encode(), _p(info), _p(ext), _p(who), cap, err, 512)
+    if rc:
+        raise OracleError(rc, f"build_manifest: {err.value.decode()}")
+    n = int(info[4])
+    return dict(layers=int(info[0]), experts=int(info[1]), top_k=int(info[2]), hidden=int(info[3]),
+                records=n, slot_bytes=int(info[5]) | int(info[6]) << 32,
+                fixed_weight_bytes=int(info[7]) | int(info[8]) << 32,
+                who=who[:min(n, cap)].copy(), extents=ext[:min(n, cap)].copy())
+
+
+class RefEngine:
+    """The reference's own fm::Engine (compiled from the FreeMoe sources into
+    libfmref) on a checkpoint, CPU backend, one token at a time."""
+
+    def __init__(self, model_path, isa: int = ISA_AVX2, threads: int = 1, top_k: int = 2):
+        err = ctypes.create_string_buffer(512)
+        self.top_k = top_k
+        self.h = ref().fmr_engine_open(str(model_path).encode(), isa, threads, err, 512)
+        if not self.h:
+            raise RuntimeError(f"fm::Engine could not open {model_path}: {err.value.decode()}")
+
+    def close(self):
+        if self.h:
+            ref().fmr_engine_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def run_prompt(self, prompt: bytes, generate: int, vocab_cap: int = 1 << 16):
+        """(input_ids, prefill logits, generated ids, routing rows
+        [position, layer, ids...]) of Engine::run_prompt."""
+        cap = len(prompt) + 2
+        ids = np.empty(cap, np.int32)
+        logits = np.empty(vocab_cap, np.float32)
+        gen = np.empty(max(generate, 1), np.int32)
+        rcap = 64 * (cap + generate)
+        routing = np.empty((rcap, 2 + self.top_k), np.uint32)
+        n_in, n_v, n_g, n_r = c_uint32(), c_uint32(), c_uint32(), c_uint32()
+        err = ctypes.create_string_buffer(512)
+        rc = ref().fmr_engine_prompt(self.h, prompt, len(prompt), generate, _p(ids), cap, ctypes.byref(n_in),
+                                     _p(logits), vocab_cap, ctypes.byref(n_v), _p(gen), max(generate, 1),
+                                     ctypes.byref(n_g), _p(routing), rcap, self.top_k, ctypes.byref(n_r),
+                                     err, 512)
+        if rc:
+            raise OracleError(rc, f"fm::Engine::run_prompt: {err.value.decode()}")
+        return (ids[:n_in.value].copy(), logits[:n_v.value].copy(), gen[:n_g.value].copy(),
+                routing[:n_r.value].copy())
 
 
 def check(rc: int, where: str) -> None:

@@ -1,0 +1,132 @@
+// engine_check — FreeMoe's unchanged fm::Engine with the physical-GPU backend
+// kind served by fm::HipBackend (freemoe_amd/host/backend_factory.cpp), next
+// to the same engine on FreeMoe's CPU backend, in one process.
+//
+// Built by oracle/Makefile (target _ref/engine_check) from this file, the
+// adapter, FreeMoe's sources and libfmx.so. Test infrastructure:
+// tests/test_gpu_engine.py runs it. Every F32 projection of the engine
+// (attention, router, experts, head) goes through Backend::matvec, so on the
+// GPU it runs libfmx's F32 row chains; routing, softmax, top-k, attention and
+// sampling stay the engine's own code.
+//
+//   engine_check compare <model.gguf> <reference_root> <prompts> <generate> <cpu|gpu>
+//       Engine::compare_reference against FreeMoe's goldens; prints one JSON
+//       line (prompts within tolerance, token and routing matches, max abs
+//       diff, and how many operations the backend logged and under which
+//       backend label).
+//   engine_check twin <model.gguf> <prompts> <prompt_len> <generate> <seed>
+//       seeded random byte prompts through a CPU-backend engine and a
+//       GPU-backend engine; prints one JSON line with the largest prompt-logit
+//       difference, the number of logits that differ in any bit, and whether
+//       routing records and greedy ids are identical.
+// Exits non-zero on an engine error.
+#include "fm/engine.hpp"
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+namespace {
+
+fm::RunConfig config_for(const std::string &model, bool gpu) {
+    fm::RunConfig rc;
+    rc.model_path = model;
+    rc.backend.kind = gpu ? fm::BackendKind::PhysicalGPU : fm::BackendKind::ScalarCPU;
+    rc.backend.kernel_isa = fm::KernelIsa::Auto;
+    return rc;
+}
+
+// Operations in the backend's log by the backend label they ran under.
+std::string op_labels(fm::Backend &b) {
+    std::map<std::string, uint64_t> by;
+    for (const auto &op : b.operations()) by[op.backend] += 1;
+    std::string s = "{";
+    for (const auto &kv : by) {
+        if (s.size() > 1) s += ",";
+        s += "\"" + kv.first + "\":" + std::to_string(kv.second);
+    }
+    return s + "}";
+}
+
+int compare(int argc, char **argv) {
+    if (argc < 7) return 2;
+    const bool gpu = std::string(argv[6]) == "gpu";
+    fm::Engine e(config_for(argv[2], gpu));
+    e.initialize();
+    const fm::ComparisonResult r =
+        e.compare_reference(argv[3], static_cast<uint32_t>(std::atoi(argv[4])), static_cast<uint32_t>(std::atoi(argv[5])));
+    std::printf("{\"mode\":\"compare\",\"backend\":\"%s\",\"prompts\":%u,\"within_tolerance\":%u,"
+                "\"token_match\":%u,\"routing_match\":%u,\"matching_tokens\":%llu,\"reference_tokens\":%llu,"
+                "\"max_abs_diff\":%.9g,\"max_rel_diff\":%.9g,\"ops\":%s}\n",
+                e.backend().name().c_str(), r.prompts, r.prompts_within_tolerance, r.prompts_token_match,
+                r.prompts_routing_match, static_cast<unsigned long long>(r.matching_tokens),
+                static_cast<unsigned long long>(r.reference_tokens), r.max_abs_diff, r.max_rel_diff,
+                op_labels(e.backend()).c_str());
+    return 0;
+}
+
+int twin(int argc, char **argv) {
+    if (argc < 7) return 2;
+    const uint32_t prompts = static_cast<uint32_t>(std::atoi(argv[3]));
+    const uint32_t len = static_cast<uint32_t>(std::atoi(argv[4]));
+    const uint32_t gen = static_cast<uint32_t>(std::atoi(argv[5]));
+    uint64_t seed = std::strtoull(argv[6], nullptr, 10);
+    fm::Engine cpu(config_for(argv[2], false)), gpu(config_for(argv[2], true));
+    cpu.initialize();
+    gpu.initialize();
+    double max_diff = 0.0;
+    uint64_t differing = 0, logits = 0, routing_events = 0, generated = 0;
+    bool routing_same = true, ids_same = true;
+    for (uint32_t p = 0; p < prompts; ++p) {
+        std::string prompt(len, '\0');
+        for (auto &c : prompt) {
+            seed = seed * 6364136223846793005ull + 1442695040888963407ull;
+            c = static_cast<char>(seed >> 56);
+        }
+        const fm::PromptResult a = cpu.run_prompt(prompt, gen);
+        const fm::PromptResult b = gpu.run_prompt(prompt, gen);
+        if (a.prefill_logits.size() != b.prefill_logits.size()) return 3;
+        for (size_t i = 0; i < a.prefill_logits.size(); ++i) {
+            uint32_t x, y;
+            std::memcpy(&x, &a.prefill_logits[i], 4);
+            std::memcpy(&y, &b.prefill_logits[i], 4);
+            differing += x != y;
+            max_diff = std::max(max_diff, std::fabs(static_cast<double>(a.prefill_logits[i]) - b.prefill_logits[i]));
+        }
+        logits += a.prefill_logits.size();
+        ids_same = ids_same && a.generated_ids == b.generated_ids && a.input_ids == b.input_ids;
+        generated += a.generated_ids.size();
+        routing_same = routing_same && a.routing.size() == b.routing.size();
+        for (size_t i = 0; routing_same && i < a.routing.size(); ++i)
+            routing_same = a.routing[i].token_index == b.routing[i].token_index &&
+                           a.routing[i].layer == b.routing[i].layer && a.routing[i].experts == b.routing[i].experts;
+        routing_events += a.routing.size();
+    }
+    std::printf("{\"mode\":\"twin\",\"backends\":[\"%s\",\"%s\"],\"prompts\":%u,\"logits\":%llu,"
+                "\"differing_logits\":%llu,\"max_abs_diff\":%.9g,\"routing_events\":%llu,\"routing_identical\":%s,"
+                "\"generated\":%llu,\"ids_identical\":%s,\"gpu_ops\":%s}\n",
+                cpu.backend().name().c_str(), gpu.backend().name().c_str(), prompts,
+                static_cast<unsigned long long>(logits), static_cast<unsigned long long>(differing), max_diff,
+                static_cast<unsigned long long>(routing_events), routing_same ? "true" : "false",
+                static_cast<unsigned long long>(generated), ids_same ? "true" : "false",
+                op_labels(gpu.backend()).c_str());
+    return 0;
+}
+
+} // namespace
+
+int main(int argc, char **argv) {
+    try {
+        if (argc >= 2 && std::string(argv[1]) == "compare") return compare(argc, argv);
+        if (argc >= 2 && std::string(argv[1]) == "twin") return twin(argc, argv);
+    } catch (const fm::Error &e) {
+        std::fprintf(stderr, "engine_check: %s: %s\n", fm::error_name(e.code), e.what());
+        return 1;
+    }
+    std::fprintf(stderr, "usage: engine_check compare|twin ...\n");
+    return 2;
+}

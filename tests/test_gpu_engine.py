@@ -1,0 +1,67 @@
+"""FreeMoe's unchanged fm::Engine with the physical-GPU backend kind served by
+fm::HipBackend (oracle/_ref/engine_check, built from tests/engine_check.cpp,
+the adapter, FreeMoe's sources and libfmx.so).
+
+  * compare_reference on FreeMoe's own MoE fixture (tests/golden/
+    freemoe_reference: moe-fm.gguf, 20 prompts with their logits, greedy ids and
+    routing records, copied as data): every prompt within the reference's 5e-3,
+    every greedy id and every routing event equal;
+  * the freemoe-tiny-v1 end-to-end model (2 layers, hidden 64, 4 experts top-2,
+    ffn 128, F32 ~N(0, 0.02)), 64-token seeded byte prompts and 32 greedy
+    tokens, on the CPU backend and on HipBackend in one process: prompt logits
+    identical bit for bit, routing records and greedy ids identical.
+"""
+import json
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from freemoe_amd import workloads as wl
+
+ROOT = Path(__file__).resolve().parents[1]
+CHECK = ROOT / "oracle" / "_ref" / "engine_check"
+FIXTURES = ROOT / "tests" / "golden" / "freemoe_reference"
+
+
+def run(*args, timeout=600):
+    if not CHECK.exists():
+        pytest.skip("oracle/_ref/engine_check not built (needs the FreeMoe tree at build time)")
+    proc = subprocess.run([str(CHECK), *map(str, args)], capture_output=True, text=True, timeout=timeout)
+    assert proc.returncode == 0, proc.stdout + proc.stderr
+    return json.loads(proc.stdout.strip().splitlines()[-1])
+
+
+def check_compare(r, prompts):
+    assert r["prompts"] == prompts
+    assert r["within_tolerance"] == prompts and r["token_match"] == prompts and r["routing_match"] == prompts, r
+    assert r["matching_tokens"] == r["reference_tokens"] > 0
+
+
+def test_unchanged_engine_compare_reference_cpu():
+    """The same binary on FreeMoe's CPU backend reproduces FreeMoe's goldens
+    (the baseline the GPU run is held to)."""
+    r = run("compare", FIXTURES / "moe-fm.gguf", FIXTURES, 20, 16, "cpu")
+    check_compare(r, 20)
+
+
+@pytest.mark.gpu
+def test_unchanged_engine_compare_reference_on_hip_backend(gpu):
+    r = run("compare", FIXTURES / "moe-fm.gguf", FIXTURES, 20, 16, "gpu")
+    print(r)
+    assert r["backend"] == "hip-gfx950"
+    check_compare(r, 20)
+    assert r["ops"].get("hip-gfx950", 0) > 0  # the projections ran on the device
+
+
+@pytest.mark.gpu
+def test_tiny_model_end_to_end_cpu_and_hip_identical(gpu, tmp_path):
+    path = tmp_path / "freemoe-tiny-v1.gguf"
+    wl.tiny_checkpoint().write(path)
+    r = run("twin", path, 4, 64, 32, 7)
+    print(r)
+    assert r["backends"] == ["cpu", "hip-gfx950"]
+    assert r["differing_logits"] == 0 and r["max_abs_diff"] == 0.0
+    assert r["routing_identical"] and r["ids_identical"]
+    assert r["generated"] == 4 * 32 and r["routing_events"] == 4 * (65 + 32) * 2
+    assert r["gpu_ops"].get("hip-gfx950", 0) > 0
