@@ -35,24 +35,112 @@ int fmx_fault_of(BackendFault f) {
     return FMX_FAULT_NONE;
 }
 
-} // namespace
-
-HipBackend::HipBackend(BackendConfig config, TraceWriter *trace) : Backend(std::move(config), trace) {
-    fmx_device_info info;
-    have_device_ = fmx_device_info_get(0, &info) == FMX_OK;
-}
-
-HipBackend::~HipBackend() {
-    std::lock_guard<std::mutex> lock(mutex_);
-    for (auto &f : fences_) fmx_fence_release(f.second);
-    for (auto &p : packed_) fmx_free(p.second);
-    fmx_free(x_dev_);
-    fmx_free(y_dev_);
-}
-
-void HipBackend::check(int status, const std::string &where) const {
+void check_status(int status, const std::string &where) {
     if (status != FMX_OK) fail(code_of(status), where + ": " + fmx_status_name(status));
 }
+
+uint64_t raw_bytes(uint32_t type_id, uint32_t rows, uint32_t cols) {
+    uint32_t bs = 0, bb = 0;
+    if (fmx_quant_geometry(type_id, &bs, &bb) != FMX_OK || cols % bs) return 0;
+    return static_cast<uint64_t>(rows) * (cols / bs) * bb;
+}
+
+} // namespace
+
+// Device-side state shared by the backend and every buffer it hands out.
+struct HipBackend::State {
+    struct Twin {
+        void *device = nullptr;
+        uint64_t bytes = 0;
+    };
+    std::mutex mutex;
+    std::map<uintptr_t, Twin> twins;                                           // host mirror start -> twin
+    std::map<std::tuple<uintptr_t, uint32_t, uint32_t, uint32_t>, void *> packed; // packed block matrices
+    std::map<uint64_t, void *> fences;                                         // fence id -> fmx fence
+    uint64_t next_fence = 1;
+    void *stream = nullptr; // the default stream
+    bool have_device = false;
+    // matvec / MoE scratch
+    void *x_dev = nullptr, *y_dev = nullptr;
+    uint64_t x_cap = 0, y_cap = 0;
+    void *moe_ws = nullptr, *moe_small = nullptr;
+    uint64_t moe_ws_cap = 0, moe_small_cap = 0;
+    std::map<std::vector<uintptr_t>, void *> slot_tables; // packed expert pointers -> device table
+
+    ~State() {
+        for (auto &f : fences) fmx_fence_release(f.second);
+        for (auto &p : packed) fmx_free(p.second);
+        for (auto &t : slot_tables) fmx_free(t.second);
+        fmx_free(x_dev);
+        fmx_free(y_dev);
+        fmx_free(moe_ws);
+        fmx_free(moe_small);
+    }
+
+    const Twin *find_twin(const void *host, uint64_t *offset) const {
+        const uintptr_t p = reinterpret_cast<uintptr_t>(host);
+        auto it = twins.upper_bound(p);
+        if (it == twins.begin()) return nullptr;
+        --it;
+        if (p - it->first >= it->second.bytes) return nullptr;
+        *offset = p - it->first;
+        return &it->second;
+    }
+
+    // Drops the packed copies (and the slot tables that point at them) of
+    // matrices inside [lo, lo + bytes): the buffer was refilled or released.
+    void drop_packed(uintptr_t lo, uint64_t bytes) {
+        bool dropped = false;
+        for (auto it = packed.begin(); it != packed.end();) {
+            if (std::get<0>(it->first) >= lo && std::get<0>(it->first) < lo + bytes) {
+                fmx_free(it->second);
+                it = packed.erase(it);
+                dropped = true;
+            } else {
+                ++it;
+            }
+        }
+        if (dropped) {
+            for (auto &t : slot_tables) fmx_free(t.second);
+            slot_tables.clear();
+        }
+    }
+
+    // The packed device copy of a [rows x cols] matrix of `type_id` stored in a
+    // buffer at host address `weights` (made once, kept until the buffer is
+    // refilled or released). F32 copies are 16-byte aligned raw copies.
+    void *packed_twin(uint32_t type_id, const void *weights, uint32_t rows, uint32_t cols) {
+        const auto key = std::make_tuple(reinterpret_cast<uintptr_t>(weights), type_id, rows, cols);
+        auto it = packed.find(key);
+        if (it != packed.end()) return it->second;
+        uint64_t off = 0;
+        const Twin *t = find_twin(weights, &off);
+        const uint64_t need = raw_bytes(type_id, rows, cols);
+        if (!t || need == 0 || off + need > t->bytes)
+            fail(ErrorCode::INVALID_ARGUMENT, "weights are not in a device buffer of this backend");
+        const uint64_t n = fmx_packed_bytes(type_id, rows, cols);
+        if (n == 0) fail(ErrorCode::SHAPE_MISMATCH, "no packed layout for this shape");
+        void *p = nullptr;
+        check_status(fmx_alloc(n, &p), "packed weights");
+        const int rc = fmx_pack(type_id, static_cast<uint8_t *>(t->device) + off, p, rows, cols, stream);
+        if (rc != FMX_OK) {
+            fmx_free(p);
+            check_status(rc, "pack");
+        }
+        packed[key] = p;
+        return p;
+    }
+};
+
+HipBackend::HipBackend(BackendConfig config, TraceWriter *trace)
+    : Backend(std::move(config), trace), state_(std::make_shared<State>()) {
+    fmx_device_info fi;
+    state_->have_device = fmx_device_info_get(0, &fi) == FMX_OK;
+}
+
+HipBackend::~HipBackend() = default; // buffers still out hold the state
+
+void HipBackend::check(int status, const std::string &where) const { check_status(status, where); }
 
 DeviceInfo HipBackend::info() const {
     DeviceInfo d;
@@ -78,7 +166,7 @@ DeviceInfo HipBackend::info() const {
 }
 
 std::unique_ptr<DeviceBuffer> HipBackend::allocate(uint64_t bytes, AllocationTag tag) {
-    if (!have_device_) fail(ErrorCode::GPU_BACKEND_UNIMPLEMENTED, "no MI355X (gfx950) device visible");
+    if (!state_->have_device) fail(ErrorCode::GPU_BACKEND_UNIMPLEMENTED, "no MI355X (gfx950) device visible");
     if (fault_ == BackendFault::DeviceLoss) fail(ErrorCode::DEVICE_LOSS, "injected device loss");
     void *host = nullptr, *dev = nullptr;
     check(fmx_host_alloc(bytes, &host), "pinned host mirror");
@@ -88,8 +176,8 @@ std::unique_ptr<DeviceBuffer> HipBackend::allocate(uint64_t bytes, AllocationTag
         check(rc, "HBM allocation");
     }
     {
-        std::lock_guard<std::mutex> lock(mutex_);
-        twins_[reinterpret_cast<uintptr_t>(host)] = Twin{dev, bytes};
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        state_->twins[reinterpret_cast<uintptr_t>(host)] = State::Twin{dev, bytes};
     }
     auto buffer = std::make_unique<DeviceBuffer>();
     buffer->data = host;
@@ -97,21 +185,11 @@ std::unique_ptr<DeviceBuffer> HipBackend::allocate(uint64_t bytes, AllocationTag
     buffer->tag = tag;
     auto tracker = tracker_;
     buffer->allocation_id = tracker->allocate(tag, bytes);
-    // The closure frees this backend's twin too, so buffers must not outlive
-    // the backend (the engine and residency release theirs first).
-    buffer->cleanup = [this, tracker, id = buffer->allocation_id, host, dev, bytes]() {
+    buffer->cleanup = [state = state_, tracker, id = buffer->allocation_id, host, dev, bytes]() {
         {
-            std::lock_guard<std::mutex> lock(mutex_);
-            twins_.erase(reinterpret_cast<uintptr_t>(host));
-            const uintptr_t lo = reinterpret_cast<uintptr_t>(host);
-            for (auto it = packed_.begin(); it != packed_.end();) {
-                if (std::get<0>(it->first) >= lo && std::get<0>(it->first) < lo + bytes) {
-                    fmx_free(it->second);
-                    it = packed_.erase(it);
-                } else {
-                    ++it;
-                }
-            }
+            std::lock_guard<std::mutex> lock(state->mutex);
+            state->twins.erase(reinterpret_cast<uintptr_t>(host));
+            state->drop_packed(reinterpret_cast<uintptr_t>(host), bytes);
         }
         tracker->free(id);
         fmx_free(dev);
@@ -120,20 +198,10 @@ std::unique_ptr<DeviceBuffer> HipBackend::allocate(uint64_t bytes, AllocationTag
     return buffer;
 }
 
-const HipBackend::Twin *HipBackend::find_twin(const void *host, uint64_t *offset) const {
-    const uintptr_t p = reinterpret_cast<uintptr_t>(host);
-    auto it = twins_.upper_bound(p);
-    if (it == twins_.begin()) return nullptr;
-    --it;
-    if (p - it->first >= it->second.bytes) return nullptr;
-    *offset = p - it->first;
-    return &it->second;
-}
-
 void *HipBackend::device_address(const void *host) const {
-    std::lock_guard<std::mutex> lock(mutex_);
+    std::lock_guard<std::mutex> lock(state_->mutex);
     uint64_t off = 0;
-    const Twin *t = find_twin(host, &off);
+    const State::Twin *t = state_->find_twin(host, &off);
     return t ? static_cast<uint8_t *>(t->device) + off : nullptr;
 }
 
@@ -141,36 +209,28 @@ Fence HipBackend::upload(DeviceBuffer &buffer, const void *src, uint64_t bytes) 
     if (fault_ == BackendFault::TransferFailure) fail(ErrorCode::TRANSFER_FAILED, "injected transfer failure");
     if (fault_ == BackendFault::DeviceLoss) fail(ErrorCode::DEVICE_LOSS, "injected device loss");
     if (!buffer.data || bytes > buffer.bytes || (!src && bytes)) fail(ErrorCode::INVALID_ARGUMENT, "bad upload");
-    std::lock_guard<std::mutex> lock(mutex_);
+    std::lock_guard<std::mutex> lock(state_->mutex);
     uint64_t off = 0;
-    const Twin *t = find_twin(buffer.data, &off);
+    const State::Twin *t = state_->find_twin(buffer.data, &off);
     if (!t) fail(ErrorCode::INVALID_ARGUMENT, "upload into a buffer this backend did not allocate");
     if (bytes) std::memcpy(buffer.data, src, static_cast<size_t>(bytes));
     // a refilled buffer (an expert slot reused for another expert) drops its packed copies
-    const uintptr_t lo = reinterpret_cast<uintptr_t>(buffer.data);
-    for (auto it = packed_.begin(); it != packed_.end();) {
-        if (std::get<0>(it->first) >= lo && std::get<0>(it->first) < lo + buffer.bytes) {
-            fmx_free(it->second);
-            it = packed_.erase(it);
-        } else {
-            ++it;
-        }
-    }
+    state_->drop_packed(reinterpret_cast<uintptr_t>(buffer.data), buffer.bytes);
     void *ev = nullptr;
-    check(fmx_upload(static_cast<uint8_t *>(t->device) + off, buffer.data, bytes, stream_, &ev), "upload");
+    check(fmx_upload(static_cast<uint8_t *>(t->device) + off, buffer.data, bytes, state_->stream, &ev), "upload");
     Fence f;
-    f.id = next_fence_++;
+    f.id = state_->next_fence++;
     f.ready_at_ms = now_ms();
     f.deferred = fault_ == BackendFault::FenceDeferred;
-    fences_[f.id] = ev;
+    state_->fences[f.id] = ev;
     return f;
 }
 
 bool HipBackend::fence_complete(const Fence &fence) const {
     if (fence.deferred && fault_ == BackendFault::FenceDeferred) return false;
-    std::lock_guard<std::mutex> lock(mutex_);
-    auto it = fences_.find(fence.id);
-    if (it == fences_.end()) return true; // already waited on and released
+    std::lock_guard<std::mutex> lock(state_->mutex);
+    auto it = state_->fences.find(fence.id);
+    if (it == state_->fences.end()) return true; // already waited on and released
     int done = 0;
     check(fmx_fence_query(it->second, &done), "fence query");
     return done != 0;
@@ -184,30 +244,33 @@ void HipBackend::wait_fence(const Fence &fence, uint32_t timeout_ms) {
     }
     void *ev = nullptr;
     {
-        std::lock_guard<std::mutex> lock(mutex_);
-        auto it = fences_.find(fence.id);
-        if (it == fences_.end()) return;
+        std::lock_guard<std::mutex> lock(state_->mutex);
+        auto it = state_->fences.find(fence.id);
+        if (it == state_->fences.end()) return;
         ev = it->second;
     }
     if (fence.deferred) Backend::wait_fence(fence, timeout_ms); // polls fence_complete until timeout
     check(fmx_fence_wait(ev, timeout_ms), "fence " + std::to_string(fence.id));
-    std::lock_guard<std::mutex> lock(mutex_);
-    fences_.erase(fence.id);
+    std::lock_guard<std::mutex> lock(state_->mutex);
+    state_->fences.erase(fence.id);
     fmx_fence_release(ev);
 }
 
 void HipBackend::ensure_scratch(uint64_t x_bytes, uint64_t y_bytes) {
-    if (x_bytes > x_cap_) {
-        fmx_free(x_dev_);
-        x_dev_ = nullptr;
-        check(fmx_alloc(x_bytes, &x_dev_), "matvec input");
-        x_cap_ = x_bytes;
+    State &s = *state_;
+    if (x_bytes > s.x_cap) {
+        fmx_free(s.x_dev);
+        s.x_dev = nullptr;
+        s.x_cap = 0;
+        check(fmx_alloc(x_bytes, &s.x_dev), "matvec input");
+        s.x_cap = x_bytes;
     }
-    if (y_bytes > y_cap_) {
-        fmx_free(y_dev_);
-        y_dev_ = nullptr;
-        check(fmx_alloc(y_bytes, &y_dev_), "matvec output");
-        y_cap_ = y_bytes;
+    if (y_bytes > s.y_cap) {
+        fmx_free(s.y_dev);
+        s.y_dev = nullptr;
+        s.y_cap = 0;
+        check(fmx_alloc(y_bytes, &s.y_dev), "matvec output");
+        s.y_cap = y_bytes;
     }
 }
 
@@ -216,42 +279,20 @@ void HipBackend::matvec(const float *weights, const float *x, float *y, uint32_t
     if (fault_ == BackendFault::DeviceLoss) fail(ErrorCode::DEVICE_LOSS, "injected device loss");
     if (!weights || !x || !y || out_dim == 0 || in_dim == 0)
         fail(ErrorCode::INVALID_ARGUMENT, "invalid matvec arguments");
-    std::lock_guard<std::mutex> lock(mutex_);
+    std::lock_guard<std::mutex> lock(state_->mutex);
+    State &s = *state_;
     uint64_t off = 0;
-    const Twin *t = find_twin(weights, &off);
+    const State::Twin *t = s.find_twin(weights, &off);
     if (!t || off + static_cast<uint64_t>(out_dim) * in_dim * 4 > t->bytes)
         fail(ErrorCode::INVALID_ARGUMENT, "matvec weights are not in a device buffer: " + op_name);
     ensure_scratch(static_cast<uint64_t>(in_dim) * 4, static_cast<uint64_t>(out_dim) * 4);
-    check(fmx_upload(x_dev_, x, static_cast<uint64_t>(in_dim) * 4, stream_, nullptr), op_name);
-    check(fmx_matvec(FMX_TYPE_F32, static_cast<uint8_t *>(t->device) + off, static_cast<const float *>(x_dev_),
-                     static_cast<float *>(y_dev_), out_dim, in_dim, stream_),
+    check(fmx_upload(s.x_dev, x, static_cast<uint64_t>(in_dim) * 4, s.stream, nullptr), op_name);
+    check(fmx_matvec(FMX_TYPE_F32, static_cast<uint8_t *>(t->device) + off, static_cast<const float *>(s.x_dev),
+                     static_cast<float *>(s.y_dev), out_dim, in_dim, s.stream),
           op_name);
-    check(fmx_download(y, y_dev_, static_cast<uint64_t>(out_dim) * 4, stream_), op_name);
+    check(fmx_download(y, s.y_dev, static_cast<uint64_t>(out_dim) * 4, s.stream), op_name);
     record_operation({op_name, name(), (static_cast<uint64_t>(out_dim) * in_dim + in_dim) * sizeof(float),
                       static_cast<uint64_t>(out_dim) * sizeof(float)});
-}
-
-void *HipBackend::packed_twin(uint32_t type_id, const void *weights, uint32_t rows, uint32_t cols) {
-    const auto key = std::make_tuple(reinterpret_cast<uintptr_t>(weights), type_id, rows, cols);
-    auto it = packed_.find(key);
-    if (it != packed_.end()) return it->second;
-    uint64_t off = 0;
-    const Twin *t = find_twin(weights, &off);
-    uint32_t bs = 0, bb = 0;
-    check(fmx_quant_geometry(type_id, &bs, &bb), "block geometry");
-    if (!t || cols % bs || off + static_cast<uint64_t>(rows) * (cols / bs) * bb > t->bytes)
-        fail(ErrorCode::INVALID_ARGUMENT, "quantised weights are not in a device buffer");
-    const uint64_t n = fmx_packed_bytes(type_id, rows, cols);
-    if (n == 0) fail(ErrorCode::SHAPE_MISMATCH, "no packed layout for this shape");
-    void *packed = nullptr;
-    check(fmx_alloc(n, &packed), "packed weights");
-    const int rc = fmx_pack(type_id, static_cast<uint8_t *>(t->device) + off, packed, rows, cols, stream_);
-    if (rc != FMX_OK) {
-        fmx_free(packed);
-        check(rc, "pack");
-    }
-    packed_[key] = packed;
-    return packed;
 }
 
 void HipBackend::matvec_quant(uint32_t type_id, const void *weights, const float *x, float *y, uint32_t out_dim,
@@ -263,18 +304,144 @@ void HipBackend::matvec_quant(uint32_t type_id, const void *weights, const float
     if (fault_ == BackendFault::DeviceLoss) fail(ErrorCode::DEVICE_LOSS, "injected device loss");
     if (!weights || !x || !y || out_dim == 0 || in_dim == 0)
         fail(ErrorCode::INVALID_ARGUMENT, "invalid matvec arguments");
-    std::lock_guard<std::mutex> lock(mutex_);
-    void *packed = packed_twin(type_id, weights, out_dim, in_dim);
+    std::lock_guard<std::mutex> lock(state_->mutex);
+    State &s = *state_;
+    void *packed = s.packed_twin(type_id, weights, out_dim, in_dim);
     ensure_scratch(static_cast<uint64_t>(in_dim) * 4, static_cast<uint64_t>(out_dim) * 4);
-    check(fmx_upload(x_dev_, x, static_cast<uint64_t>(in_dim) * 4, stream_, nullptr), op_name);
-    check(fmx_matvec(type_id, packed, static_cast<const float *>(x_dev_), static_cast<float *>(y_dev_), out_dim,
-                     in_dim, stream_),
+    check(fmx_upload(s.x_dev, x, static_cast<uint64_t>(in_dim) * 4, s.stream, nullptr), op_name);
+    check(fmx_matvec(type_id, packed, static_cast<const float *>(s.x_dev), static_cast<float *>(s.y_dev), out_dim,
+                     in_dim, s.stream),
           op_name);
-    check(fmx_download(y, y_dev_, static_cast<uint64_t>(out_dim) * 4, stream_), op_name);
-    uint32_t bs = 1, bb = 4;
-    fmx_quant_geometry(type_id, &bs, &bb);
-    record_operation({op_name, name(), static_cast<uint64_t>(out_dim) * (in_dim / bs) * bb + in_dim * 4ull,
+    check(fmx_download(y, s.y_dev, static_cast<uint64_t>(out_dim) * 4, s.stream), op_name);
+    record_operation({op_name, name(), raw_bytes(type_id, out_dim, in_dim) + in_dim * 4ull,
                       static_cast<uint64_t>(out_dim) * sizeof(float)});
+}
+
+void HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, uint32_t *ids, float *weights) {
+    if (fault_ == BackendFault::DeviceLoss) fail(ErrorCode::DEVICE_LOSS, "injected device loss");
+    const uint32_t H = L.hidden, F = L.ffn, E = L.experts, K = L.top_k;
+    if (!x || !out || !ids || !weights || !L.router || H == 0 || F == 0 || E == 0 || K == 0 || K > E ||
+        L.expert_payloads.size() != E)
+        fail(ErrorCode::INVALID_ARGUMENT, "invalid MoE layer arguments");
+    if (L.up_type != L.gate_type) fail(ErrorCode::UNSUPPORTED_QUANTISATION, "gate and up of different types");
+    const uint64_t gate_bytes = raw_bytes(L.gate_type, F, H), down_bytes = raw_bytes(L.down_type, H, F);
+    const uint64_t router_bytes = raw_bytes(L.router_type, E, H);
+    if (gate_bytes == 0 || down_bytes == 0 || router_bytes == 0)
+        fail(ErrorCode::SHAPE_MISMATCH, "projection is not a whole number of blocks");
+    const std::string l = std::to_string(L.layer);
+
+    std::lock_guard<std::mutex> lock(state_->mutex);
+    State &s = *state_;
+    // the experts' packed slots and the device table of their addresses
+    std::vector<uintptr_t> key;
+    key.reserve(3 * E);
+    for (uint32_t e = 0; e < E; ++e) {
+        const uint8_t *base = static_cast<const uint8_t *>(L.expert_payloads[e]);
+        key.push_back(reinterpret_cast<uintptr_t>(s.packed_twin(L.gate_type, base, F, H)));
+        key.push_back(reinterpret_cast<uintptr_t>(s.packed_twin(L.up_type, base + gate_bytes, F, H)));
+        key.push_back(reinterpret_cast<uintptr_t>(s.packed_twin(L.down_type, base + 2 * gate_bytes, H, F)));
+    }
+    void *table = nullptr;
+    auto tit = s.slot_tables.find(key);
+    if (tit != s.slot_tables.end()) {
+        table = tit->second;
+    } else {
+        std::vector<uint64_t> host(3 * E);
+        for (uint32_t e = 0; e < E; ++e)
+            for (uint32_t r = 0; r < 3; ++r) host[r * E + e] = key[3 * e + r];
+        check(fmx_alloc(host.size() * 8, &table), "expert slot table");
+        const int rc = fmx_upload(table, host.data(), host.size() * 8, s.stream, nullptr);
+        if (rc == FMX_OK) check(fmx_stream_sync(s.stream), "expert slot table");
+        if (rc != FMX_OK) {
+            fmx_free(table);
+            check(rc, "expert slot table");
+        }
+        s.slot_tables[key] = table;
+    }
+    void *router = s.packed_twin(L.router_type, L.router, E, H);
+
+    // small per-call inputs and outputs: x, the norm gains (when not resident
+    // in a buffer), the logit bias, out, ids, weights
+    const uint64_t o_x = 0, o_norm = o_x + ((H * 4ull + 255) & ~255ull), o_bias = o_norm + ((H * 4ull + 255) & ~255ull),
+                   o_out = o_bias + ((E * 4ull + 255) & ~255ull), o_ids = o_out + ((H * 4ull + 255) & ~255ull),
+                   o_w = o_ids + 256, small = o_w + 256;
+    if (K > 64) fail(ErrorCode::INVALID_ARGUMENT, "top_k above 64");
+    if (small > s.moe_small_cap) {
+        fmx_free(s.moe_small);
+        s.moe_small = nullptr;
+        s.moe_small_cap = 0;
+        check(fmx_alloc(small, &s.moe_small), "MoE inputs");
+        s.moe_small_cap = small;
+    }
+    uint8_t *sm = static_cast<uint8_t *>(s.moe_small);
+    const float *norm_dev = nullptr;
+    if (L.norm_weight) {
+        uint64_t off = 0;
+        const State::Twin *t = s.find_twin(L.norm_weight, &off);
+        const uintptr_t addr = t ? reinterpret_cast<uintptr_t>(t->device) + off : 0;
+        if (t && off + H * 4ull <= t->bytes && addr % 16 == 0) {
+            norm_dev = reinterpret_cast<const float *>(addr);
+        } else {
+            check(fmx_upload(sm + o_norm, L.norm_weight, H * 4ull, s.stream, nullptr), "norm gains");
+            norm_dev = reinterpret_cast<const float *>(sm + o_norm);
+        }
+    }
+    if (L.router_bias) check(fmx_upload(sm + o_bias, L.router_bias, E * 4ull, s.stream, nullptr), "router bias");
+    check(fmx_upload(sm + o_x, x, H * 4ull, s.stream, nullptr), "MoE input");
+
+    fmx_moe_layer d;
+    std::memset(&d, 0, sizeof(d));
+    d.hidden = H;
+    d.ffn = F;
+    d.experts = E;
+    d.top_k = K;
+    d.norm_weight = norm_dev;
+    d.rms_eps = L.rms_eps;
+    d.norm_bias = L.norm_bias;
+    d.router_type = L.router_type;
+    d.router = router;
+    d.router_bias = L.router_bias ? reinterpret_cast<const float *>(sm + o_bias) : nullptr;
+    d.weights_norm = L.weights_norm ? 1 : 0;
+    d.epsilon_additive = L.epsilon_additive ? 1 : 0;
+    d.weights_epsilon = L.weights_epsilon;
+    d.weights_scale = L.weights_scale;
+    d.gate_type = L.gate_type;
+    d.up_type = L.up_type;
+    d.down_type = L.down_type;
+    const void *const *tab = static_cast<const void *const *>(table);
+    d.gate = tab;
+    d.up = tab + E;
+    d.down = tab + 2 * E;
+    const uint64_t ws = fmx_moe_workspace_bytes(&d, 1);
+    if (ws == 0) fail(ErrorCode::SHAPE_MISMATCH, "MoE layer shape not supported");
+    if (ws > s.moe_ws_cap) {
+        fmx_free(s.moe_ws);
+        s.moe_ws = nullptr;
+        s.moe_ws_cap = 0;
+        check(fmx_alloc(ws, &s.moe_ws), "MoE workspace");
+        s.moe_ws_cap = ws;
+    }
+    check(fmx_moe_decode(&d, reinterpret_cast<const float *>(sm + o_x), reinterpret_cast<float *>(sm + o_out), 1,
+                         reinterpret_cast<uint32_t *>(sm + o_ids), reinterpret_cast<float *>(sm + o_w), s.moe_ws,
+                         s.moe_ws_cap, s.stream),
+          "moe layer " + l);
+    check(fmx_download(out, sm + o_out, H * 4ull, s.stream), "MoE output");
+    check(fmx_download(ids, sm + o_ids, K * 4ull, s.stream), "MoE routing");
+    check(fmx_download(weights, sm + o_w, K * 4ull, s.stream), "MoE weights");
+    check(fmx_moe_status(s.moe_ws, s.stream), "router scores of layer " + l);
+
+    // the reference's operation log for this block (engine.cpp:1603-1776)
+    record_operation({"router.L" + l, name(), router_bytes + H * 4ull, E * 4ull});
+    record_control("router_gating.L" + l, E * 4ull, E * 4ull, name());
+    record_control("router_topk.L" + l, E * 4ull, K * 4ull, name());
+    for (uint32_t i = 0; i < K; ++i) {
+        const std::string ex = ".L" + l + ".E" + std::to_string(ids[i]);
+        record_operation({"expert_gate" + ex, name(), gate_bytes + H * 4ull, F * 4ull});
+        record_operation({"expert_up" + ex, name(), gate_bytes + H * 4ull, F * 4ull});
+        record_control("expert_swiglu.L" + l, 2 * F * 4ull, F * 4ull, name());
+        record_operation({"expert_down" + ex, name(), down_bytes + F * 4ull, H * 4ull});
+    }
+    record_control("expert_combine.L" + l, K * H * 4ull, H * 4ull, name());
 }
 
 void HipBackend::inject_fault(BackendFault fault) {

@@ -3,8 +3,8 @@
 // The drop-in for FreeMoe's physical-GPU placeholder (src/backend.cpp:528-571):
 // same BackendKind::PhysicalGPU, same `--backend gpu`, same fault and error
 // codes. It is compiled inside the FreeMoe tree (it includes FreeMoe's own
-// headers) and linked with libfmx.so; see INTEGRATION.md for the three edits
-// that wire it in.
+// headers) and linked with libfmx.so; backend_factory.cpp wires it into
+// Backend::create.
 //
 // Memory. FreeMoe's engine and residency read DeviceBuffer::data on the host
 // (engine.cpp:203, 330, 346, 824-836, 1733-1737; residency.cpp:703-719), so
@@ -12,17 +12,45 @@
 // copies into the mirror and queues the H2D copy of the twin; the fence is the
 // HIP event recorded after it. Kernels read the twins; a host pointer anywhere
 // inside a buffer resolves to the same offset in its twin.
+//
+// Lifetime. The twins, packed copies, fences and stream live in a device
+// state object that every buffer's cleanup closure shares, as FreeMoe's VNPU
+// backend shares its runtime (backend.cpp:441-446): a buffer released after
+// its backend still frees its memory on a live device.
 #pragma once
 
 #include "fm/backend.hpp"
 
+#include <cstdint>
 #include <map>
 #include <memory>
 #include <mutex>
 #include <string>
 #include <tuple>
+#include <vector>
 
 namespace fm {
+
+// One routed MoE layer for HipBackend::moe_layer (the block of
+// engine.cpp:1602-1776), described by host pointers as the engine holds them:
+// weights inside this backend's buffers (the fixed-weight buffer, the expert
+// slots); the norm gains may also be ordinary host memory (FreeMoe decodes
+// block-type norm vectors into host vectors, engine.cpp:223-266).
+struct MoeLayerView {
+    uint32_t layer = 0;
+    uint32_t hidden = 0, ffn = 0, experts = 0, top_k = 0;
+    const float *norm_weight = nullptr; // [hidden]
+    double rms_eps = 1e-5, norm_bias = 0.0;
+    uint32_t router_type = 0;
+    const void *router = nullptr;       // [experts x hidden] raw rows
+    const float *router_bias = nullptr; // [experts] host, or nullptr
+    bool weights_norm = false, epsilon_additive = false;
+    double weights_epsilon = 6.103515625e-5, weights_scale = 1.0;
+    // Every expert's slot payload (gate | up | down, raw rows, the layout of
+    // residency's slots), all resident: the kernels route on the device.
+    std::vector<const void *> expert_payloads;
+    uint32_t gate_type = 0, up_type = 0, down_type = 0;
+};
 
 class HipBackend final : public Backend {
 public:
@@ -46,29 +74,26 @@ public:
     void matvec_quant(uint32_t type_id, const void *weights, const float *x, float *y, uint32_t out_dim,
                       uint32_t in_dim, const std::string &op_name);
 
+    // The whole MoE block for one token on the device (fmx_moe_decode):
+    // out[hidden] = x + sum_i w_i down_i(SwiGLU(gate_i h, up_i h)) with
+    // h = RMSNorm(x); ids / weights receive the routing in rank order (the
+    // RoutingEvent's experts). Logs the reference's operation names
+    // (router.L*, router_gating.L*, router_topk.L*, expert_gate/up/down.L*.E*,
+    // expert_swiglu.L*, expert_combine.L*) under this backend's label. The
+    // engine's optional hook at engine.cpp:1602.
+    void moe_layer(const MoeLayerView &layer, const float *x, float *out, uint32_t *ids, float *weights);
+
     // Device address of a host pointer inside one of this backend's buffers
     // (nullptr when it is not in one).
     void *device_address(const void *host) const;
 
-private:
-    struct Twin {
-        void *device = nullptr;
-        uint64_t bytes = 0;
-    };
-    const Twin *find_twin(const void *host, uint64_t *offset) const;
-    void *packed_twin(uint32_t type_id, const void *weights, uint32_t rows, uint32_t cols);
-    void ensure_scratch(uint64_t x_bytes, uint64_t y_bytes);
-    void check(int status, const std::string &where) const;
+    struct State;
 
-    bool have_device_ = false;
-    void *stream_ = nullptr;
-    mutable std::mutex mutex_;
-    std::map<uintptr_t, Twin> twins_;                                           // host mirror start -> twin
-    std::map<std::tuple<uintptr_t, uint32_t, uint32_t, uint32_t>, void *> packed_; // packed block matrices
-    std::map<uint64_t, void *> fences_;                                         // fence id -> fmx fence
-    uint64_t next_fence_ = 1;
-    void *x_dev_ = nullptr, *y_dev_ = nullptr;
-    uint64_t x_cap_ = 0, y_cap_ = 0;
+private:
+    void check(int status, const std::string &where) const;
+    void ensure_scratch(uint64_t x_bytes, uint64_t y_bytes);
+
+    std::shared_ptr<State> state_;
     BackendFault fault_ = BackendFault::None;
 };
 

@@ -13,6 +13,8 @@
 #include "fm/kernels.hpp"
 #include "fm/quant.hpp"
 
+#include "fmoracle.h"
+
 #include <cstdio>
 #include <cstring>
 #include <vector>
@@ -115,6 +117,152 @@ int main() {
         gpu.matvec_quant(type, qb->data, xq.data(), yq.data(), qr, qc, "check.quant.refill");
         std::snprintf(what, sizeof what, "matvec_quant type %u follows a slot refill", type);
         report(std::memcmp(yr.data(), yq.data(), qr * 4) == 0, what);
+    }
+
+    // ---- the fused MoE block (moe_layer) on buffers laid out as the engine and
+    // residency hold them, against the oracle's layer (which reproduces
+    // FreeMoe's engine bit for bit): output, routing and the operation log
+    struct MoeCase {
+        uint32_t hidden, ffn, experts, top_k, gate_type, down_type, router_type, norm_offset;
+    };
+    for (const MoeCase &mc : {MoeCase{512, 256, 8, 2, 12, 8, 8, 4}, MoeCase{256, 512, 6, 2, 2, 2, 0, 16}}) {
+        const uint32_t H = mc.hidden, F = mc.ffn, E = mc.experts, K = mc.top_k;
+        const fm::QuantGeometry gg = fm::quant_geometry(mc.gate_type), gd = fm::quant_geometry(mc.down_type);
+        const uint64_t gate_bytes = static_cast<uint64_t>(F) * (H / gg.block_size) * gg.block_bytes;
+        const uint64_t down_bytes = static_cast<uint64_t>(H) * (F / gd.block_size) * gd.block_bytes;
+        // fixed weights: [pad][norm gains][router rows], contiguous as engine.cpp:216-224 packs them
+        std::vector<float> norm(H);
+        for (auto &v : norm) v = 1.0f + static_cast<float>(static_cast<int32_t>(lcg(s) >> 8) - (1 << 23)) / (1 << 29);
+        std::vector<uint8_t> router;
+        if (mc.router_type == 0) {
+            router.resize(static_cast<size_t>(E) * H * 4);
+            float *rf = reinterpret_cast<float *>(router.data());
+            for (uint64_t i = 0; i < static_cast<uint64_t>(E) * H; ++i)
+                rf[i] = static_cast<float>(static_cast<int32_t>(lcg(s) >> 8) - (1 << 23)) / (1 << 27);
+        } else {
+            router = quant_matrix(mc.router_type, E, H, 300);
+        }
+        std::vector<uint8_t> fixed(mc.norm_offset + H * 4 + router.size());
+        std::memcpy(fixed.data() + mc.norm_offset, norm.data(), H * 4);
+        std::memcpy(fixed.data() + mc.norm_offset + H * 4, router.data(), router.size());
+        auto fb = gpu.allocate(fixed.size(), fm::AllocationTag::Weights);
+        gpu.wait_fence(gpu.upload(*fb, fixed.data(), fixed.size()), 5000);
+        // one slot per expert: gate | up | down, raw rows
+        std::vector<std::vector<uint8_t>> gate(E), up(E), down(E);
+        std::vector<std::unique_ptr<fm::DeviceBuffer>> slots;
+        fm::MoeLayerView view;
+        for (uint32_t e = 0; e < E; ++e) {
+            gate[e] = quant_matrix(mc.gate_type, F, H, 400 + e);
+            up[e] = quant_matrix(mc.gate_type, F, H, 500 + e);
+            down[e] = quant_matrix(mc.down_type, H, F, 600 + e);
+            std::vector<uint8_t> payload(2 * gate_bytes + down_bytes);
+            std::memcpy(payload.data(), gate[e].data(), gate_bytes);
+            std::memcpy(payload.data() + gate_bytes, up[e].data(), gate_bytes);
+            std::memcpy(payload.data() + 2 * gate_bytes, down[e].data(), down_bytes);
+            slots.push_back(gpu.allocate(payload.size(), fm::AllocationTag::ExpertCache));
+            gpu.wait_fence(gpu.upload(*slots.back(), payload.data(), payload.size()), 5000);
+            view.expert_payloads.push_back(slots.back()->data);
+        }
+        view.layer = 3;
+        view.hidden = H;
+        view.ffn = F;
+        view.experts = E;
+        view.top_k = K;
+        view.norm_weight = reinterpret_cast<const float *>(static_cast<uint8_t *>(fb->data) + mc.norm_offset);
+        view.rms_eps = static_cast<double>(1e-5f);
+        view.router_type = mc.router_type;
+        view.router = static_cast<uint8_t *>(fb->data) + mc.norm_offset + H * 4;
+        view.weights_norm = true;
+        view.gate_type = view.up_type = mc.gate_type;
+        view.down_type = mc.down_type;
+        // the oracle's layer on the same bytes
+        std::vector<const uint8_t *> gp(E), upp(E), dp(E);
+        for (uint32_t e = 0; e < E; ++e) {
+            gp[e] = gate[e].data();
+            upp[e] = up[e].data();
+            dp[e] = down[e].data();
+        }
+        fmo_layer ol{};
+        ol.hidden = H;
+        ol.ffn = F;
+        ol.experts = E;
+        ol.top_k = K;
+        ol.norm_weight = norm.data();
+        ol.rms_eps = view.rms_eps;
+        ol.router_type = mc.router_type;
+        ol.router = router.data();
+        ol.weights_norm = 1;
+        ol.weights_epsilon = view.weights_epsilon;
+        ol.weights_scale = 1.0;
+        ol.gate_type = ol.up_type = mc.gate_type;
+        ol.down_type = mc.down_type;
+        ol.gate = gp.data();
+        ol.up = upp.data();
+        ol.down = dp.data();
+        const size_t ops_before = gpu.operations().size();
+        bool same = true;
+        std::vector<uint32_t> seen;
+        for (int t = 0; t < 6; ++t) {
+            std::vector<float> xt(H), og(H), orf(H), wg(K), wr(K);
+            std::vector<uint32_t> ig(K), ir(K);
+            for (auto &v : xt) v = static_cast<float>(static_cast<int32_t>(lcg(s) >> 8) - (1 << 23)) / (1 << 22);
+            gpu.moe_layer(view, xt.data(), og.data(), ig.data(), wg.data());
+            if (fmo_moe_layer(FMO_ISA_AVX2, &ol, xt.data(), orf.data(), ir.data(), wr.data(), nullptr, nullptr))
+                same = false;
+            same = same && std::memcmp(og.data(), orf.data(), H * 4) == 0 && ig == ir &&
+                   std::memcmp(wg.data(), wr.data(), K * 4) == 0;
+            seen.insert(seen.end(), ig.begin(), ig.end());
+        }
+        char what[160];
+        std::snprintf(what, sizeof what,
+                      "moe_layer (gate/up type %u, down %u, router %u) bit-identical to the oracle's layer, 6 tokens",
+                      mc.gate_type, mc.down_type, mc.router_type);
+        report(same, what);
+        const auto ops = gpu.operations();
+        uint32_t named = 0, on_gpu = 0;
+        for (size_t i = ops_before; i < ops.size(); ++i) {
+            const std::string &n = ops[i].name;
+            named += n == "router.L3" || n == "router_gating.L3" || n == "router_topk.L3" ||
+                     n.rfind("expert_gate.L3.E", 0) == 0 || n.rfind("expert_up.L3.E", 0) == 0 ||
+                     n.rfind("expert_down.L3.E", 0) == 0 || n == "expert_swiglu.L3" || n == "expert_combine.L3";
+            on_gpu += ops[i].backend == "hip-gfx950";
+        }
+        const size_t expect = 6 * (3 + 4 * K + 1);
+        report(ops.size() - ops_before == expect && named == expect && on_gpu == expect,
+               "moe_layer logs the reference's op names per token under hip-gfx950");
+        std::snprintf(what, sizeof what, "op log names the routed experts: expert_gate.L3.E%u present", seen[0]);
+        bool found = false;
+        for (size_t i = ops_before; i < ops.size(); ++i)
+            found = found || ops[i].name == "expert_gate.L3.E" + std::to_string(seen[0]);
+        report(found, what);
+        // refill one slot with another expert: the fused path follows it
+        const uint32_t ex = seen[0];
+        std::vector<uint8_t> g2 = quant_matrix(mc.gate_type, F, H, 700);
+        std::vector<uint8_t> payload(2 * gate_bytes + down_bytes);
+        std::memcpy(payload.data(), g2.data(), gate_bytes);
+        std::memcpy(payload.data() + gate_bytes, up[ex].data(), gate_bytes);
+        std::memcpy(payload.data() + 2 * gate_bytes, down[ex].data(), down_bytes);
+        gpu.wait_fence(gpu.upload(*slots[ex], payload.data(), payload.size()), 5000);
+        gate[ex] = g2;
+        gp[ex] = gate[ex].data();
+        std::vector<float> xt(H), og(H), orf(H), wg(K), wr(K);
+        std::vector<uint32_t> ig(K), ir(K);
+        for (auto &v : xt) v = static_cast<float>(static_cast<int32_t>(lcg(s) >> 8) - (1 << 23)) / (1 << 22);
+        gpu.moe_layer(view, xt.data(), og.data(), ig.data(), wg.data());
+        fmo_moe_layer(FMO_ISA_AVX2, &ol, xt.data(), orf.data(), ir.data(), wr.data(), nullptr, nullptr);
+        report(std::memcmp(og.data(), orf.data(), H * 4) == 0 && ig == ir, "moe_layer follows an expert slot refill");
+    }
+
+    // ---- buffers outlive their backend (the device state stays alive, as the
+    // VNPU backend keeps its runtime, backend.cpp:441-446)
+    {
+        auto late = std::make_unique<fm::HipBackend>(gcfg);
+        auto tracker = late->tracker();
+        auto buf = late->allocate(1 << 20, fm::AllocationTag::Other);
+        late->wait_fence(late->upload(*buf, w.data(), 4096), 5000);
+        late.reset();
+        buf.reset();
+        report(tracker->snapshot().live_bytes == 0, "a buffer released after its backend frees cleanly");
     }
 
     // ---- faults forced from the host (backend.hpp:118), as the CPU backend raises them
