@@ -14,6 +14,12 @@
 //       line (prompts within tolerance, token and routing matches, max abs
 //       diff, and how many operations the backend logged and under which
 //       backend label).
+//   engine_check residency <model.gguf> <reference_root> <prompts> <generate> <slots>
+//       compare_reference on the GPU backend with `slots` expert slots (fewer
+//       than the model's experts, so ResidencyManager::load_slot refills them:
+//       host payload -> upload into the slot's pinned mirror and HBM twin ->
+//       fence -> FNV-1a read-back, residency.cpp:617-723); prints the
+//       comparison and residency's counters.
 //   engine_check twin <model.gguf> <prompts> <prompt_len> <generate> <seed>
 //       seeded random byte prompts through a CPU-backend engine and a
 //       GPU-backend engine; prints one JSON line with the largest prompt-logit
@@ -21,6 +27,7 @@
 //       routing records and greedy ids are identical.
 // Exits non-zero on an engine error.
 #include "fm/engine.hpp"
+#include "fm/residency.hpp"
 
 #include <cmath>
 #include <cstdio>
@@ -66,6 +73,32 @@ int compare(int argc, char **argv) {
                 r.prompts_routing_match, static_cast<unsigned long long>(r.matching_tokens),
                 static_cast<unsigned long long>(r.reference_tokens), r.max_abs_diff, r.max_rel_diff,
                 op_labels(e.backend()).c_str());
+    return 0;
+}
+
+int residency(int argc, char **argv) {
+    if (argc < 7) return 2;
+    fm::RunConfig rc = config_for(argv[2], true);
+    rc.cache_slots = static_cast<uint32_t>(std::atoi(argv[6]));
+    fm::Engine e(rc);
+    e.initialize();
+    const fm::ComparisonResult r =
+        e.compare_reference(argv[3], static_cast<uint32_t>(std::atoi(argv[4])), static_cast<uint32_t>(std::atoi(argv[5])));
+    const fm::ResidencyMetrics &m = e.residency()->metrics();
+    std::printf("{\"mode\":\"residency\",\"backend\":\"%s\",\"slots\":%u,\"prompts\":%u,\"within_tolerance\":%u,"
+                "\"token_match\":%u,\"routing_match\":%u,\"cache_hits\":%llu,\"cache_misses\":%llu,"
+                "\"evictions\":%llu,\"checksum_checks\":%llu,\"checksum_failures\":%llu,\"h2d_bytes\":%llu,"
+                "\"selected_experts\":%llu,\"experts_executed\":%llu,\"transfer_failures\":%llu,"
+                "\"fence_timeouts\":%llu}\n",
+                e.backend().name().c_str(), rc.cache_slots, r.prompts, r.prompts_within_tolerance,
+                r.prompts_token_match, r.prompts_routing_match, static_cast<unsigned long long>(m.cache_hits),
+                static_cast<unsigned long long>(m.cache_misses), static_cast<unsigned long long>(m.evictions),
+                static_cast<unsigned long long>(m.checksum_checks),
+                static_cast<unsigned long long>(m.checksum_failures), static_cast<unsigned long long>(m.h2d_bytes),
+                static_cast<unsigned long long>(m.selected_experts),
+                static_cast<unsigned long long>(m.experts_executed),
+                static_cast<unsigned long long>(m.transfer_failures),
+                static_cast<unsigned long long>(m.fence_timeouts));
     return 0;
 }
 
@@ -123,6 +156,7 @@ int main(int argc, char **argv) {
     try {
         if (argc >= 2 && std::string(argv[1]) == "compare") return compare(argc, argv);
         if (argc >= 2 && std::string(argv[1]) == "twin") return twin(argc, argv);
+        if (argc >= 2 && std::string(argv[1]) == "residency") return residency(argc, argv);
     } catch (const fm::Error &e) {
         std::fprintf(stderr, "engine_check: %s: %s\n", fm::error_name(e.code), e.what());
         return 1;

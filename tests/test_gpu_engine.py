@@ -65,3 +65,20 @@ def test_tiny_model_end_to_end_cpu_and_hip_identical(gpu, tmp_path):
     assert r["routing_identical"] and r["ids_identical"]
     assert r["generated"] == 4 * 32 and r["routing_events"] == 4 * (65 + 32) * 2
     assert r["gpu_ops"].get("hip-gfx950", 0) > 0
+
+
+@pytest.mark.gpu
+def test_residency_refills_slots_through_hip_backend(gpu):
+    """Two expert slots for moe-fm's 16 experts (2 layers x 8): residency
+    refills slots through HipBackend (upload into the pinned mirror and the
+    HBM twin, the event fence, the FNV-1a read-back, residency.cpp:617-723) on
+    nearly every routed expert, and every prompt still matches FreeMoe's
+    goldens."""
+    r = run("residency", FIXTURES / "moe-fm.gguf", FIXTURES, 20, 16, 2)
+    print(r)
+    assert r["backend"] == "hip-gfx950" and r["slots"] == 2
+    check_compare(r | {"matching_tokens": 1, "reference_tokens": 1}, 20)
+    assert r["evictions"] > 100 and r["cache_misses"] > 100
+    assert r["checksum_checks"] >= 2 * r["cache_misses"] and r["checksum_failures"] == 0
+    assert r["transfer_failures"] == 0 and r["fence_timeouts"] == 0
+    assert r["experts_executed"] == r["selected_experts"]
