@@ -124,8 +124,9 @@ struct Routing {
 //   rank order, optional division by it (plus or at least epsilon), scale.
 // A logit that is not finite (the reference raises INTERNAL_ERROR) sets *bad
 // and yields expert r with weight 0, which keeps every later kernel in bounds.
+// kSlots: experts per lane, 64 kSlots >= experts.
+template <int kSlots = 4>
 __device__ Routing wave_route(const RouteArgs &a, const float *__restrict__ logits, bool *bad) {
-    constexpr int kSlots = 4; // 64 * kSlots >= experts
     const uint32_t E = a.experts, K = a.top_k, lane = threadIdx.x & 63;
     float v[kSlots];
     bool nonfinite = false;
@@ -335,6 +336,67 @@ __host__ __device__ inline uint32_t route_chain_stride(uint32_t hidden) {
     return cs + (68u - cs % 64u) % 64u;
 }
 
+// One F32 router row's logit in the reference's gemv_avx2_row order from h
+// and the row staged in LDS in chain layout (chain c at hs / rs + c * cs, see
+// route_chain_stride): lane c of a whole 16-lane group runs chain c (FMA over
+// the chain's elements in order), then the 8-element tail, the lane tree and
+// the sequential tail; every lane of the group returns the value.
+// kB float4 of h and of the row per operand batch, the next batch's reads
+// issued before this one's FMAs.
+template <uint32_t kB>
+__device__ inline float chain_layout_logit(const float *hs, const float *rs, uint32_t cs, uint32_t H, uint32_t c) {
+    const uint32_t S = H / 16, n16 = S * 16;
+    const float4 *h4 = reinterpret_cast<const float4 *>(hs + c * cs);
+    const float4 *w4 = reinterpret_cast<const float4 *>(rs + c * cs);
+    float acc = 0.0f;
+    // the chain is a dependent FMA sequence: its operands come from LDS in
+    // batches of 4 kB steps, the next batch requested before this one's FMAs
+    const uint32_t nb = S / 4 / kB;
+    float4 hb[2][kB], wb[2][kB];
+    if (nb > 0) {
+#pragma unroll
+        for (uint32_t q = 0; q < kB; ++q) {
+            hb[0][q] = h4[q];
+            wb[0][q] = w4[q];
+        }
+    }
+    for (uint32_t bi = 0; bi < nb; bi += 2) {
+#pragma unroll
+        for (uint32_t half = 0; half < 2; ++half) {
+            const uint32_t b = bi + half;
+            if (b >= nb) break;
+            const uint32_t nx = (b + 1 < nb ? b + 1 : b) * kB;
+#pragma unroll
+            for (uint32_t q = 0; q < kB; ++q) {
+                hb[half ^ 1][q] = h4[nx + q];
+                wb[half ^ 1][q] = w4[nx + q];
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < kB; ++q) {
+                acc = fma_rn(wb[half][q].x, hb[half][q].x, acc);
+                acc = fma_rn(wb[half][q].y, hb[half][q].y, acc);
+                acc = fma_rn(wb[half][q].z, hb[half][q].z, acc);
+                acc = fma_rn(wb[half][q].w, hb[half][q].w, acc);
+            }
+        }
+    }
+    for (uint32_t i = nb * kB; i < S / 4; ++i) {
+        const float4 hq = h4[i], wq = w4[i];
+        acc = fma_rn(wq.x, hq.x, acc);
+        acc = fma_rn(wq.y, hq.y, acc);
+        acc = fma_rn(wq.z, hq.z, acc);
+        acc = fma_rn(wq.w, hq.w, acc);
+    }
+    for (uint32_t s = S / 4 * 4; s < S; ++s) acc = fma_rn(rs[c * cs + s], hs[c * cs + s], acc);
+    const bool tail8 = H - n16 >= 8;
+    if (tail8 && c < 8) acc = fma_rn(rs[c * cs + S], hs[c * cs + S], acc);
+    const float tt = acc + lane_xor(acc, 8);
+    float total = hsum8_lanes(tt);
+    for (uint32_t k = tail8 ? n16 + 8 : n16; k < H; ++k)
+        total = fma_rn(rs[(k - n16) * cs + S], hs[(k - n16) * cs + S], total);
+    return total;
+}
+
 // Router logit of row blockIdx.y for token blockIdx.x. Every workgroup of the
 // token computes the token's RMSNorm (engine.cpp:723-740) from x held in
 // registers (4 float4 per thread: hidden <= 16 NT), the first one writes it to
@@ -360,7 +422,10 @@ __global__ __launch_bounds__(NT) __attribute__((aligned(kHotAlign))) void route_
     float *rs = lds + 16 * cs;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + static_cast<uint64_t>(t) * H);
     const float4 *r4 = reinterpret_cast<const float4 *>(a.router + static_cast<uint64_t>(row) * H);
-    const float4 *g4 = reinterpret_cast<const float4 *>(a.norm_weight);
+    // unconditional loads (gains from x when there are none, unused): a load
+    // under a branch makes the compiler wait for it before the branch
+    const bool has_gain = a.norm_weight != nullptr;
+    const float4 *g4 = has_gain ? reinterpret_cast<const float4 *>(a.norm_weight) : x4;
     float4 xv[P], gv[P], rv[P];
 #pragma unroll
     for (uint32_t i = 0; i < P; ++i) {
@@ -368,10 +433,10 @@ __global__ __launch_bounds__(NT) __attribute__((aligned(kHotAlign))) void route_
         const uint32_t qc = q < H4 ? q : H4 - 1;
         xv[i] = x4[qc];
         rv[i] = r4[qc];
-        gv[i] = g4 ? g4[qc] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        gv[i] = g4[qc];
     }
     float hv[4 * P];
-    token_rmsnorm<NT, P>(a, xv, gv, g4 != nullptr, hv, rs);
+    token_rmsnorm<NT, P>(a, xv, gv, has_gain, hv, rs);
     // h and the router row into the chain layout
 #pragma unroll
     for (uint32_t i = 0; i < P; ++i) {
@@ -391,57 +456,8 @@ __global__ __launch_bounds__(NT) __attribute__((aligned(kHotAlign))) void route_
     }
     __syncthreads();
     if (tid < 16) {
-        const uint32_t c = tid, S = H / 16, n16 = S * 16;
-        const float4 *h4 = reinterpret_cast<const float4 *>(hs + c * cs);
-        const float4 *w4 = reinterpret_cast<const float4 *>(rs + c * cs);
-        float acc = 0.0f;
-        // the chain is a dependent FMA sequence: its operands come from LDS in
-        // batches of 32 steps, the next batch requested before this one's FMAs
-        constexpr uint32_t kB = 8; // float4 per batch
-        const uint32_t nb = S / 4 / kB;
-        float4 hb[2][kB], wb[2][kB];
-        if (nb > 0) {
-#pragma unroll
-            for (uint32_t q = 0; q < kB; ++q) {
-                hb[0][q] = h4[q];
-                wb[0][q] = w4[q];
-            }
-        }
-        for (uint32_t bi = 0; bi < nb; bi += 2) {
-#pragma unroll
-            for (uint32_t half = 0; half < 2; ++half) {
-                const uint32_t b = bi + half;
-                if (b >= nb) break;
-                const uint32_t nx = (b + 1 < nb ? b + 1 : b) * kB;
-#pragma unroll
-                for (uint32_t q = 0; q < kB; ++q) {
-                    hb[half ^ 1][q] = h4[nx + q];
-                    wb[half ^ 1][q] = w4[nx + q];
-                }
-#pragma unroll
-                for (uint32_t q = 0; q < kB; ++q) {
-                    acc = fma_rn(wb[half][q].x, hb[half][q].x, acc);
-                    acc = fma_rn(wb[half][q].y, hb[half][q].y, acc);
-                    acc = fma_rn(wb[half][q].z, hb[half][q].z, acc);
-                    acc = fma_rn(wb[half][q].w, hb[half][q].w, acc);
-                }
-            }
-        }
-        for (uint32_t i = nb * kB; i < S / 4; ++i) {
-            const float4 hq = h4[i], wq = w4[i];
-            acc = fma_rn(wq.x, hq.x, acc);
-            acc = fma_rn(wq.y, hq.y, acc);
-            acc = fma_rn(wq.z, hq.z, acc);
-            acc = fma_rn(wq.w, hq.w, acc);
-        }
-        for (uint32_t s = S / 4 * 4; s < S; ++s) acc = fma_rn(rs[c * cs + s], hs[c * cs + s], acc);
-        const bool tail8 = H - n16 >= 8;
-        if (tail8 && c < 8) acc = fma_rn(rs[c * cs + S], hs[c * cs + S], acc);
-        const float tt = acc + lane_xor(acc, 8);
-        float total = hsum8_lanes(tt);
-        for (uint32_t k = tail8 ? n16 + 8 : n16; k < H; ++k)
-            total = fma_rn(rs[(k - n16) * cs + S], hs[(k - n16) * cs + S], total);
-        if (c == 0) logits[static_cast<uint64_t>(t) * E + row] = a.router_bias ? total + a.router_bias[row] : total;
+        const float total = chain_layout_logit<8>(hs, rs, cs, H, tid);
+        if (tid == 0) logits[static_cast<uint64_t>(t) * E + row] = a.router_bias ? total + a.router_bias[row] : total;
     }
 }
 
@@ -454,17 +470,18 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *_
     extern __shared__ __align__(16) float lds[];
     const uint32_t H = a.hidden, H4 = H / 4, tid = threadIdx.x, t = blockIdx.x;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + static_cast<uint64_t>(t) * H);
-    const float4 *g4 = reinterpret_cast<const float4 *>(a.norm_weight);
+    const bool has_gain = a.norm_weight != nullptr;
+    const float4 *g4 = has_gain ? reinterpret_cast<const float4 *>(a.norm_weight) : x4; // unconditional loads
     float4 xv[P], gv[P];
 #pragma unroll
     for (uint32_t i = 0; i < P; ++i) {
         const uint32_t q = tid + i * NT;
         const uint32_t qc = q < H4 ? q : H4 - 1;
         xv[i] = x4[qc];
-        gv[i] = g4 ? g4[qc] : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+        gv[i] = g4[qc];
     }
     float hv[4 * P];
-    token_rmsnorm<NT, P, true>(a, xv, gv, g4 != nullptr, hv, lds);
+    token_rmsnorm<NT, P, true>(a, xv, gv, has_gain, hv, lds);
     float4 *h4 = reinterpret_cast<float4 *>(h + static_cast<uint64_t>(t) * H);
 #pragma unroll
     for (uint32_t i = 0; i < P; ++i) {
