@@ -46,8 +46,9 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 // ------------------------------------------------------------ block types --
 // kChunkK: elements per packed chunk (eight 16-byte lane slices). elem(p) /
 // pos(e): element held at packed position p of a chunk, and its inverse.
-// WStep: a lane's packed bytes (and scales) for one GEMM K step; dequant_kk()
-// turns 8 consecutive positions of it into the bf16 B operand of one MFMA.
+// WStep: a lane's packed bytes (and scales) for one GEMM K step; decode()
+// turns its scales into floats once per step (Dec), and dequant_kk() turns 8
+// consecutive positions of it into the bf16 B operand of one MFMA.
 
 struct GQ80 {
     static constexpr uint32_t kType = FMX_TYPE_Q8_0;
@@ -69,14 +70,22 @@ struct GQ80 {
         for (int i = 0; i < 4; ++i) w.q[i] = ld16(q + 16 * i);
         w.d = ld8(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(step) * 8);
     }
-    __device__ static void decode_header(WStep &) {}
+    // The step's block scales as floats (once per step, not per K slice).
+    struct Dec {
+        float d[4];
+    };
+    __device__ static void decode(const WStep &w, Dec &c) {
+        c.d[0] = half_bits_to_float(w.d.x & 0xFFFFu);
+        c.d[1] = half_bits_to_float(w.d.x >> 16);
+        c.d[2] = half_bits_to_float(w.d.y & 0xFFFFu);
+        c.d[3] = half_bits_to_float(w.d.y >> 16);
+    }
     // Positions 64 h + 8 kk .. +8 of the step: bytes 8 (kk % 2) .. +8 of the
     // lane's slice kk / 2, i.e. blocks 2 (kk % 2) and 2 (kk % 2) + 1.
-    __device__ static bf16x8 dequant_kk(const WStep &w, int kk) {
+    __device__ static bf16x8 dequant_kk(const WStep &w, const Dec &c, int kk) {
         const uint4 q = w.q[kk >> 1];
         const uint32_t lo = (kk & 1) ? q.z : q.x, hi = (kk & 1) ? q.w : q.y;
-        const uint32_t dd = (kk & 1) ? w.d.y : w.d.x;
-        const float d0 = half_bits_to_float(dd & 0xFFFFu), d1 = half_bits_to_float(dd >> 16);
+        const float d0 = c.d[2 * (kk & 1)], d1 = c.d[2 * (kk & 1) + 1];
         uint32_t v[4];
         v[0] = pack_bf16x2(d0 * static_cast<float>(static_cast<int8_t>(lo)),
                            d0 * static_cast<float>(static_cast<int8_t>(lo >> 8)));
@@ -117,23 +126,33 @@ struct GQ40 {
         w.q[1] = ld16(q + 16);
         w.d = ld16(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(c) * 16);
     }
-    __device__ static void decode_header(WStep &) {}
+    // The chunk's block scales d and -8 d as floats, once per step.
+    struct Dec {
+        float d[8], nd[8];
+    };
+    __device__ static void decode(const WStep &w, Dec &c) {
+        const uint32_t dw[4] = {w.d.x, w.d.y, w.d.z, w.d.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            c.d[j] = half_bits_to_float((j & 1) ? dw[j >> 1] >> 16 : dw[j >> 1] & 0xFFFFu);
+            c.nd[j] = -8.0f * c.d[j];
+        }
+    }
     // Positions 64 h + 8 kk .. +8 of the step: dword kk % 4 of the lane's slice
     // kk / 4; its bytes are blocks 2 (kk % 4) (bytes 0, 1) and 2 (kk % 4) + 1
-    // (bytes 2, 3), low nibble first.
-    __device__ static bf16x8 dequant_kk(const WStep &w, int kk) {
+    // (bytes 2, 3), low nibble first. d (q - 8) = fma(d, q, -8 d) exactly (both
+    // products are exact in f32).
+    __device__ static bf16x8 dequant_kk(const WStep &w, const Dec &c, int kk) {
         const uint4 q = w.q[kk >> 2];
         const int i = kk & 3;
         const uint32_t qw = i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
-        const uint32_t dd = i == 0 ? w.d.x : i == 1 ? w.d.y : i == 2 ? w.d.z : w.d.w;
-        const float d0 = half_bits_to_float(dd & 0xFFFFu), d1 = half_bits_to_float(dd >> 16);
+        const uint32_t lo = qw & 0x0F0F0F0Fu, hi = (qw >> 4) & 0x0F0F0F0Fu;
         uint32_t v[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const uint32_t byte = (qw >> (8 * b)) & 0xFFu;
-            const float d = b < 2 ? d0 : d1;
-            v[b] = pack_bf16x2(d * static_cast<float>(static_cast<int32_t>(byte & 15u) - 8),
-                               d * static_cast<float>(static_cast<int32_t>(byte >> 4) - 8));
+            const float d = c.d[2 * i + (b >> 1)], nd = c.nd[2 * i + (b >> 1)];
+            v[b] = pack_bf16x2(__builtin_fmaf(d, static_cast<float>((lo >> (8 * b)) & 0xFFu), nd),
+                               __builtin_fmaf(d, static_cast<float>((hi >> (8 * b)) & 0xFFu), nd));
         }
         return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
     }
@@ -164,27 +183,38 @@ struct GQ4K {
         w.q[1] = ld16(q + 16);
         w.hd = ld16(packed + (static_cast<uint64_t>(r) * g.chunks + c) * 16);
     }
-    // Positions 64 h + 8 kk .. +8 of the step: dword g = kk % 4 of the lane's
-    // slice kk / 4, group g: low nibbles sub-block 2 g, high 2 g + 1.
-    __device__ static bf16x8 dequant_kk(const WStep &w, int kk) {
-        const uint4 q = w.q[kk >> 2];
-        const int gi = kk & 3;
-        const uint32_t qw = gi == 0 ? q.x : gi == 1 ? q.y : gi == 2 ? q.z : q.w;
+    // The super-block's sub-block scales d sc_j and negated mins -dmin m_j
+    // (j < 8) as floats, once per step; both products are exact in f32.
+    struct Dec {
+        float d[8], nm[8];
+    };
+    __device__ static void decode(const WStep &w, Dec &c) {
         uint8_t hdr[16];
         memcpy(hdr, &w.hd, 16);
         const float d = half_bits_to_float(hdr[0] | (hdr[1] << 8));
         const float dmin = half_bits_to_float(hdr[2] | (hdr[3] << 8));
-        uint32_t sc1, m1, sc2, m2;
-        k4_scale_min(2 * gi, hdr + 4, sc1, m1);
-        k4_scale_min(2 * gi + 1, hdr + 4, sc2, m2);
-        const float d1 = d * static_cast<float>(sc1), mm1 = dmin * static_cast<float>(m1);
-        const float d2 = d * static_cast<float>(sc2), mm2 = dmin * static_cast<float>(m2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uint32_t sc, m;
+            k4_scale_min(j, hdr + 4, sc, m);
+            c.d[j] = d * static_cast<float>(sc);
+            c.nm[j] = -(dmin * static_cast<float>(m));
+        }
+    }
+    // Positions 64 h + 8 kk .. +8 of the step: dword g = kk % 4 of the lane's
+    // slice kk / 4, group g: low nibbles sub-block 2 g, high 2 g + 1.
+    // d sc q - dmin m = fma(d sc, q, -dmin m) exactly (d sc q is exact).
+    __device__ static bf16x8 dequant_kk(const WStep &w, const Dec &c, int kk) {
+        const uint4 q = w.q[kk >> 2];
+        const int gi = kk & 3;
+        const uint32_t qw = gi == 0 ? q.x : gi == 1 ? q.y : gi == 2 ? q.z : q.w;
+        const uint32_t lo = qw & 0x0F0F0F0Fu, hi = (qw >> 4) & 0x0F0F0F0Fu;
+        const float d1 = c.d[2 * gi], m1 = c.nm[2 * gi], d2 = c.d[2 * gi + 1], m2 = c.nm[2 * gi + 1];
         uint32_t v[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const uint32_t byte = (qw >> (8 * k)) & 0xFFu;
-            v[k] = pack_bf16x2(d1 * static_cast<float>(byte & 15u) - mm1, d2 * static_cast<float>(byte >> 4) - mm2);
-        }
+        for (int k = 0; k < 4; ++k)
+            v[k] = pack_bf16x2(__builtin_fmaf(d1, static_cast<float>((lo >> (8 * k)) & 0xFFu), m1),
+                               __builtin_fmaf(d2, static_cast<float>((hi >> (8 * k)) & 0xFFu), m2));
         return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
     }
 };
@@ -282,10 +312,12 @@ struct GemmWave {
     // MFMAs of slice kk run, so the VALU work overlaps the matrix unit.
     __device__ __forceinline__ void multiply(int slot, const char *const (&a_kk)[8]) {
         bf16x8 av[2][NMB], bv[2];
+        typename T::Dec dc;
+        T::decode(w[slot], dc);
 #pragma unroll
         for (uint32_t mb = 0; mb < NMB; ++mb)
             av[0][mb] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4 *>(a_kk[0] + mb * 32 * kGRowBytes));
-        bv[0] = T::dequant_kk(w[slot], 0);
+        bv[0] = T::dequant_kk(w[slot], dc, 0);
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
             const int c = kk & 1, n = c ^ 1;
@@ -294,7 +326,7 @@ struct GemmWave {
                 for (uint32_t mb = 0; mb < NMB; ++mb)
                     av[n][mb] = __builtin_bit_cast(
                         bf16x8, *reinterpret_cast<const uint4 *>(a_kk[kk + 1] + mb * 32 * kGRowBytes));
-                bv[n] = T::dequant_kk(w[slot], kk + 1);
+                bv[n] = T::dequant_kk(w[slot], dc, kk + 1);
             }
 #pragma unroll
             for (uint32_t mb = 0; mb < NMB; ++mb)
