@@ -12,9 +12,14 @@ Prints one JSON line (the driver's contract) with:
   value        whole-job tokens/s
   roofline     the gate/up kernel (the dominant one): algorithmic bytes per
                launch / its mean duration from HIP events, against 8 TB/s
-  cpu_baseline the reference's own kernels (oracle/_ref, AVX2 + WorkerPool
-               threads) on a bounded sample of the same tokens, host cores
+  cpu_baseline the reference's own kernels (oracle/_ref) on a bounded sample
+               of the same tokens on the host: AVX2 + WorkerPool threads
+               (`value`) and scalar at one thread, each with best and median
+               per-token rates, and the host's CPU model and counts
   parity       GPU vs reference outputs on that sample
+  prefill      the 512-token Q8_0 prefill: roofline of its gate/up GEMM kernel
+               (flops per launch / the launch's own event-timed duration)
+               against bf16 MFMA peak, the down GEMM and the whole layer beside
 """
 from __future__ import annotations
 
@@ -43,43 +48,89 @@ def algorithmic_bytes(H, F, E, K, row_bytes_h, row_bytes_f):
     return gate_up, down, route
 
 
-def cpu_baseline(lw, x, target_s=15.0, max_tokens=256):
-    """The reference's own kernels on the host, one token at a time, until
-    target_s seconds or max_tokens tokens have run.
+def host_info():
+    """The GPU box's host CPU: model name (/proc/cpuinfo), logical CPUs and
+    the CPUs this process may run on."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": len(os.sched_getaffinity(0)), "logical_cpus": os.cpu_count()}
 
-    Two threads: the reference's WorkerPool (kernels.cpp:414-459) publishes
-    `pending = ranges - 1` into every worker's slot, each worker decrements only
-    its own slot, and the caller waits for worker 0's slot to reach zero, so a
-    split into more than two ranges never completes. Two threads (one range
-    each for the caller and worker 0) is the largest count that finishes; it is
-    also the thread count of the reference's own 2-vCPU test machine."""
+
+def timed_tokens(run_one, n_max, target_s, label):
+    """run_one(i) for i = 0, 1, ... until n_max tokens or target_s seconds;
+    returns per-token seconds."""
+    times = []
+    t0 = last = time.perf_counter()
+    while len(times) < n_max:
+        a = time.perf_counter()
+        run_one(len(times))
+        b = time.perf_counter()
+        times.append(b - a)
+        if b - last > 5.0:
+            print(f"[bench] {label}: {len(times)} tokens in {b - t0:.1f}s", file=sys.stderr, flush=True)
+            last = b
+        if b - t0 > target_s:
+            break
+    return times
+
+
+def rate_summary(times):
+    """tokens/s over the sample, and from the best and the median token."""
+    import numpy as np
+    t = np.asarray(times)
+    return {"tokens": int(t.size), "tokens_per_s": round(t.size / t.sum(), 3),
+            "best_tokens_per_s": round(1.0 / t.min(), 3), "median_tokens_per_s": round(1.0 / np.median(t), 3)}
+
+
+def cpu_baseline(lw, x, target_s=12.0, scalar_s=6.0, max_tokens=256):
+    """The reference's own kernels (oracle/_ref) on the host, one token at a
+    time in the engine's MoE order, in two modes, each until its time budget or
+    max_tokens tokens:
+      reference-default  KernelIsa::Auto (AVX2+FMA) with WorkerPool threads
+      reference-scalar   KernelIsa::Scalar, one thread (a shorter sample)
+    `value` is the default mode's tokens/s over its sample.
+
+    Two threads for the default mode: the reference's WorkerPool
+    (kernels.cpp:414-459) publishes `pending = ranges - 1` into every worker's
+    slot, each worker decrements only its own slot, and the caller waits for
+    worker 0's slot to reach zero, so a split into more than two ranges never
+    completes. Two threads (one range each for the caller and worker 0) is the
+    largest count that finishes; it is also the thread count of the
+    reference's own 2-vCPU test machine."""
     sys.path.insert(0, str(ROOT / "oracle"))
     import numpy as np
     import fmoracle as fo
     hl = fo.host_layer(lw)
     threads = 2
     outs, idss, ws = [], [], []
-    hl.ref_forward_batch(x[:1], fo.ISA_AVX2, threads=threads)  # wakes the worker pool
-    t0 = time.perf_counter()
-    last = t0
-    n = 0
-    while n < min(max_tokens, len(x)):
-        o, i, w = hl.ref_forward_batch(x[n:n + 1], fo.ISA_AVX2, threads=threads)
+
+    def default_one(i):
+        o, ids, w = hl.ref_forward_batch(x[i:i + 1], fo.ISA_AVX2, threads=threads)
         outs.append(o)
-        idss.append(i)
+        idss.append(ids)
         ws.append(w)
-        n += 1
-        now = time.perf_counter()
-        if now - last > 5.0:
-            print(f"[bench] cpu baseline: {n} tokens in {now - t0:.1f}s", file=sys.stderr, flush=True)
-            last = now
-        if now - t0 > target_s:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": round(n / dt, 3), "unit": "tokens/s", "cores": threads, "kind": "reference",
+
+    hl.ref_forward_batch(x[:1], fo.ISA_AVX2, threads=threads)  # wakes the worker pool
+    t_def = timed_tokens(default_one, min(max_tokens, len(x)), target_s, "cpu baseline (AVX2)")
+    t_sc = timed_tokens(lambda i: hl.ref_forward_batch(x[i:i + 1], fo.ISA_SCALAR, threads=1),
+                        min(max_tokens, len(x)), scalar_s, "cpu baseline (scalar)")
+    n = len(t_def)
+    dflt, scal = rate_summary(t_def), rate_summary(t_sc)
+    base = {"value": dflt["tokens_per_s"], "unit": "tokens/s", "cores": threads, "kind": "reference",
             "sample": f"first {n} of the 1000 tokens, one at a time, through the reference's gemv/gemv_quant "
-                      f"(KernelIsa::Auto = AVX2+FMA, WorkerPool {threads} threads) in the engine's MoE order"}, \
-        (np.concatenate(outs), np.concatenate(idss), np.concatenate(ws), n)
+                      f"(KernelIsa::Auto = AVX2+FMA, WorkerPool {threads} threads) in the engine's MoE order",
+            "modes": {"reference-default": dict(dflt, isa="Auto (AVX2+FMA)", threads=threads),
+                      "reference-scalar": dict(scal, isa="Scalar", threads=1,
+                                               sample=f"first {scal['tokens']} tokens (subsampled)")},
+            "host": host_info()}
+    return base, (np.concatenate(outs), np.concatenate(idss), np.concatenate(ws), n)
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -94,9 +145,11 @@ PREFILL_TITLES = {
 
 def prefill_leg(dev, workload=PREFILL_WORKLOAD, seed=1234, reps=10, cpu=True, cpu_seconds=10.0):
     """A whole-layer prefill (routing, bucketing, both grouped GEMMs, combine)
-    timed with HIP events on the launch stream, against bf16 MFMA peak, HBM
-    peak and the ragged bound sum_e max(flops_e / MFMA peak, bytes_e / HBM
-    peak) over the experts that received tokens."""
+    timed with HIP events on the launch stream; the roofline is the gate/up
+    GEMM's (4 pairs H F flops per launch over its own duration between events
+    the launch records) against bf16 MFMA peak; the layer's fractions of MFMA
+    peak, HBM peak and the ragged bound sum_e max(flops_e / MFMA peak,
+    bytes_e / HBM peak) over the experts that received tokens sit beside it."""
     import numpy as np
     import torch
     from freemoe_amd import fmx
@@ -136,33 +189,51 @@ def prefill_leg(dev, workload=PREFILL_WORKLOAD, seed=1234, reps=10, cpu=True, cp
     gbs = (wbytes + act_bytes) / (ms * 1e-3) / 1e9
     ragged_s = sum(max(6.0 * n * H * F / (MFMA_BF16_PEAK_TFLOPS * 1e12), per_expert / (HBM_PEAK_GBS * 1e9))
                    for n in counts if n > 0)
+    # the GEMMs' own times, from events their launches record
+    gu_ms, dn_ms = [], []
+    for _ in range(reps):
+        km = []
+        dl.prefill(xd, out, ids, wts, kernel_ms=km)
+        gu_ms.append(km[0])
+        dn_ms.append(km[1])
+    gu_ms, dn_ms = float(np.mean(gu_ms)), float(np.mean(dn_ms))
+    gu_flops = 4.0 * pairs * H * F
+    gu_tflops = gu_flops / (gu_ms * 1e-3) / 1e12
+    gu_wbytes = int((counts > 0).sum()) * per_expert * 2 // 3  # gate and up of the experts with pairs
+    gu_tile = "GQ80" if lw.gate_type == wl.Q8_0 else ("GQ40" if lw.gate_type == wl.Q4_0 else "GQ4K")
+    dn_tile = "GQ80" if lw.down_type == wl.Q8_0 else ("GQ40" if lw.down_type == wl.Q4_0 else "GQ4K")
     res = {"workload": PREFILL_TITLES[workload], "tokens": T, "hidden": H,
            "ffn": F, "experts": E, "top_k": K, "expert_weights": wl.TYPE_NAMES[lw.gate_type].upper(),
            "ms": round(ms, 4), "tokens_per_s": round(T / (ms * 1e-3), 1),
            "expert_token_counts": counts.tolist(),
-           "roofline": {"bound": "mfma", "kernel": "whole layer (route, bucket, gather, gate/up GEMM, down GEMM, "
-                                                   "combine)", "achieved": round(tflops, 1),
-                        "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flops": flops,
-                        "hbm_achieved_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-                        "hbm_bytes": wbytes + act_bytes,
-                        "ragged_bound_ms": round(ragged_s * 1e3, 4),
-                        "ragged_frac": round(ragged_s * 1e3 / ms, 4)}}
+           "roofline": {"bound": "mfma", "kernel": f"gate_up_gemm_kernel<{gu_tile}, {dn_tile}>",
+                        "achieved": round(gu_tflops, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(gu_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "flops_per_launch": gu_flops,
+                        "mean_us": round(gu_ms * 1e3, 3),
+                        "hbm_GBs": round(gu_wbytes / (gu_ms * 1e-3) / 1e9, 1),
+                        "hbm_frac": round(gu_wbytes / (gu_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "weight_bytes_per_launch": gu_wbytes},
+           "down_gemm": {"kernel": f"down_gemm_kernel<{dn_tile}>", "mean_us": round(dn_ms * 1e3, 3),
+                         "achieved_TFLOPs": round(2.0 * pairs * H * F / (dn_ms * 1e-3) / 1e12, 1)},
+           "layer": {"achieved_TFLOPs": round(tflops, 1), "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "flops": flops, "hbm_achieved_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "hbm_bytes": wbytes + act_bytes, "ragged_bound_ms": round(ragged_s * 1e3, 4),
+                     "ragged_frac": round(ragged_s * 1e3 / ms, 4)}}
     if cpu:
         sys.path.insert(0, str(ROOT / "oracle"))
         import fmoracle as fo
         hl = fo.host_layer(lw)
-        n, t0 = 0, time.perf_counter()
         outs = []
-        while n < T and time.perf_counter() - t0 < cpu_seconds:
-            o, _, _ = hl.ref_forward_batch(x[n:n + 1], fo.ISA_AVX2, threads=2)
-            outs.append(o)
-            n += 1
-        dt = time.perf_counter() - t0
+        times = timed_tokens(lambda i: outs.append(hl.ref_forward_batch(x[i:i + 1], fo.ISA_AVX2, threads=2)[0]),
+                             T, cpu_seconds, "prefill cpu baseline")
+        n = len(times)
         ref = np.concatenate(outs).astype(np.float64) - x[:n]
         got = out[:n].cpu().numpy().astype(np.float64) - x[:n]
         err = got - ref
-        res["cpu_baseline"] = {"value": round(n / dt, 3), "unit": "tokens/s", "cores": 2, "kind": "reference",
+        rs = rate_summary(times)
+        res["cpu_baseline"] = {"value": rs["tokens_per_s"], "unit": "tokens/s", "cores": 2, "kind": "reference",
+                               "best_tokens_per_s": rs["best_tokens_per_s"],
+                               "median_tokens_per_s": rs["median_tokens_per_s"],
                                "sample": f"first {n} of the {T} tokens, one at a time (the reference has no "
                                          "batched MoE path), reference gemv_quant at 2 WorkerPool threads"}
         res["parity"] = {"tokens": n, "ids_equal": None,

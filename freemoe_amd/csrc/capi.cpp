@@ -492,8 +492,14 @@ uint64_t fmx_moe_prefill_workspace_bytes(const fmx_moe_layer *L, uint32_t tokens
     return prefill_workspace(L, tokens).total;
 }
 
-int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
-                    float *weights, void *workspace, uint64_t workspace_bytes, void *stream) {
+namespace {
+
+// fmx_moe_prefill; kev (optional) as launch_prefill_experts. *tiled: whether
+// the grouped GEMMs ran (false: the decode kernels, per token).
+int prefill_layer(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
+                  float *weights, void *workspace, uint64_t workspace_bytes, void *stream, hipEvent_t *kev,
+                  bool *tiled) {
+    *tiled = false;
     if (int rc = fault_gate()) return rc;
     if (int rc = validate_layer(L)) return rc;
     if (tokens == 0) return FMX_OK;
@@ -544,8 +550,46 @@ int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t
                                reinterpret_cast<uint32_t *>(base + ws.rank_list), slot_of, status, s,
                                reinterpret_cast<uint32_t *>(base + ws.tiles), kPrefillTileRows))
         return rc;
-    if (int rc = launch_prefill_experts(ea, b, ws.max_tiles, s)) return rc;
+    if (int rc = launch_prefill_experts(ea, b, ws.max_tiles, s, kev)) return rc;
+    *tiled = true;
     return launch_combine(x, b.dn, b.splits, b.pairs, slot_of, weights, L->hidden, L->top_k, tokens, out, s);
+}
+
+} // namespace
+
+int fmx_moe_prefill(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
+                    float *weights, void *workspace, uint64_t workspace_bytes, void *stream) {
+    bool tiled;
+    return prefill_layer(L, x, out, tokens, ids, weights, workspace, workspace_bytes, stream, nullptr, &tiled);
+}
+
+int fmx_moe_prefill_timed(const fmx_moe_layer *L, const float *x, float *out, uint32_t tokens, uint32_t *ids,
+                          float *weights, void *workspace, uint64_t workspace_bytes, void *stream,
+                          double *kernel_ms) {
+    if (!kernel_ms) return FMX_ERR_INVALID_ARGUMENT;
+    kernel_ms[0] = kernel_ms[1] = 0.0;
+    hipEvent_t kev[4] = {};
+    for (auto &e : kev)
+        if (hipEventCreate(&e) != hipSuccess) {
+            for (auto &f : kev)
+                if (f) (void)hipEventDestroy(f);
+            return FMX_ERR_LAUNCH_FAILED;
+        }
+    bool tiled = false;
+    int rc = prefill_layer(L, x, out, tokens, ids, weights, workspace, workspace_bytes, stream, kev, &tiled);
+    if (rc == FMX_OK && hipStreamSynchronize(static_cast<hipStream_t>(stream)) != hipSuccess)
+        rc = FMX_ERR_LAUNCH_FAILED;
+    if (rc == FMX_OK && !tiled) rc = FMX_ERR_SHAPE_MISMATCH;
+    if (rc == FMX_OK) {
+        float a = 0, b = 0;
+        if (hipEventElapsedTime(&a, kev[0], kev[1]) != hipSuccess ||
+            hipEventElapsedTime(&b, kev[2], kev[3]) != hipSuccess)
+            rc = FMX_ERR_LAUNCH_FAILED;
+        kernel_ms[0] = a;
+        kernel_ms[1] = b;
+    }
+    for (auto &e : kev) (void)hipEventDestroy(e);
+    return rc;
 }
 
 int fmx_moe_status(void *workspace, void *stream) {

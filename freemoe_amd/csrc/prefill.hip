@@ -25,6 +25,8 @@
 #include "moe.hpp"
 #include "prefill.hpp"
 
+#include <hip/hip_ext.h>
+
 namespace fmx {
 
 namespace {
@@ -578,7 +580,7 @@ int launch_gather(const float *h, uint32_t hidden, uint32_t tokens, uint32_t K, 
 }
 
 template <class T, class TD>
-int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s) {
+int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s, hipEvent_t *kev) {
     const size_t lds = 2ull * kGBufBytes; // two activation buffers
     auto gu = gate_up_gemm_kernel<T, TD>;
     auto dn = down_gemm_kernel<TD>;
@@ -586,11 +588,21 @@ int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tile
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds)) return rc;
     if (b.pairs == 0) return FMX_OK;
     if (int rc = launch_gather<T>(b.h, a.hidden, b.tokens, b.top_k, b.slot_of, b.pairs, b.x, s)) return rc;
-    hipLaunchKernelGGL(gu, dim3(a.ffn / 128, max_tiles), dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.x, b.act);
-    FMX_LAUNCH_CHECK();
+    const dim3 gu_grid(a.ffn / 128, max_tiles), dn_grid(a.hidden / 256, b.splits, max_tiles);
     const uint32_t steps = a.ffn / kGStepK / b.splits;
-    hipLaunchKernelGGL(dn, dim3(a.hidden / 256, b.splits, max_tiles), dim3(kGThreads), lds, s, a, b.tiles, b.pairs,
-                       b.act, steps, b.dn);
+    if (kev) {
+        // the launches record kev[0..1] / kev[2..3] at kernel start and end
+        hipExtLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, kev[0], kev[1], 0, a, b.tiles, b.pairs, b.x,
+                              b.act);
+        FMX_LAUNCH_CHECK();
+        hipExtLaunchKernelGGL(dn, dn_grid, dim3(kGThreads), lds, s, kev[2], kev[3], 0, a, b.tiles, b.pairs, b.act,
+                              steps, b.dn);
+        FMX_LAUNCH_CHECK();
+        return FMX_OK;
+    }
+    hipLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.x, b.act);
+    FMX_LAUNCH_CHECK();
+    hipLaunchKernelGGL(dn, dn_grid, dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.act, steps, b.dn);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
@@ -613,28 +625,29 @@ bool prefill_gemm_supported(const ExpertArgs &a) {
            a.hidden % kGStepK == 0 && a.ffn % kGStepK == 0;
 }
 
-int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s) {
+int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s,
+                           hipEvent_t *kev) {
     if (!prefill_gemm_supported(a)) return FMX_ERR_SHAPE_MISMATCH;
     switch (a.type_gu) {
     case FMX_TYPE_Q8_0:
         switch (a.type_dn) {
-        case FMX_TYPE_Q8_0: return launch_gemms<GQ80, GQ80>(a, b, max_tiles, s);
-        case FMX_TYPE_Q4_0: return launch_gemms<GQ80, GQ40>(a, b, max_tiles, s);
-        case FMX_TYPE_Q4_K: return launch_gemms<GQ80, GQ4K>(a, b, max_tiles, s);
+        case FMX_TYPE_Q8_0: return launch_gemms<GQ80, GQ80>(a, b, max_tiles, s, kev);
+        case FMX_TYPE_Q4_0: return launch_gemms<GQ80, GQ40>(a, b, max_tiles, s, kev);
+        case FMX_TYPE_Q4_K: return launch_gemms<GQ80, GQ4K>(a, b, max_tiles, s, kev);
         }
         break;
     case FMX_TYPE_Q4_0:
         switch (a.type_dn) {
-        case FMX_TYPE_Q8_0: return launch_gemms<GQ40, GQ80>(a, b, max_tiles, s);
-        case FMX_TYPE_Q4_0: return launch_gemms<GQ40, GQ40>(a, b, max_tiles, s);
-        case FMX_TYPE_Q4_K: return launch_gemms<GQ40, GQ4K>(a, b, max_tiles, s);
+        case FMX_TYPE_Q8_0: return launch_gemms<GQ40, GQ80>(a, b, max_tiles, s, kev);
+        case FMX_TYPE_Q4_0: return launch_gemms<GQ40, GQ40>(a, b, max_tiles, s, kev);
+        case FMX_TYPE_Q4_K: return launch_gemms<GQ40, GQ4K>(a, b, max_tiles, s, kev);
         }
         break;
     case FMX_TYPE_Q4_K:
         switch (a.type_dn) {
-        case FMX_TYPE_Q8_0: return launch_gemms<GQ4K, GQ80>(a, b, max_tiles, s);
-        case FMX_TYPE_Q4_0: return launch_gemms<GQ4K, GQ40>(a, b, max_tiles, s);
-        case FMX_TYPE_Q4_K: return launch_gemms<GQ4K, GQ4K>(a, b, max_tiles, s);
+        case FMX_TYPE_Q8_0: return launch_gemms<GQ4K, GQ80>(a, b, max_tiles, s, kev);
+        case FMX_TYPE_Q4_0: return launch_gemms<GQ4K, GQ40>(a, b, max_tiles, s, kev);
+        case FMX_TYPE_Q4_K: return launch_gemms<GQ4K, GQ4K>(a, b, max_tiles, s, kev);
         }
         break;
     }

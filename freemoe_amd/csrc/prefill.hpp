@@ -31,7 +31,10 @@ bool prefill_gemm_supported(const ExpertArgs &a);
 // combine).
 uint32_t prefill_down_splits(uint32_t experts, uint32_t ffn);
 // gather -> gate/up GEMM + SwiGLU -> down GEMM, over `max_tiles` row tiles.
-int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s);
+// kev (optional): events the gate/up launch records at its start and end
+// (kev[0], kev[1]) and the down launch likewise (kev[2], kev[3]).
+int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s,
+                           hipEvent_t *kev = nullptr);
 // out[t] = x[t] + sum over ranks (rank order) of w * (sum over splits of
 // dn[split][slot_of[t, r]]).
 int launch_combine(const float *x, const float *dn, uint32_t splits, uint32_t pairs, const uint32_t *slot_of,

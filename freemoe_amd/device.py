@@ -92,8 +92,10 @@ class DeviceLayer:
                  wts.data_ptr(), ws.data_ptr(), ws.numel(), fmx.stream_handle(stream))
         return out, ids, wts
 
-    def prefill(self, x: torch.Tensor, out=None, ids=None, wts=None, stream=None):
-        """The whole layer over all rows of x at once (grouped GEMMs)."""
+    def prefill(self, x: torch.Tensor, out=None, ids=None, wts=None, stream=None, kernel_ms=None):
+        """The whole layer over all rows of x at once (grouped GEMMs). With
+        kernel_ms (a list), runs fmx_moe_prefill_timed and appends the gate/up
+        and down GEMMs' own milliseconds (synchronises the stream)."""
         t = x.shape[0]
         K = self.w.top_k
         out = torch.empty_like(x) if out is None else out
@@ -105,8 +107,14 @@ class DeviceLayer:
         if self.prefill_workspace is None or self.prefill_workspace.numel() < need:
             self.prefill_workspace = torch.zeros(need, dtype=torch.uint8, device=self.device)
         ws = self.prefill_workspace
-        fmx.call("fmx_moe_prefill", ctypes.byref(self.desc), x.data_ptr(), out.data_ptr(), t, ids.data_ptr(),
-                 wts.data_ptr(), ws.data_ptr(), ws.numel(), fmx.stream_handle(stream))
+        if kernel_ms is None:
+            fmx.call("fmx_moe_prefill", ctypes.byref(self.desc), x.data_ptr(), out.data_ptr(), t, ids.data_ptr(),
+                     wts.data_ptr(), ws.data_ptr(), ws.numel(), fmx.stream_handle(stream))
+        else:
+            ms = (ctypes.c_double * 2)()
+            fmx.call("fmx_moe_prefill_timed", ctypes.byref(self.desc), x.data_ptr(), out.data_ptr(), t,
+                     ids.data_ptr(), wts.data_ptr(), ws.data_ptr(), ws.numel(), fmx.stream_handle(stream), ms)
+            kernel_ms.extend([ms[0], ms[1]])
         return out, ids, wts
 
     def prefill_status(self, stream=None) -> int:

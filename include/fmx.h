@@ -224,6 +224,16 @@ int fmx_moe_prefill(const fmx_moe_layer *layer, const float *x, float *out, uint
                     uint32_t *ids, float *weights, void *workspace, uint64_t workspace_bytes,
                     void *stream);
 
+/* Instrumented fmx_moe_prefill (no reference counterpart; for measurement):
+ * the same launches on `stream`; kernel_ms[0] and kernel_ms[1] receive the
+ * gate/up and the down grouped GEMM's own execution time, between events
+ * their launches record at kernel start and end (hipExtLaunchKernelGGL), in
+ * milliseconds. Synchronises the stream. FMX_ERR_SHAPE_MISMATCH when the
+ * grouped GEMMs do not run (no tokens, or a shape they do not tile). */
+int fmx_moe_prefill_timed(const fmx_moe_layer *layer, const float *x, float *out, uint32_t tokens,
+                          uint32_t *ids, float *weights, void *workspace, uint64_t workspace_bytes,
+                          void *stream, double *kernel_ms);
+
 /* Device error word written by the routing kernels (non-finite score or an
  * expert id out of range): reads and clears it, blocking on `stream`. */
 int fmx_moe_status(void *workspace, void *stream);

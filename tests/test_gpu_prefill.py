@@ -130,3 +130,26 @@ def test_prefill_matches_decode_routing(gpu):
     torch.cuda.synchronize()
     assert torch.equal(ids_p, ids_d)
     assert torch.equal(w_p, w_d)
+
+
+def test_prefill_timed_matches_prefill(gpu):
+    """The instrumented prefill (events recorded by the GEMM launches) gives
+    the plain prefill's outputs bit for bit and positive GEMM times; a shape
+    the GEMMs do not tile is refused with FMX_ERR_SHAPE_MISMATCH."""
+    import torch
+    from freemoe_amd import fmx
+    lw = wl.make_layer(256, 512, 8, 2, wl.Q8_0, 61)
+    x = torch.from_numpy(wl.inputs(256, 40, 62)).to(gpu)
+    dl = DeviceLayer(lw, gpu)
+    out1, ids1, w1 = dl.prefill(x)
+    out1, ids1, w1 = out1.clone(), ids1.clone(), w1.clone()
+    ms = []
+    out2, ids2, w2 = dl.prefill(x, kernel_ms=ms)
+    torch.cuda.synchronize()
+    assert dl.prefill_status() == 0
+    assert torch.equal(out1.view(torch.int32), out2.view(torch.int32))
+    assert torch.equal(ids1, ids2) and torch.equal(w1, w2)
+    assert len(ms) == 2 and all(v > 0.0 for v in ms)
+    f32 = DeviceLayer(wl.make_layer(64, 128, 4, 2, wl.F32, 5), gpu)
+    with pytest.raises(fmx.FmxError):
+        f32.prefill(torch.from_numpy(wl.inputs(64, 4, 6)).to(gpu), kernel_ms=[])
