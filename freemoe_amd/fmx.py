@@ -7,10 +7,13 @@ is no fallback path.
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, c_char, c_char_p, c_double, c_int, c_int32, c_uint16, c_uint32, c_uint64, c_void_p
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libfmx.so"
+# FMX_LIBRARY: another build of the same library (the host-sanitizer build of
+# the CPU tests); by default the in-tree libfmx.so.
+LIB_PATH = Path(os.environ.get("FMX_LIBRARY") or Path(__file__).resolve().parent / "libfmx.so")
 
 FMX_TYPE_F32, FMX_TYPE_Q4_0, FMX_TYPE_Q8_0, FMX_TYPE_Q4_K = 0, 2, 8, 12
 BLOCK_GEOMETRY = {FMX_TYPE_F32: (1, 4), FMX_TYPE_Q4_0: (32, 18), FMX_TYPE_Q8_0: (32, 34),

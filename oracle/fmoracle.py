@@ -6,13 +6,15 @@ cpu_baseline leg of bench.py, as the checker. Nothing in freemoe_amd/ imports it
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import POINTER, c_double, c_float, c_int, c_uint16, c_uint32, c_uint64, c_void_p
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-ORACLE_PATH = HERE / "libfmoracle.so"
+# FMORACLE_LIBRARY: another build of the C restatement (the host-sanitizer build)
+ORACLE_PATH = Path(os.environ.get("FMORACLE_LIBRARY") or HERE / "libfmoracle.so")
 REF_PATH = HERE / "_ref" / "libfmref.so"
 
 ISA_SCALAR, ISA_AVX2 = 0, 1
