@@ -69,6 +69,7 @@ _SIGNATURES = {
     "fmx_packed_bytes": (c_uint64, [c_uint32, c_uint32, c_uint32]),
     "fmx_pack": (c_int, [c_uint32, c_void_p, c_void_p, c_uint32, c_uint32, c_void_p]),
     "fmx_matvec": (c_int, [c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_void_p]),
+    "fmx_gemm_quant": (c_int, [c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32, c_void_p]),
     "fmx_moe_workspace_bytes": (c_uint64, [POINTER(MoELayer), c_uint32]),
     "fmx_moe_route": (c_int, [POINTER(MoELayer), c_void_p, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_uint64, c_void_p]),

@@ -24,3 +24,22 @@ std::unique_ptr<Backend> Backend::create(const BackendConfig &config, TraceWrite
 }
 
 } // namespace fm
+
+extern "C" void fmx_engine_gemv_quant(const fm::KernelConfig &config, uint32_t type_id, const uint8_t *weights,
+                                      const float *x, float *y, uint32_t out_dim, uint32_t in_dim) {
+    if (fm::HipBackend *b = fm::HipBackend::owner_of(weights)) {
+        b->matvec_quant(type_id, weights, x, y, out_dim, in_dim, "gemv_quant");
+        return;
+    }
+    fm::gemv_quant(config, type_id, weights, x, y, out_dim, in_dim);
+}
+
+extern "C" void fmx_engine_gemm_quant(const fm::KernelConfig &config, uint32_t type_id, const uint8_t *weights,
+                                      const float *x, float *y, uint32_t tokens, uint32_t out_dim,
+                                      uint32_t in_dim) {
+    if (fm::HipBackend *b = fm::HipBackend::owner_of(weights)) {
+        b->gemm_quant(type_id, weights, x, y, tokens, out_dim, in_dim, "gemm_quant");
+        return;
+    }
+    fm::gemm_quant(config, type_id, weights, x, y, tokens, out_dim, in_dim);
+}

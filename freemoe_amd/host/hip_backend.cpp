@@ -132,13 +132,40 @@ struct HipBackend::State {
     }
 };
 
+namespace {
+
+// Live backends, for owner_of.
+std::mutex g_backends_mutex;
+std::vector<HipBackend *> g_backends;
+
+} // namespace
+
 HipBackend::HipBackend(BackendConfig config, TraceWriter *trace)
     : Backend(std::move(config), trace), state_(std::make_shared<State>()) {
     fmx_device_info fi;
     state_->have_device = fmx_device_info_get(0, &fi) == FMX_OK;
+    std::lock_guard<std::mutex> lock(g_backends_mutex);
+    g_backends.push_back(this);
 }
 
-HipBackend::~HipBackend() = default; // buffers still out hold the state
+HipBackend::~HipBackend() { // buffers still out hold the state
+    std::lock_guard<std::mutex> lock(g_backends_mutex);
+    for (auto it = g_backends.begin(); it != g_backends.end(); ++it)
+        if (*it == this) {
+            g_backends.erase(it);
+            break;
+        }
+}
+
+HipBackend *HipBackend::owner_of(const void *host) {
+    std::lock_guard<std::mutex> lock(g_backends_mutex);
+    for (HipBackend *b : g_backends) {
+        std::lock_guard<std::mutex> state_lock(b->state_->mutex);
+        uint64_t off = 0;
+        if (b->state_->find_twin(host, &off)) return b;
+    }
+    return nullptr;
+}
 
 void HipBackend::check(int status, const std::string &where) const { check_status(status, where); }
 
@@ -315,6 +342,32 @@ void HipBackend::matvec_quant(uint32_t type_id, const void *weights, const float
     check(fmx_download(y, s.y_dev, static_cast<uint64_t>(out_dim) * 4, s.stream), op_name);
     record_operation({op_name, name(), raw_bytes(type_id, out_dim, in_dim) + in_dim * 4ull,
                       static_cast<uint64_t>(out_dim) * sizeof(float)});
+}
+
+void HipBackend::gemm_quant(uint32_t type_id, const void *weights, const float *x, float *y, uint32_t tokens,
+                            uint32_t out_dim, uint32_t in_dim, const std::string &op_name) {
+    if (fault_ == BackendFault::DeviceLoss) fail(ErrorCode::DEVICE_LOSS, "injected device loss");
+    if (tokens == 0 || out_dim == 0 || in_dim == 0) return;
+    if (!weights || !x || !y) fail(ErrorCode::INVALID_ARGUMENT, "invalid batched product arguments");
+    uint32_t bs = 0, bb = 0;
+    if (fmx_quant_geometry(type_id, &bs, &bb) != FMX_OK)
+        fail(ErrorCode::UNSUPPORTED_QUANTISATION, "no kernel for tensor type " + std::to_string(type_id));
+    if (in_dim % bs) fail(ErrorCode::SHAPE_MISMATCH, "quantised row length is not a whole number of blocks");
+    const uint64_t w_bytes = raw_bytes(type_id, out_dim, in_dim);
+    std::lock_guard<std::mutex> lock(state_->mutex);
+    State &s = *state_;
+    uint64_t off = 0;
+    const State::Twin *t = s.find_twin(weights, &off);
+    if (!t || off + w_bytes > t->bytes)
+        fail(ErrorCode::INVALID_ARGUMENT, "batched product weights are not in a device buffer: " + op_name);
+    const uint64_t x_bytes = static_cast<uint64_t>(tokens) * in_dim * 4, y_bytes = static_cast<uint64_t>(tokens) * out_dim * 4;
+    ensure_scratch(x_bytes, y_bytes);
+    check(fmx_upload(s.x_dev, x, x_bytes, s.stream, nullptr), op_name);
+    check(fmx_gemm_quant(type_id, static_cast<uint8_t *>(t->device) + off, static_cast<const float *>(s.x_dev),
+                         static_cast<float *>(s.y_dev), tokens, out_dim, in_dim, s.stream),
+          op_name);
+    check(fmx_download(y, s.y_dev, y_bytes, s.stream), op_name);
+    record_operation({op_name, name(), w_bytes + x_bytes, y_bytes});
 }
 
 void HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, uint32_t *ids, float *weights) {

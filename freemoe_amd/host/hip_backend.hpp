@@ -79,13 +79,24 @@ public:
     // h = RMSNorm(x); ids / weights receive the routing in rank order (the
     // RoutingEvent's experts). Logs the reference's operation names
     // (router.L*, router_gating.L*, router_topk.L*, expert_gate/up/down.L*.E*,
-    // expert_swiglu.L*, expert_combine.L*) under this backend's label. The
-    // engine's optional hook at engine.cpp:1602.
+    // expert_swiglu.L*, expert_combine.L*) under this backend's label. Meant
+    // for a call at the top of the engine's routed branch (engine.cpp:1602),
+    // which skips the per-expert loop when the layer ran here.
     void moe_layer(const MoeLayerView &layer, const float *x, float *out, uint32_t *ids, float *weights);
+
+    // gemm_quant (include/fm/kernels.hpp:68) for a matrix (raw rows, any
+    // supported type) inside one of this backend's buffers: y[t][o] for
+    // tokens t, bit for bit the reference's (fmx_gemm_quant). The batched
+    // prefill's projections (engine.cpp:2007-2024) call this.
+    void gemm_quant(uint32_t type_id, const void *weights, const float *x, float *y, uint32_t tokens,
+                    uint32_t out_dim, uint32_t in_dim, const std::string &op_name);
 
     // Device address of a host pointer inside one of this backend's buffers
     // (nullptr when it is not in one).
     void *device_address(const void *host) const;
+
+    // The live HipBackend whose buffers hold `host`, or nullptr.
+    static HipBackend *owner_of(const void *host);
 
     struct State;
 

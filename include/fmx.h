@@ -132,6 +132,16 @@ int fmx_pack(uint32_t type_id, const void *raw, void *packed, uint32_t rows, uin
 int fmx_matvec(uint32_t type_id, const void *packed, const float *x, float *y,
                uint32_t out_dim, uint32_t in_dim, void *stream);
 
+/* gemm_quant (include/fm/kernels.hpp:68; kernels.cpp:289-345), the batched
+ * product of the engine's dense prefill (engine.cpp:2007-2024):
+ * y[t][o] = dot(dequantize_row(W row o), x[t]) for tokens t < `tokens`, W in
+ * its raw GGUF rows (device, not packed), x [tokens x in_dim] and
+ * y [tokens x out_dim] device F32. Bit-identical to the reference's
+ * KernelIsa::Auto path (dot_avx2, kernels.cpp:206-223). No-op for a zero
+ * dimension, as the reference. */
+int fmx_gemm_quant(uint32_t type_id, const void *weights, const float *x, float *y, uint32_t tokens,
+                   uint32_t out_dim, uint32_t in_dim, void *stream);
+
 /* ------------------------------------------------------------ MoE layer -- */
 
 /* One routed MoE layer with softmax gating (engine.cpp:1602-1776). All pointers

@@ -307,6 +307,35 @@ int fmo_gemv(int isa, uint32_t type_id, const uint8_t *weights, const float *x, 
     return FMO_OK;
 }
 
+/* gemm_quant / gemm_rows (kernels.cpp:289-345): every row dequantised
+ * (dequantize_row) and dotted with each token's input by dot_isa
+ * (kernels.cpp:251-260): dot_avx2 (kernels.cpp:206-223, the order of
+ * gemv_avx2_row) for the AVX2 ISA, the plain multiply-add loop for the scalar
+ * one. y is [tokens x out_dim], x [tokens x in_dim]. */
+int fmo_gemm(int isa, uint32_t type_id, const uint8_t *weights, const float *x, float *y, uint32_t tokens,
+             uint32_t out_dim, uint32_t in_dim) {
+    if (tokens == 0 || out_dim == 0 || in_dim == 0) return FMO_OK;
+    if (!weights || !x || !y) return FMO_ERR_INVALID_ARGUMENT;
+    uint32_t bs, bb;
+    int rc = fmo_quant_geometry(type_id, &bs, &bb);
+    if (rc) return rc;
+    if (in_dim % bs) return FMO_ERR_SHAPE_MISMATCH;
+    const uint64_t row_bytes = (uint64_t)(in_dim / bs) * bb;
+    float *rowf = (float *)malloc((size_t)in_dim * sizeof(float));
+    if (!rowf) return FMO_ERR_INVALID_ARGUMENT;
+    for (uint32_t o = 0; o < out_dim; ++o) {
+        rc = fmo_dequantize_region(type_id, weights + (uint64_t)o * row_bytes, rowf, in_dim);
+        if (rc) break;
+        for (uint32_t t = 0; t < tokens; ++t) {
+            const float *xt = x + (uint64_t)t * in_dim;
+            y[(uint64_t)t * out_dim + o] =
+                isa == FMO_ISA_SCALAR ? dot_scalar(rowf, xt, in_dim) : dot_f32_avx2(rowf, xt, in_dim);
+        }
+    }
+    free(rowf);
+    return rc;
+}
+
 /* ------------------------------------------------------------------------ */
 /* Layer pieces                                                              */
 /* ------------------------------------------------------------------------ */

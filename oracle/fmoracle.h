@@ -61,6 +61,11 @@ int fmo_dequantize_region(uint32_t type_id, const uint8_t *src, float *dst, uint
 int fmo_gemv(int isa, uint32_t type_id, const uint8_t *weights, const float *x, float *y,
              uint32_t out_dim, uint32_t in_dim);
 
+/* y[tokens x out_dim] = x[tokens x in_dim] * W^T (gemm_quant: each row
+ * dequantised, then dot_isa per token). */
+int fmo_gemm(int isa, uint32_t type_id, const uint8_t *weights, const float *x, float *y, uint32_t tokens,
+             uint32_t out_dim, uint32_t in_dim);
+
 int fmo_rmsnorm(const float *x, const float *w, uint32_t n, double eps, double norm_bias,
                 float *y);
 int fmo_softmax(const float *v, uint32_t n, float *out);

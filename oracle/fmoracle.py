@@ -51,12 +51,13 @@ def oracle() -> ctypes.CDLL:
         lib = ctypes.CDLL(str(ORACLE_PATH))
         lib.fmo_fp16_to_f32.restype = c_float
         lib.fmo_fp16_to_f32.argtypes = [c_uint16]
-        for name in ["fmo_dequantize_block", "fmo_dequantize_region", "fmo_gemv", "fmo_rmsnorm",
+        for name in ["fmo_dequantize_block", "fmo_dequantize_region", "fmo_gemv", "fmo_gemm", "fmo_rmsnorm",
                      "fmo_softmax", "fmo_topk", "fmo_route", "fmo_moe_layer", "fmo_moe_layer_batch",
                      "fmo_moe_bucket", "fmo_quant_geometry"]:
             getattr(lib, name).restype = c_int
         lib.fmo_dequantize_region.argtypes = [c_uint32, c_void_p, c_void_p, c_uint64]
         lib.fmo_gemv.argtypes = [c_int, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]
+        lib.fmo_gemm.argtypes = [c_int, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]
         lib.fmo_rmsnorm.argtypes = [c_void_p, c_void_p, c_uint32, c_double, c_double, c_void_p]
         lib.fmo_softmax.argtypes = [c_void_p, c_uint32, c_void_p]
         lib.fmo_topk.argtypes = [c_void_p, c_uint32, c_uint32, c_void_p]
@@ -84,6 +85,8 @@ def ref() -> ctypes.CDLL:
         lib.fmr_fp16_to_f32.argtypes = [c_uint16]
         lib.fmr_dequantize_block.argtypes = [c_uint32, c_void_p, c_void_p]
         lib.fmr_gemv.argtypes = [c_int, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]
+        lib.fmr_gemm.argtypes = [c_int, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32,
+                                 c_uint32]
         lib.fmr_moe_layer_batch.argtypes = [c_int, c_uint32, POINTER(Layer), c_void_p, c_void_p, c_void_p,
                                             c_void_p, c_uint32]
         lib.fmr_resolved_threads.restype = c_uint32
@@ -196,6 +199,25 @@ def ref_gemv(type_id: int, w: np.ndarray, x: np.ndarray, out_dim: int, in_dim: i
     w = np.ascontiguousarray(w)
     x = np.ascontiguousarray(x, dtype=np.float32)
     check(ref().fmr_gemv(isa, threads, type_id, _p(w), _p(x), _p(y), out_dim, in_dim), "fmr_gemv")
+    return y
+
+
+def gemm(type_id: int, w: np.ndarray, x: np.ndarray, out_dim: int, in_dim: int, isa: int = ISA_AVX2) -> np.ndarray:
+    """gemm_quant: x [tokens x in_dim] -> y [tokens x out_dim]."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_dim)
+    y = np.empty((x.shape[0], out_dim), np.float32)
+    w = np.ascontiguousarray(w)
+    check(oracle().fmo_gemm(isa, type_id, _p(w), _p(x), _p(y), x.shape[0], out_dim, in_dim), "fmo_gemm")
+    return y
+
+
+def ref_gemm(type_id: int, w: np.ndarray, x: np.ndarray, out_dim: int, in_dim: int, isa: int = ISA_AVX2,
+             threads: int = 1) -> np.ndarray:
+    """The reference's own gemm_quant."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, in_dim)
+    y = np.empty((x.shape[0], out_dim), np.float32)
+    w = np.ascontiguousarray(w)
+    check(ref().fmr_gemm(isa, threads, type_id, _p(w), _p(x), _p(y), x.shape[0], out_dim, in_dim), "fmr_gemm")
     return y
 
 

@@ -78,6 +78,16 @@ int fmr_gemv(int isa, uint32_t threads, uint32_t type_id, const uint8_t *w, cons
     }
 }
 
+int fmr_gemm(int isa, uint32_t threads, uint32_t type_id, const uint8_t *w, const float *x, float *y,
+             uint32_t tokens, uint32_t out_dim, uint32_t in_dim) {
+    try {
+        fm::gemm_quant(config_of(isa, threads), type_id, w, x, y, tokens, out_dim, in_dim);
+        return FMO_OK;
+    } catch (const fm::Error &e) {
+        return status_of(e);
+    }
+}
+
 // The decode MoE block per token (engine.cpp:1602-1776, 1822) with the
 // reference's kernels for the router and all expert projections.
 int fmr_moe_layer_batch(int isa, uint32_t threads, const fmo_layer *L, const float *x,

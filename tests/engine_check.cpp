@@ -25,6 +25,11 @@
 //       GPU-backend engine; prints one JSON line with the largest prompt-logit
 //       difference, the number of logits that differ in any bit, and whether
 //       routing records and greedy ids are identical.
+//   engine_check prompt <model.gguf> <generate> <text>
+//       the reference's conformance run (tests.cpp:1424-1468: run_prompt of a
+//       fixed text) on a CPU-backend and a GPU-backend engine; one JSON line
+//       as for twin. Block-type projections reach the GPU through the renamed
+//       gemv_quant / gemm_quant calls (backend_factory.cpp).
 // Exits non-zero on an engine error.
 #include "fm/engine.hpp"
 #include "fm/residency.hpp"
@@ -47,16 +52,26 @@ fm::RunConfig config_for(const std::string &model, bool gpu) {
     return rc;
 }
 
-// Operations in the backend's log by the backend label they ran under.
+// Operations in the backend's log by the backend label they ran under, and
+// (key "hooked") the kernels the engine called directly that ran on the
+// device through the renamed gemv_quant / gemm_quant.
 std::string op_labels(fm::Backend &b) {
-    std::map<std::string, uint64_t> by;
-    for (const auto &op : b.operations()) by[op.backend] += 1;
-    std::string s = "{";
-    for (const auto &kv : by) {
-        if (s.size() > 1) s += ",";
-        s += "\"" + kv.first + "\":" + std::to_string(kv.second);
+    std::map<std::string, uint64_t> by, hooked;
+    for (const auto &op : b.operations()) {
+        by[op.backend] += 1;
+        if (op.name == "gemv_quant" || op.name == "gemm_quant") hooked[op.name] += 1;
     }
-    return s + "}";
+    auto obj = [](const std::map<std::string, uint64_t> &m) {
+        std::string s = "{";
+        for (const auto &kv : m) {
+            if (s.size() > 1) s += ",";
+            s += "\"" + kv.first + "\":" + std::to_string(kv.second);
+        }
+        return s + "}";
+    };
+    std::string s = obj(by);
+    s.pop_back();
+    return s + (by.empty() ? "" : ",") + "\"hooked\":" + obj(hooked) + "}";
 }
 
 int compare(int argc, char **argv) {
@@ -102,23 +117,26 @@ int residency(int argc, char **argv) {
     return 0;
 }
 
-int twin(int argc, char **argv) {
-    if (argc < 7) return 2;
-    const uint32_t prompts = static_cast<uint32_t>(std::atoi(argv[3]));
-    const uint32_t len = static_cast<uint32_t>(std::atoi(argv[4]));
-    const uint32_t gen = static_cast<uint32_t>(std::atoi(argv[5]));
-    uint64_t seed = std::strtoull(argv[6], nullptr, 10);
-    fm::Engine cpu(config_for(argv[2], false)), gpu(config_for(argv[2], true));
+// CPU-backend and GPU-backend engines over the same prompts (explicit texts,
+// or `prompts` seeded random byte strings of length len when texts is empty).
+int twin_run(const std::string &model, std::vector<std::string> texts, uint32_t prompts, uint32_t len,
+             uint32_t gen, uint64_t seed) {
+    fm::Engine cpu(config_for(model, false)), gpu(config_for(model, true));
     cpu.initialize();
     gpu.initialize();
     double max_diff = 0.0;
     uint64_t differing = 0, logits = 0, routing_events = 0, generated = 0;
     bool routing_same = true, ids_same = true;
+    if (!texts.empty()) prompts = static_cast<uint32_t>(texts.size());
     for (uint32_t p = 0; p < prompts; ++p) {
         std::string prompt(len, '\0');
-        for (auto &c : prompt) {
-            seed = seed * 6364136223846793005ull + 1442695040888963407ull;
-            c = static_cast<char>(seed >> 56);
+        if (!texts.empty()) {
+            prompt = texts[p];
+        } else {
+            for (auto &c : prompt) {
+                seed = seed * 6364136223846793005ull + 1442695040888963407ull;
+                c = static_cast<char>(seed >> 56);
+            }
         }
         const fm::PromptResult a = cpu.run_prompt(prompt, gen);
         const fm::PromptResult b = gpu.run_prompt(prompt, gen);
@@ -150,6 +168,17 @@ int twin(int argc, char **argv) {
     return 0;
 }
 
+int twin(int argc, char **argv) {
+    if (argc < 7) return 2;
+    return twin_run(argv[2], {}, static_cast<uint32_t>(std::atoi(argv[3])), static_cast<uint32_t>(std::atoi(argv[4])),
+                    static_cast<uint32_t>(std::atoi(argv[5])), std::strtoull(argv[6], nullptr, 10));
+}
+
+int prompt(int argc, char **argv) {
+    if (argc < 5) return 2;
+    return twin_run(argv[2], {argv[4]}, 1, 0, static_cast<uint32_t>(std::atoi(argv[3])), 0);
+}
+
 } // namespace
 
 int main(int argc, char **argv) {
@@ -157,10 +186,11 @@ int main(int argc, char **argv) {
         if (argc >= 2 && std::string(argv[1]) == "compare") return compare(argc, argv);
         if (argc >= 2 && std::string(argv[1]) == "twin") return twin(argc, argv);
         if (argc >= 2 && std::string(argv[1]) == "residency") return residency(argc, argv);
+        if (argc >= 2 && std::string(argv[1]) == "prompt") return prompt(argc, argv);
     } catch (const fm::Error &e) {
         std::fprintf(stderr, "engine_check: %s: %s\n", fm::error_name(e.code), e.what());
         return 1;
     }
-    std::fprintf(stderr, "usage: engine_check compare|twin ...\n");
+    std::fprintf(stderr, "usage: engine_check compare|twin|residency|prompt ...\n");
     return 2;
 }

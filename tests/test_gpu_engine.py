@@ -6,6 +6,13 @@ the adapter, FreeMoe's sources and libfmx.so).
     freemoe_reference: moe-fm.gguf, 20 prompts with their logits, greedy ids and
     routing records, copied as data): every prompt within the reference's 5e-3,
     every greedy id and every routing event equal;
+  * compare_reference on FreeMoe's dense fixture (dense-fm.gguf, 20 prompts):
+    its prompts take the engine's batched prefill, whose projections are
+    gemm_quant calls, so on HipBackend they run fmx_gemm_quant;
+  * FreeMoe's block-type conformance checkpoints (quant-moe-*.gguf, every
+    matrix including the router in one block type; the run of tests.cpp:
+    1424-1468) on the CPU backend and on HipBackend in one process, the
+    quantised projections on the device: logits bit for bit, ids equal;
   * the freemoe-tiny-v1 end-to-end model (2 layers, hidden 64, 4 experts top-2,
     ffn 128, F32 ~N(0, 0.02)), 64-token seeded byte prompts and 32 greedy
     tokens, on the CPU backend and on HipBackend in one process: prompt logits
@@ -52,6 +59,42 @@ def test_unchanged_engine_compare_reference_on_hip_backend(gpu):
     assert r["backend"] == "hip-gfx950"
     check_compare(r, 20)
     assert r["ops"].get("hip-gfx950", 0) > 0  # the projections ran on the device
+
+
+def test_unchanged_engine_dense_compare_reference_cpu():
+    """The dense fixture's goldens on FreeMoe's CPU backend (batched prefill)."""
+    r = run("compare", FIXTURES / "dense-fm.gguf", FIXTURES, 20, 16, "cpu")
+    check_compare(r, 20)
+    assert r["ops"].get("cpu-batched", 0) > 0
+
+
+@pytest.mark.gpu
+def test_unchanged_engine_dense_compare_reference_on_hip_backend(gpu):
+    """The dense fixture's goldens on HipBackend: the batched prefill's
+    projections run fmx_gemm_quant, decode runs fmx_matvec."""
+    r = run("compare", FIXTURES / "dense-fm.gguf", FIXTURES, 20, 16, "gpu")
+    print(r)
+    assert r["backend"] == "hip-gfx950"
+    check_compare(r, 20)
+    assert r["ops"].get("hip-gfx950", 0) > 0
+    assert r["ops"]["hooked"].get("gemm_quant", 0) > 0  # the batched projections ran on the device
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("variant", ["q8_0", "q4_0", "q4_k"])
+def test_quantised_checkpoint_conformance_on_hip_backend(gpu, variant):
+    """FreeMoe's quant-moe-<type> checkpoint (router, attention and experts
+    in the block type) through the unchanged engine: HipBackend runs every
+    quantised projection, and its prompt logits and greedy ids equal the CPU
+    backend's bit for bit (the reference's own test holds the CPU run to the
+    F32 twin within 1e-4)."""
+    r = run("prompt", FIXTURES / f"quant-moe-{variant}.gguf", 6, "quantised conformance")
+    print(r)
+    assert r["backends"] == ["cpu", "hip-gfx950"]
+    assert r["logits"] > 0 and r["differing_logits"] == 0 and r["max_abs_diff"] == 0.0
+    assert r["ids_identical"] and r["routing_identical"] and r["generated"] == 6
+    assert r["gpu_ops"].get("hip-gfx950", 0) > 0
+    assert r["gpu_ops"]["hooked"].get("gemv_quant", 0) > 0  # the quantised projections ran on the device
 
 
 @pytest.mark.gpu

@@ -95,3 +95,42 @@ def test_matvec_bitwise_vs_oracle(gpu, t, rows, cols):
     want = fo.gemv(t, raw, x, rows, cols, fo.ISA_AVX2)
     got = y.cpu().numpy()
     assert np.array_equal(bits(got), bits(want)), f"max diff {np.abs(got - want).max()}"
+
+
+GEMM_CASES = [(0, 7, 13, 33), (0, 25, 40, 5), (0, 1031, 17, 70), (2, 32, 1, 1), (2, 4096, 40, 33),
+              (8, 96, 300, 100), (8, 2304, 16, 32), (12, 256, 13, 9), (12, 2048, 33, 65)]
+
+
+@pytest.mark.parametrize("t,in_dim,out_dim,tokens", GEMM_CASES)
+def test_gemm_quant_bitwise(gpu, t, in_dim, out_dim, tokens):
+    """The batched product (gemm_quant) bit for bit against the oracle and,
+    where it is built, the reference's own gemm_quant: F32 rows with 8-wide
+    and scalar tails, every block type, token counts around the 32-token
+    tile, rows around the 16-row tile."""
+    import torch
+    rng = np.random.default_rng(in_dim * 31 + out_dim + t)
+    w = wl.matrix(t, rng, out_dim, in_dim, sigma=0.03, f32_sigma=0.3)
+    x = rng.standard_normal((tokens, in_dim), dtype=np.float32) * np.float32(3.0)
+    y = torch.full((tokens, out_dim), float("nan"), dtype=torch.float32, device=gpu)
+    wd, xd = dev(w, gpu), dev(x, gpu)  # held: a temporary's memory would be reused by the next
+    fmx.call("fmx_gemm_quant", t, wd.data_ptr(), xd.data_ptr(), y.data_ptr(), tokens, out_dim, in_dim,
+             fmx.stream_handle())
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert same_floats(got, fo.gemm(t, w, x, out_dim, in_dim))
+    if fo.REF_PATH.exists():
+        assert same_floats(got, fo.ref_gemm(t, w, x, out_dim, in_dim))
+
+
+def test_gemm_quant_errors(gpu):
+    """The reference's argument checks: a zero dimension is a no-op, a row that
+    is not whole blocks is SHAPE_MISMATCH, an unknown type UNSUPPORTED."""
+    import torch
+    lib = fmx.lib()
+    x = torch.zeros(64, dtype=torch.float32, device=gpu)
+    y = torch.zeros(64, dtype=torch.float32, device=gpu)
+    w = torch.zeros(4096, dtype=torch.uint8, device=gpu)
+    assert lib.fmx_gemm_quant(8, w.data_ptr(), x.data_ptr(), y.data_ptr(), 0, 4, 32, None) == 0
+    assert lib.fmx_gemm_quant(8, w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, 4, 48, None) == 3
+    assert lib.fmx_gemm_quant(77, w.data_ptr(), x.data_ptr(), y.data_ptr(), 1, 4, 32, None) == 2
+    assert lib.fmx_gemm_quant(8, None, x.data_ptr(), y.data_ptr(), 1, 4, 32, None) == 1

@@ -65,6 +65,25 @@ def test_gemv_bitwise_vs_live_reference(ref_lib, type_id, isa):
                 assert np.array_equal(bits(got), bits(want)), (in_dim, out_dim, threads)
 
 
+@pytest.mark.parametrize("type_id", [0, 2, 8, 12])
+@pytest.mark.parametrize("isa", [fo.ISA_SCALAR, fo.ISA_AVX2])
+def test_gemm_bitwise_vs_live_reference(ref_lib, type_id, isa):
+    """gemm_quant (the batched product): the oracle's dequantise-then-dot
+    against the reference's own gemm_quant, bit for bit, over F32 tails, block
+    multiples and token counts around the 32-token tile."""
+    rng = np.random.default_rng(100 + type_id * 7 + isa)
+    bs = fo.GEOMETRY[type_id][0]
+    dims = [7, 24, 25, 300, 1031] if type_id == 0 else sorted({bs, bs * 3, bs * 9, 2304})
+    for in_dim in dims:
+        for out_dim, tokens in ((1, 1), (13, 33), (40, 5)):
+            w = wl.matrix(type_id, rng, out_dim, in_dim, sigma=0.03, f32_sigma=0.3)
+            x = rng.standard_normal((tokens, in_dim), dtype=np.float32) * np.float32(3.0)
+            got = fo.gemm(type_id, w, x, out_dim, in_dim, isa)
+            for threads in (1, 2):
+                want = fo.ref_gemm(type_id, w, x, out_dim, in_dim, isa, threads)
+                assert np.array_equal(bits(got), bits(want)), (in_dim, out_dim, tokens, threads)
+
+
 def test_f32_tails_bitwise_vs_live_reference(ref_lib):
     rng = np.random.default_rng(3)
     for n in [1, 7, 8, 9, 15, 16, 17, 23, 24, 25, 31, 33, 4103]:
