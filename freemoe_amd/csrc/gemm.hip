@@ -63,6 +63,21 @@ __device__ inline void dequant_segment(uint32_t type_id, const uint8_t *blk, uin
         for (int j = 0; j < 16; ++j) o[j] = d1 * static_cast<float>(hi ? qs[j] >> 4 : qs[j] & 0x0Fu) - m1;
         break;
     }
+    case FMX_TYPE_Q6_K: {
+        // segment s: half n = s / 8, quarter qt = (s / 2) % 4 of the half,
+        // l = 16 (s % 2) + j; sub-block scale 8 n + s % 2 + 2 qt
+        const float d = half_bits_to_float(blk[208] | (blk[209] << 8));
+        const uint32_t n = s >> 3, qt = (s >> 1) & 3, l0 = 16 * (s & 1);
+        const float sc = static_cast<float>(static_cast<int8_t>(blk[192 + 8 * n + (s & 1) + 2 * qt]));
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t l = l0 + j;
+            const uint32_t ql = blk[64 * n + l + 32 * (qt & 1)], qh = blk[128 + 32 * n + l];
+            const int q = static_cast<int>((qt >= 2 ? ql >> 4 : ql & 0x0Fu) | (((qh >> (2 * qt)) & 3u) << 4)) - 32;
+            o[j] = d * sc * static_cast<float>(q);
+        }
+        break;
+    }
     default:
         break;
     }

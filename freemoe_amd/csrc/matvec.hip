@@ -1,6 +1,10 @@
 // matvec.hip — y = W x for one matrix (Backend::matvec / gemv_quant).
 //
-// Block-type rows use the lane chains of chains.hpp; F32 rows use the
+// Block-type rows use the lane chains of chains.hpp (Q4_0, Q8_0, Q4_K: the
+// reference's dedicated AVX2 row dots); Q6_K rows, which the reference runs
+// through row_dot_fused_scalar (kernels.cpp:574-590: each block decoded,
+// dotted by dot_avx2, the block's dot added to the row total), use that order
+// on 16 lanes per row; F32 rows use the
 // reference's gemv_avx2_row order (kernels.cpp:147-167): per row 16 chains
 // (chain c takes k = c mod 16; chains 0..7 are acc0, 8..15 acc1), an 8-element
 // tail into acc0, lane-wise acc0 + acc1, the 8-lane tree sum, then a scalar
@@ -63,6 +67,41 @@ __global__ __launch_bounds__(kThreads) void matvec_f32_kernel(const float *__res
     if (c == 0 && r < rows) y[r] = total;
 }
 
+// Q6_K: 16 lanes per row over raw blocks. For block b, lane c runs chain
+// k = c mod 16 of dot_avx2 over the block's 256 decoded values (elements
+// 16 m + c), the 16 chains meet as in f32_row_chains, and the block's dot is
+// added to the row total in block order.
+__device__ inline float q6_k_value(const uint8_t *blk, uint32_t e) {
+    const uint32_t n = e >> 7, r = e & 127, l = r & 31, qt = r >> 5; // half, quarter of the half
+    const uint32_t ql = blk[64 * n + l + 32 * (qt & 1)];
+    const uint32_t qh = blk[128 + 32 * n + l];
+    const int q = static_cast<int>(((qt >= 2 ? ql >> 4 : ql & 0x0Fu)) | (((qh >> (2 * qt)) & 3u) << 4)) - 32;
+    const float d = half_bits_to_float(blk[208] | (blk[209] << 8));
+    const float sc = static_cast<float>(static_cast<int8_t>(blk[192 + 8 * n + l / 16 + 2 * qt]));
+    return d * sc * static_cast<float>(q);
+}
+
+__global__ __launch_bounds__(kThreads) void matvec_q6_k_kernel(const uint8_t *__restrict__ w,
+                                                               const float *__restrict__ x,
+                                                               float *__restrict__ y, uint32_t rows,
+                                                               uint32_t blocks) {
+    const uint32_t tid = threadIdx.x, c = tid & 15;
+    const uint32_t r = blockIdx.x * (kThreads / 16) + (tid >> 4);
+    const uint32_t rr = r < rows ? r : rows - 1;
+    const uint8_t *row = w + static_cast<uint64_t>(rr) * blocks * 210;
+    float total = 0.0f;
+    for (uint32_t b = 0; b < blocks; ++b) {
+        const uint8_t *blk = row + static_cast<uint64_t>(b) * 210;
+        const float *xb = x + static_cast<uint64_t>(b) * 256;
+        float acc = 0.0f;
+#pragma unroll 4
+        for (uint32_t m = 0; m < 16; ++m) acc = fma_rn(q6_k_value(blk, 16 * m + c), xb[16 * m + c], acc);
+        const float t = acc + lane_xor(acc, 8);
+        total = total + hsum8_lanes(t);
+    }
+    if (c == 0 && r < rows) y[r] = total;
+}
+
 template <class T, int NR>
 int launch_matvec(const PackedGeometry &g, const void *packed, const float *x, float *y,
                   hipStream_t s) {
@@ -101,6 +140,11 @@ extern "C" int fmx_matvec(uint32_t type_id, const void *packed, const float *x, 
     case FMX_TYPE_Q4_0: return launch_matvec<Q40, 2>(g, packed, x, y, s);
     case FMX_TYPE_Q8_0: return launch_matvec<Q80, 2>(g, packed, x, y, s);
     case FMX_TYPE_Q4_K: return launch_matvec<Q4K, 1>(g, packed, x, y, s);
+    case FMX_TYPE_Q6_K:
+        hipLaunchKernelGGL(matvec_q6_k_kernel, dim3(div_up(out_dim, kThreads / 16)), dim3(kThreads), 0, s,
+                           static_cast<const uint8_t *>(packed), x, y, out_dim, g.blocks);
+        FMX_LAUNCH_CHECK();
+        return FMX_OK;
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }

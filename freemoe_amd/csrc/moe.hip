@@ -1097,6 +1097,12 @@ int prepare_expert_args(const fmx_moe_layer *L, const RouteArgs &route, ExpertAr
     e.up = L->up;
     e.down = L->down;
     if (L->up_type != L->gate_type) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    // the fused expert kernels: F32, Q4_0, Q8_0, Q4_K (Q6_K matrices run
+    // through fmx_matvec / fmx_gemm_quant only)
+    auto fused = [](uint32_t t) {
+        return t == FMX_TYPE_F32 || t == FMX_TYPE_Q4_0 || t == FMX_TYPE_Q8_0 || t == FMX_TYPE_Q4_K;
+    };
+    if (!fused(L->gate_type) || !fused(L->down_type)) return FMX_ERR_UNSUPPORTED_QUANTISATION;
     if (int rc = packed_geometry(L->gate_type, L->ffn, L->hidden, &e.gu)) return rc;
     if (int rc = packed_geometry(L->down_type, L->hidden, L->ffn, &e.dn)) return rc;
     // LDS tiles (blocks): gate/up stages one tile of h, down one tile of every

@@ -1,10 +1,10 @@
 // quant.hip — block geometry, dequantisation and the packed device layout.
 //
-// Dequantisation follows dequantize_block (quant.cpp:163-318) for F32, Q4_0,
-// Q8_0 and Q4_K. Every product there is exact in float (Q4_0/Q8_0: an 11-bit
-// half times a small integer; Q4_K: d*sc <= 17 bits times a nibble), so the
-// only rounding is Q4_K's final subtraction and the decoded values are the
-// reference's bit for bit.
+// Dequantisation follows dequantize_block (quant.cpp:163-371) for F32, Q4_0,
+// Q8_0, Q4_K and Q6_K. Every product there is exact in float (Q4_0/Q8_0: an
+// 11-bit half times a small integer; Q4_K: d*sc <= 17 bits times a nibble;
+// Q6_K: d*sc <= 18 bits times |q| <= 32), so the only rounding is Q4_K's final
+// subtraction and the decoded values are the reference's bit for bit.
 #include "fmx_internal.hpp"
 
 namespace fmx {
@@ -16,6 +16,7 @@ int raw_geometry(uint32_t type_id, uint32_t *block_size, uint32_t *block_bytes) 
     case FMX_TYPE_Q4_0: bs = 32; bb = 18; break;
     case FMX_TYPE_Q8_0: bs = 32; bb = 34; break;
     case FMX_TYPE_Q4_K: bs = 256; bb = 144; break;
+    case FMX_TYPE_Q6_K: bs = 256; bb = 210; break;
     default: return FMX_ERR_UNSUPPORTED_QUANTISATION;
     }
     if (block_size) *block_size = bs;
@@ -32,6 +33,7 @@ int raw_geometry(uint32_t type_id, uint32_t *block_size, uint32_t *block_bytes) 
 //   Q4_K  A: [rows][S][16 B] header (d, dmin, 12 B scales) B: [rows][S][lane][16 B]
 //         lane l's bytes 4g+k = qs[32g + 8k + l] (group g, k = 0..3).
 //   F32   raw row-major, no packing.
+//   Q6_K  raw rows (its matvec and batched product read the GGUF blocks).
 // Block-type layouts end with kPackedTail spare bytes: the decode streams
 // request up to 8 chunks (1 KiB) past a row's last chunk before they know the
 // row has ended, and the last row's requests must stay inside the allocation.
@@ -72,6 +74,12 @@ int packed_geometry(uint32_t type_id, uint32_t rows, uint32_t cols, PackedGeomet
         p.scale_bytes = align_up(p.scale_row_bytes * rows, 256);
         p.quant_bytes = static_cast<uint64_t>(rows) * p.chunks * 128;
         p.total = p.scale_bytes + align_up(p.quant_bytes, 256) + kPackedTail;
+        break;
+    case FMX_TYPE_Q6_K:
+        p.blocks_padded = p.blocks;
+        p.chunks = p.blocks;
+        p.quant_bytes = static_cast<uint64_t>(rows) * p.blocks * bb;
+        p.total = p.quant_bytes;
         break;
     }
     *g = p;
@@ -161,6 +169,30 @@ __global__ void pack_q4_k_kernel(const uint8_t *__restrict__ raw, uint8_t *__res
     }
 }
 
+// Q6_K (quant.cpp:347-371): two halves of 128 elements; in a half, l < 32
+// gives elements l, l+32, l+64, l+96 from the low / high nibbles of ql[l] and
+// ql[l+32] and the four bit pairs of qh[l], with sub-block scales
+// sc[l/16 + 0, 2, 4, 6]; value (d * sc) * (q - 32).
+__device__ inline void q6_k_block(const uint8_t *blk, float *o) {
+    const float d = half_bits_to_float(blk[208] | (blk[209] << 8));
+    for (int n = 0; n < 2; ++n) {
+        const uint8_t *ql = blk + 64 * n, *qh = blk + 128 + 32 * n;
+        const int8_t *sc = reinterpret_cast<const int8_t *>(blk + 192 + 8 * n);
+        float *y = o + 128 * n;
+        for (int l = 0; l < 32; ++l) {
+            const int is = l / 16;
+            const int q1 = static_cast<int>((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+            const int q2 = static_cast<int>((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+            const int q3 = static_cast<int>((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+            const int q4 = static_cast<int>((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+            y[l] = d * static_cast<float>(sc[is]) * static_cast<float>(q1);
+            y[l + 32] = d * static_cast<float>(sc[is + 2]) * static_cast<float>(q2);
+            y[l + 64] = d * static_cast<float>(sc[is + 4]) * static_cast<float>(q3);
+            y[l + 96] = d * static_cast<float>(sc[is + 6]) * static_cast<float>(q4);
+        }
+    }
+}
+
 // One thread per block (dequantize_block).
 __global__ void dequant_kernel(uint32_t type_id, const uint8_t *__restrict__ raw,
                                float *__restrict__ dst, uint64_t blocks) {
@@ -208,6 +240,9 @@ __global__ void dequant_kernel(uint32_t type_id, const uint8_t *__restrict__ raw
         }
         break;
     }
+    case FMX_TYPE_Q6_K:
+        q6_k_block(raw + b * 210, dst + b * 256);
+        break;
     default:
         break;
     }
@@ -240,6 +275,7 @@ extern "C" int fmx_pack(uint32_t type_id, const void *raw, void *packed, uint32_
     const uint32_t threads = 256;
     switch (type_id) {
     case FMX_TYPE_F32:
+    case FMX_TYPE_Q6_K:
         FMX_HIP_TRY(hipMemcpyAsync(dst, src, g.total, hipMemcpyDeviceToDevice, s));
         return FMX_OK;
     case FMX_TYPE_Q4_0: {

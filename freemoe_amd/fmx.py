@@ -15,9 +15,9 @@ from pathlib import Path
 # the CPU tests); by default the in-tree libfmx.so.
 LIB_PATH = Path(os.environ.get("FMX_LIBRARY") or Path(__file__).resolve().parent / "libfmx.so")
 
-FMX_TYPE_F32, FMX_TYPE_Q4_0, FMX_TYPE_Q8_0, FMX_TYPE_Q4_K = 0, 2, 8, 12
+FMX_TYPE_F32, FMX_TYPE_Q4_0, FMX_TYPE_Q8_0, FMX_TYPE_Q4_K, FMX_TYPE_Q6_K = 0, 2, 8, 12, 14
 BLOCK_GEOMETRY = {FMX_TYPE_F32: (1, 4), FMX_TYPE_Q4_0: (32, 18), FMX_TYPE_Q8_0: (32, 34),
-                  FMX_TYPE_Q4_K: (256, 144)}
+                  FMX_TYPE_Q4_K: (256, 144), FMX_TYPE_Q6_K: (256, 210)}
 FAULT_NONE, FAULT_TRANSFER, FAULT_FENCE_DEFERRED, FAULT_FENCE_TIMEOUT, FAULT_DEVICE_LOSS = range(5)
 
 STATUS_NAMES = {0: "OK", 1: "INVALID_ARGUMENT", 2: "UNSUPPORTED_QUANTISATION", 3: "SHAPE_MISMATCH",

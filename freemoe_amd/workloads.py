@@ -21,9 +21,9 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
-F32, Q4_0, Q8_0, Q4_K = 0, 2, 8, 12
-GEOMETRY = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144)}
-TYPE_NAMES = {F32: "f32", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k"}
+F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
+GEOMETRY = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+TYPE_NAMES = {F32: "f32", Q4_0: "q4_0", Q8_0: "q8_0", Q4_K: "q4_k", Q6_K: "q6_k"}
 
 
 def row_bytes(type_id: int, cols: int) -> int:
@@ -49,6 +49,10 @@ def matrix(type_id: int, rng: np.random.Generator, rows: int, cols: int, sigma: 
         w[:, 2:] = rng.integers(-127, 128, size=(nb, 32), dtype=np.int8).view(np.uint8)
     else:
         w = np.frombuffer(rng.bytes(nb * bb), np.uint8).reshape(nb, bb).copy()
+    if type_id == Q6_K:
+        # ql, qh and the 16 int8 sub-block scales uniform; f16 d last
+        w[:, 208:210] = _half_scales(rng, nb, sigma)
+        return w.reshape(rows, -1)
     w[:, 0:2] = _half_scales(rng, nb, sigma)
     if type_id == Q4_K:
         w[:, 2:4] = _half_scales(rng, nb, sigma)

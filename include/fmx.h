@@ -54,7 +54,7 @@ typedef enum fmx_status {
 } fmx_status;
 
 /* Tensor type ids (GGUF, gguf.cpp:58-106) this library executes. */
-enum { FMX_TYPE_F32 = 0, FMX_TYPE_Q4_0 = 2, FMX_TYPE_Q8_0 = 8, FMX_TYPE_Q4_K = 12 };
+enum { FMX_TYPE_F32 = 0, FMX_TYPE_Q4_0 = 2, FMX_TYPE_Q8_0 = 8, FMX_TYPE_Q4_K = 12, FMX_TYPE_Q6_K = 14 };
 
 /* Faults forced from the host, as fm::BackendFault (include/fm/backend.hpp:118). */
 enum { FMX_FAULT_NONE = 0, FMX_FAULT_TRANSFER = 1, FMX_FAULT_FENCE_DEFERRED = 2,

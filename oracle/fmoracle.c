@@ -53,7 +53,7 @@ static uint16_t rd16(const uint8_t *p) {
     return v;
 }
 
-/* Block geometry for the four types on this path (gguf.cpp:58-106). */
+/* Block geometry for the types on this path (gguf.cpp:58-106). */
 int fmo_quant_geometry(uint32_t type_id, uint32_t *block_size, uint32_t *block_bytes) {
     uint32_t bs, bb;
     switch (type_id) {
@@ -61,6 +61,7 @@ int fmo_quant_geometry(uint32_t type_id, uint32_t *block_size, uint32_t *block_b
     case FMO_TYPE_Q4_0: bs = 32; bb = 18; break;
     case FMO_TYPE_Q8_0: bs = 32; bb = 34; break;
     case FMO_TYPE_Q4_K: bs = 256; bb = 144; break;
+    case FMO_TYPE_Q6_K: bs = 256; bb = 210; break;
     default: return FMO_ERR_UNSUPPORTED_QUANTISATION;
     }
     if (block_size) *block_size = bs;
@@ -118,6 +119,36 @@ int fmo_dequantize_block(uint32_t type_id, const uint8_t *src, float *dst) {
             for (int l = 0; l < 32; ++l) dst[64 * g + l] = d1 * (float)(qs[l] & 0x0F) - m1;
             for (int l = 0; l < 32; ++l) dst[64 * g + 32 + l] = d2 * (float)(qs[l] >> 4) - m2;
             qs += 32;
+        }
+        return FMO_OK;
+    }
+    case FMO_TYPE_Q6_K: {
+        /* quant.cpp:347-371: 128 B low nibbles ql, 64 B high 2-bit pairs qh,
+         * 16 int8 sub-block scales, f16 d. Two halves of 128 elements; in a
+         * half, l < 32 gives elements l, l+32, l+64, l+96 from ql[l] / ql[l+32]
+         * (low and high nibbles) and the four bit pairs of qh[l]; sub-block
+         * scale is = l / 16 (+0, +2, +4, +6); value d * sc * (q - 32),
+         * evaluated (d * sc) * q as the reference's left-to-right product. */
+        const uint8_t *ql = src, *qh = src + 128;
+        const int8_t *sc = (const int8_t *)(src + 192);
+        const float d = fmo_fp16_to_f32(rd16(src + 208));
+        float *y = dst;
+        for (int n = 0; n < 256; n += 128) {
+            for (int l = 0; l < 32; ++l) {
+                const int is = l / 16;
+                const int q1 = (int)((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int q2 = (int)((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[l] = d * (float)sc[is] * (float)q1;
+                y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+            }
+            y += 128;
+            ql += 64;
+            qh += 32;
+            sc += 8;
         }
         return FMO_OK;
     }
@@ -277,6 +308,22 @@ static float dot_fused_scalar(uint32_t type_id, const uint8_t *row, const float 
     return total;
 }
 
+/* row_dot_fused_scalar with the AVX2 ISA (kernels.cpp:574-590, selected by
+ * select_row_dot for the block types without a dedicated kernel, e.g. Q6_K):
+ * each block decoded, dotted by dot_avx2 (kernels.cpp:206-223), and the
+ * block's dot added to the running total (a plain add: that function is
+ * compiled without FMA). */
+static float dot_fused_avx2(uint32_t type_id, const uint8_t *row, const float *x, uint32_t n) {
+    uint32_t bs, bb;
+    fmo_quant_geometry(type_id, &bs, &bb);
+    float total = 0.0f, dec[256];
+    for (uint32_t b = 0; b < n / bs; ++b) {
+        fmo_dequantize_block(type_id, row + (uint64_t)b * bb, dec);
+        total += dot_f32_avx2(dec, x + (uint64_t)b * bs, bs);
+    }
+    return total;
+}
+
 /* gemv (kernels.cpp:470-508) for F32 and gemv_quant (kernels.cpp:846-878)
  * for the block types. Threading splits rows only, so it never changes bits. */
 int fmo_gemv(int isa, uint32_t type_id, const uint8_t *weights, const float *x, float *y,
@@ -299,7 +346,8 @@ int fmo_gemv(int isa, uint32_t type_id, const uint8_t *weights, const float *x, 
             case FMO_TYPE_F32: v = dot_f32_avx2((const float *)row, x, in_dim); break;
             case FMO_TYPE_Q4_0: v = dot_q4_0_avx2(row, x, in_dim); break;
             case FMO_TYPE_Q8_0: v = dot_q8_0_avx2(row, x, in_dim); break;
-            default: v = dot_q4_k_avx2(row, x, in_dim); break;
+            case FMO_TYPE_Q4_K: v = dot_q4_k_avx2(row, x, in_dim); break;
+            default: v = dot_fused_avx2(type_id, row, x, in_dim); break;
             }
         }
         y[o] = v;

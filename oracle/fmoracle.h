@@ -50,7 +50,7 @@ enum {
 enum { FMO_ISA_SCALAR = 0, FMO_ISA_AVX2 = 1 };
 
 /* GGUF tensor type ids handled on this path (gguf.cpp:58-106). */
-enum { FMO_TYPE_F32 = 0, FMO_TYPE_Q4_0 = 2, FMO_TYPE_Q8_0 = 8, FMO_TYPE_Q4_K = 12 };
+enum { FMO_TYPE_F32 = 0, FMO_TYPE_Q4_0 = 2, FMO_TYPE_Q8_0 = 8, FMO_TYPE_Q4_K = 12, FMO_TYPE_Q6_K = 14 };
 
 float fmo_fp16_to_f32(uint16_t h);
 int fmo_quant_geometry(uint32_t type_id, uint32_t *block_size, uint32_t *block_bytes);

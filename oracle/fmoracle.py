@@ -18,8 +18,9 @@ ORACLE_PATH = Path(os.environ.get("FMORACLE_LIBRARY") or HERE / "libfmoracle.so"
 REF_PATH = HERE / "_ref" / "libfmref.so"
 
 ISA_SCALAR, ISA_AVX2 = 0, 1
-TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K = 0, 2, 8, 12
-GEOMETRY = {TYPE_F32: (1, 4), TYPE_Q4_0: (32, 18), TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144)}
+TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 2, 8, 12, 14
+GEOMETRY = {TYPE_F32: (1, 4), TYPE_Q4_0: (32, 18), TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144),
+            TYPE_Q6_K: (256, 210)}
 
 
 class OracleError(RuntimeError):

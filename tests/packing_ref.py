@@ -5,7 +5,7 @@ is a pure permutation of the raw GGUF bytes (unpack(pack(raw)) == raw).
 """
 import numpy as np
 
-Q4_0, Q8_0, Q4_K, F32 = 2, 8, 12, 0
+Q4_0, Q8_0, Q4_K, F32, Q6_K = 2, 8, 12, 0, 14
 # zero bytes after a block-type layout (room for the decode streams' prefetch)
 PACKED_TAIL = 4096
 
@@ -16,7 +16,7 @@ def _align(v, a=256):
 
 def pack(type_id: int, raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
     raw = np.ascontiguousarray(raw, np.uint8).reshape(rows, -1)
-    if type_id == F32:
+    if type_id in (F32, Q6_K):  # raw rows
         return raw.reshape(-1).copy()
     if type_id in (Q4_0, Q8_0):
         bb, per = (18, 8) if type_id == Q4_0 else (34, 4)
@@ -57,7 +57,7 @@ def pack(type_id: int, raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
 
 
 def unpack(type_id: int, packed: np.ndarray, rows: int, cols: int) -> np.ndarray:
-    if type_id == F32:
+    if type_id in (F32, Q6_K):
         return packed.reshape(rows, -1).copy()
     if type_id in (Q4_0, Q8_0):
         bb, per = (18, 8) if type_id == Q4_0 else (34, 4)

@@ -81,14 +81,18 @@ def test_unchanged_engine_dense_compare_reference_on_hip_backend(gpu):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("variant", ["q8_0", "q4_0", "q4_k"])
+@pytest.mark.parametrize("variant", ["quant-moe-q8_0", "quant-moe-q4_0", "quant-moe-q4_k", "quant-moe-q6_k",
+                                     "quant-expert-fused", "quant-expert-separate"])
 def test_quantised_checkpoint_conformance_on_hip_backend(gpu, variant):
-    """FreeMoe's quant-moe-<type> checkpoint (router, attention and experts
-    in the block type) through the unchanged engine: HipBackend runs every
-    quantised projection, and its prompt logits and greedy ids equal the CPU
-    backend's bit for bit (the reference's own test holds the CPU run to the
-    F32 twin within 1e-4)."""
-    r = run("prompt", FIXTURES / f"quant-moe-{variant}.gguf", 6, "quantised conformance")
+    """FreeMoe's block-type checkpoints through the unchanged engine:
+    quant-moe-<type> (router, attention and experts in one block type) and
+    quant-expert-{fused,separate} (Q4_K gate/up with Q6_K down experts, the
+    mixed-type case of tests.cpp:1479-1544). HipBackend runs every quantised
+    projection, and its prompt logits and greedy ids equal the CPU backend's
+    bit for bit (the reference's own tests hold the CPU run to the F32 twin
+    within 1e-4)."""
+    text = "mixed experts" if variant.startswith("quant-expert") else "quantised conformance"
+    r = run("prompt", FIXTURES / f"{variant}.gguf", 6, text)
     print(r)
     assert r["backends"] == ["cpu", "hip-gfx950"]
     assert r["logits"] > 0 and r["differing_logits"] == 0 and r["max_abs_diff"] == 0.0

@@ -28,7 +28,7 @@ def same_floats(got, want):
 
 
 @pytest.mark.parametrize("t,rows,cols", [(2, 5, 96), (2, 33, 4096), (2, 7, 14336), (8, 5, 160), (8, 9, 4096),
-                                         (12, 4, 768), (12, 17, 2048), (0, 3, 40)])
+                                         (12, 4, 768), (12, 17, 2048), (0, 3, 40), (14, 6, 512)])
 def test_pack_matches_layout(gpu, t, rows, cols):
     import torch
     raw = wl.matrix(t, np.random.default_rng(rows + cols), rows, cols)
@@ -38,7 +38,7 @@ def test_pack_matches_layout(gpu, t, rows, cols):
     assert np.array_equal(out.cpu().numpy(), packing_ref.pack(t, raw, rows, cols))
 
 
-@pytest.mark.parametrize("t", [0, 2, 8, 12])
+@pytest.mark.parametrize("t", [0, 2, 8, 12, 14])
 def test_dequant_bitwise(gpu, t):
     import torch
     bs, bb = wl.GEOMETRY[t]
@@ -77,6 +77,7 @@ MATVEC_CASES = [
     (2, 37, 512), (2, 11, 96), (2, 6, 4096), (2, 1000, 4096), (2, 513, 14336),
     (8, 37, 512), (8, 11, 96), (8, 6, 4096), (8, 1000, 4096), (8, 300, 14336),
     (12, 37, 512), (12, 6, 2048), (12, 768, 2048), (12, 2048, 768),
+    (14, 37, 256), (14, 9, 2048), (14, 300, 14336),
 ]
 
 
@@ -98,7 +99,8 @@ def test_matvec_bitwise_vs_oracle(gpu, t, rows, cols):
 
 
 GEMM_CASES = [(0, 7, 13, 33), (0, 25, 40, 5), (0, 1031, 17, 70), (2, 32, 1, 1), (2, 4096, 40, 33),
-              (8, 96, 300, 100), (8, 2304, 16, 32), (12, 256, 13, 9), (12, 2048, 33, 65)]
+              (8, 96, 300, 100), (8, 2304, 16, 32), (12, 256, 13, 9), (12, 2048, 33, 65), (14, 256, 17, 33),
+              (14, 1024, 40, 5)]
 
 
 @pytest.mark.parametrize("t,in_dim,out_dim,tokens", GEMM_CASES)

@@ -45,13 +45,13 @@ def test_fp16_all_encodings_match_ieee():
     assert np.array_equal(got[nan].view(np.uint32) | quiet, exp_bits | quiet)
 
 
-@pytest.mark.parametrize("type_id", [0, 2, 8, 12])
+@pytest.mark.parametrize("type_id", [0, 2, 8, 12, 14])
 def test_dequant_matches_reference_fixture(type_id):
     recs = [r for r in read_quant_reference() if r[0] == type_id]
     assert recs, f"fixture has a record for type {type_id}"
     for t, raw, exp in recs:
         got = fo.dequantize(t, raw, exp.size)
-        # 1e-6 relative is the reference test's bar; these four decode exactly
+        # 1e-6 relative is the reference test's bar; these types decode exactly
         assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
 
 

@@ -50,7 +50,7 @@ def test_layer_matches_reference_golden(layers, name):
 
 # ------------------------------------------------------- live, where built --
 
-@pytest.mark.parametrize("type_id", [0, 2, 8, 12])
+@pytest.mark.parametrize("type_id", [0, 2, 8, 12, 14])
 @pytest.mark.parametrize("isa", [fo.ISA_SCALAR, fo.ISA_AVX2])
 def test_gemv_bitwise_vs_live_reference(ref_lib, type_id, isa):
     rng = np.random.default_rng(type_id * 7 + isa)
@@ -65,7 +65,7 @@ def test_gemv_bitwise_vs_live_reference(ref_lib, type_id, isa):
                 assert np.array_equal(bits(got), bits(want)), (in_dim, out_dim, threads)
 
 
-@pytest.mark.parametrize("type_id", [0, 2, 8, 12])
+@pytest.mark.parametrize("type_id", [0, 2, 8, 12, 14])
 @pytest.mark.parametrize("isa", [fo.ISA_SCALAR, fo.ISA_AVX2])
 def test_gemm_bitwise_vs_live_reference(ref_lib, type_id, isa):
     """gemm_quant (the batched product): the oracle's dequantise-then-dot
@@ -98,14 +98,15 @@ def test_f32_tails_bitwise_vs_live_reference(ref_lib):
 def test_dequant_bitwise_vs_live_reference(ref_lib):
     import ctypes
     rng = np.random.default_rng(11)
-    for t in (2, 8, 12):
+    for t in (2, 8, 12, 14):
         bs, bb = fo.GEOMETRY[t]
         raw = wl.matrix(t, rng, 64, bs, sigma=0.5)
+        d = 208 if t == 14 else 0  # the f16 scale's offset (Q6_K stores it last)
         # subnormal, zero, negative and large scales
-        raw[0, 0:2] = [1, 0]
-        raw[1, 0:2] = [0, 0]
-        raw[2, 0:2] = np.frombuffer(np.float16(-2.5).tobytes(), np.uint8)
-        raw[3, 0:2] = np.frombuffer(np.float16(60000).tobytes(), np.uint8)
+        raw[0, d:d + 2] = [1, 0]
+        raw[1, d:d + 2] = [0, 0]
+        raw[2, d:d + 2] = np.frombuffer(np.float16(-2.5).tobytes(), np.uint8)
+        raw[3, d:d + 2] = np.frombuffer(np.float16(60000).tobytes(), np.uint8)
         got = fo.dequantize(t, raw, 64 * bs).reshape(64, bs)
         for r in range(64):
             want = np.empty(bs, np.float32)
