@@ -384,6 +384,16 @@ int fmo_gemm(int isa, uint32_t type_id, const uint8_t *weights, const float *x, 
     return rc;
 }
 
+/* FNV-1a 64 (the expert-slot checksum of residency.cpp:700-720 and the
+ * native adapter's expert checksums): h = (h xor byte) * prime mod 2^64,
+ * continued from h0 (the offset basis 14695981039346656037 for a new
+ * payload). */
+uint64_t fmo_fnv1a64(uint64_t h0, const uint8_t *data, uint64_t n) {
+    uint64_t h = h0;
+    for (uint64_t i = 0; i < n; ++i) h = (h ^ data[i]) * 1099511628211ull;
+    return h;
+}
+
 /* ------------------------------------------------------------------------ */
 /* Layer pieces                                                              */
 /* ------------------------------------------------------------------------ */

@@ -61,6 +61,9 @@ int fmo_dequantize_region(uint32_t type_id, const uint8_t *src, float *dst, uint
 int fmo_gemv(int isa, uint32_t type_id, const uint8_t *weights, const float *x, float *y,
              uint32_t out_dim, uint32_t in_dim);
 
+/* FNV-1a 64 of n bytes, continued from h0. */
+uint64_t fmo_fnv1a64(uint64_t h0, const uint8_t *data, uint64_t n);
+
 /* y[tokens x out_dim] = x[tokens x in_dim] * W^T (gemm_quant: each row
  * dequantised, then dot_isa per token). */
 int fmo_gemm(int isa, uint32_t type_id, const uint8_t *weights, const float *x, float *y, uint32_t tokens,

@@ -59,6 +59,8 @@ def oracle() -> ctypes.CDLL:
         lib.fmo_dequantize_region.argtypes = [c_uint32, c_void_p, c_void_p, c_uint64]
         lib.fmo_gemv.argtypes = [c_int, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]
         lib.fmo_gemm.argtypes = [c_int, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_uint32]
+        lib.fmo_fnv1a64.restype = c_uint64
+        lib.fmo_fnv1a64.argtypes = [c_uint64, c_void_p, c_uint64]
         lib.fmo_rmsnorm.argtypes = [c_void_p, c_void_p, c_uint32, c_double, c_double, c_void_p]
         lib.fmo_softmax.argtypes = [c_void_p, c_uint32, c_void_p]
         lib.fmo_topk.argtypes = [c_void_p, c_uint32, c_uint32, c_void_p]
@@ -201,6 +203,15 @@ def ref_gemv(type_id: int, w: np.ndarray, x: np.ndarray, out_dim: int, in_dim: i
     x = np.ascontiguousarray(x, dtype=np.float32)
     check(ref().fmr_gemv(isa, threads, type_id, _p(w), _p(x), _p(y), out_dim, in_dim), "fmr_gemv")
     return y
+
+
+def fnv1a64(*parts) -> int:
+    """FNV-1a 64 over the concatenated bytes of `parts` (arrays or bytes)."""
+    h = 14695981039346656037
+    for p in parts:
+        a = np.ascontiguousarray(np.frombuffer(p, np.uint8) if isinstance(p, (bytes, bytearray)) else p)
+        h = oracle().fmo_fnv1a64(h, _p(a.view(np.uint8)), a.nbytes)
+    return h
 
 
 def gemm(type_id: int, w: np.ndarray, x: np.ndarray, out_dim: int, in_dim: int, isa: int = ISA_AVX2) -> np.ndarray:

@@ -20,7 +20,7 @@
 //       host payload -> upload into the slot's pinned mirror and HBM twin ->
 //       fence -> FNV-1a read-back, residency.cpp:617-723); prints the
 //       comparison and residency's counters.
-//   engine_check twin <model.gguf> <prompts> <prompt_len> <generate> <seed>
+//   engine_check twin <model.gguf> <prompts> <prompt_len> <generate> <seed> [<hot GiB> <slots>]
 //       seeded random byte prompts through a CPU-backend engine and a
 //       GPU-backend engine; prints one JSON line with the largest prompt-logit
 //       difference, the number of logits that differ in any bit, and whether
@@ -44,11 +44,21 @@
 
 namespace {
 
+// Hot-memory budget and expert slots for models larger than the defaults
+// (64 MiB, as many slots as fit): set by the twin mode's optional arguments.
+uint64_t g_hot_bytes = 0;
+uint32_t g_slots = 0;
+
 fm::RunConfig config_for(const std::string &model, bool gpu) {
     fm::RunConfig rc;
     rc.model_path = model;
     rc.backend.kind = gpu ? fm::BackendKind::PhysicalGPU : fm::BackendKind::ScalarCPU;
     rc.backend.kernel_isa = fm::KernelIsa::Auto;
+    // two kernel threads: FreeMoe's WorkerPool finishes a split into at most
+    // two ranges (kernels.cpp:414-459), which large projections would exceed
+    rc.backend.kernel_threads = 2;
+    if (g_hot_bytes) rc.budget.total_hot_bytes = g_hot_bytes;
+    if (g_slots) rc.cache_slots = g_slots;
     return rc;
 }
 
@@ -170,6 +180,10 @@ int twin_run(const std::string &model, std::vector<std::string> texts, uint32_t 
 
 int twin(int argc, char **argv) {
     if (argc < 7) return 2;
+    if (argc >= 9) {
+        g_hot_bytes = std::strtoull(argv[7], nullptr, 10) << 30;
+        g_slots = static_cast<uint32_t>(std::atoi(argv[8]));
+    }
     return twin_run(argv[2], {}, static_cast<uint32_t>(std::atoi(argv[3])), static_cast<uint32_t>(std::atoi(argv[4])),
                     static_cast<uint32_t>(std::atoi(argv[5])), std::strtoull(argv[6], nullptr, 10));
 }

@@ -124,3 +124,34 @@ def oracle_run_prompt(m: Model, prompt: bytes, generate: int):
         pos += 1
     return (np.array(input_ids, np.int32), prompt_logits, np.array(generated, np.int32),
             np.array(routing, np.uint32).reshape(-1, 2 + m.top_k))
+
+
+def write_decoder(path: Path, *, layers: int = 8, hidden: int = 4096, ffn: int = 14336, experts: int = 8,
+                  top_k: int = 2, heads: int = 32, expert_type: int = wl.Q4_0, seed: int = 5) -> int:
+    """A full-size seeded freemoe-tiny-v1 decoder (the 8-layer Mixtral-shaped
+    decoder: F32 attention and router ~N(0, 0.02), norm gains 1 + N(0, 0.02),
+    Q4_0 experts of the Mixtral layer's shape) written to `path`, with the
+    adapter's FNV-1a expert checksums; returns the file size. About 8.5 GB at
+    the default sizes; the tensors are generated in memory."""
+    rng = np.random.default_rng(seed)
+
+    def n(*shape):
+        return (rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02))
+
+    def gain():
+        return (1.0 + rng.standard_normal(hidden, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+
+    blocks, lay = [], []
+    for _ in range(layers):
+        gate = [wl.matrix(expert_type, rng, ffn, hidden) for _ in range(experts)]
+        up = [wl.matrix(expert_type, rng, ffn, hidden) for _ in range(experts)]
+        down = [wl.matrix(expert_type, rng, hidden, ffn) for _ in range(experts)]
+        b = gguf.MoEBlock(n(experts, hidden), wl.F32, gate, up, down, expert_type, expert_type)
+        blocks.append(b)
+        lay.append(dict(attn_norm=gain(), attn_q=n(hidden, hidden), attn_k=n(hidden, hidden),
+                        attn_v=n(hidden, hidden), attn_output=n(hidden, hidden), ffn_norm=gain(), moe=b))
+    sums = [fo.fnv1a64(b.gate[e], b.up[e], b.down[e]) for b in blocks for e in range(experts)]
+    vocab = dict(token_embd=n(VOCAB, hidden), output_norm=gain(), output=n(VOCAB, hidden))
+    g = gguf.freemoe_tiny(hidden=hidden, ffn=ffn, heads=heads, experts=experts, top_k=top_k, layers=lay,
+                          vocab_tensors=vocab, seed=seed, checksums=sums, name="fmx 8-layer decoder")
+    return g.write(path)

@@ -13,6 +13,8 @@ the adapter, FreeMoe's sources and libfmx.so).
     matrix including the router in one block type; the run of tests.cpp:
     1424-1468) on the CPU backend and on HipBackend in one process, the
     quantised projections on the device: logits bit for bit, ids equal;
+  * the 8-layer Mixtral-shaped decoder (hidden 4096, Q4_0 experts, F32
+    attention, written at test time): CPU and HipBackend engines bit for bit;
   * the freemoe-tiny-v1 end-to-end model (2 layers, hidden 64, 4 experts top-2,
     ffn 128, F32 ~N(0, 0.02)), 64-token seeded byte prompts and 32 greedy
     tokens, on the CPU backend and on HipBackend in one process: prompt logits
@@ -129,3 +131,40 @@ def test_residency_refills_slots_through_hip_backend(gpu):
     assert r["checksum_checks"] >= 2 * r["cache_misses"] and r["checksum_failures"] == 0
     assert r["transfer_failures"] == 0 and r["fence_timeouts"] == 0
     assert r["experts_executed"] == r["selected_experts"]
+
+
+@pytest.mark.gpu
+def test_eight_layer_decoder_cpu_and_hip_identical(gpu, tmp_path):
+    """The 8-layer Mixtral-shaped decoder (hidden 4096, ffn 14336, 8 experts
+    top-2, Q4_0 experts, F32 attention; about 8.5 GB) through the unchanged
+    engine on the CPU backend and on HipBackend in one process, every expert
+    resident: prompt logits bit for bit, routing records and greedy ids
+    identical. The attention projections run as fmx_matvec F32, the experts
+    and router as the engine's gemv_quant calls on the device."""
+    import shutil
+    import sys
+    import time
+
+    sys.path.insert(0, str(ROOT / "tests" / "golden"))
+    import engine_models as em
+
+    need = 12 << 30
+    base = next((d for d in (Path("/dev/shm"), tmp_path)
+                 if d.exists() and shutil.disk_usage(d).free > need), None)
+    if base is None:
+        pytest.skip("no 12 GiB of scratch space for the 8.5 GB checkpoint")
+    path = base / f"fmx-decoder-{id(tmp_path)}.gguf"
+    try:
+        t0 = time.time()
+        size = em.write_decoder(path)
+        print(f"[decoder] checkpoint {size / 1e9:.2f} GB in {time.time() - t0:.0f}s", file=sys.__stderr__, flush=True)
+        r = run("twin", path, 1, 12, 8, 9, 24, 64, timeout=900)
+        print(f"[decoder] twin run done at {time.time() - t0:.0f}s", file=sys.__stderr__, flush=True)
+    finally:
+        path.unlink(missing_ok=True)
+    print(r)
+    assert r["backends"] == ["cpu", "hip-gfx950"]
+    assert r["logits"] > 0 and r["differing_logits"] == 0 and r["max_abs_diff"] == 0.0
+    assert r["routing_identical"] and r["ids_identical"] and r["generated"] >= 1
+    assert r["routing_events"] >= (12 + 1) * 8
+    assert r["gpu_ops"].get("hip-gfx950", 0) > 0 and r["gpu_ops"]["hooked"].get("gemv_quant", 0) > 0
