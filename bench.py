@@ -246,6 +246,83 @@ def prefill_leg(dev, workload=PREFILL_WORKLOAD, seed=1234, reps=10, cpu=True, cp
     return res
 
 
+FP32_PEAK_TFLOPS = 157.3  # MI355X published fp32 (the exact chains issue unpacked FMAs: half of it)
+
+
+def kernels_leg(dev, reps=10, cpu=True):
+    """The per-matrix entry points of the boundary at their engine shapes:
+    fmx_gemm_quant (gemm_quant of the dense batched prefill: a [4096 x 4096]
+    Q8_0 projection over 256 tokens) against fp32 peak, and fmx_matvec over a
+    Q6_K [14336 x 4096] matrix against HBM peak; HIP events on the launch
+    stream; the reference's own gemm_quant (oracle/_ref, 2 threads) beside
+    it, and parity bit for bit."""
+    import numpy as np
+    import torch
+    from freemoe_amd import fmx
+    from freemoe_amd import workloads as wl
+
+    rng = np.random.default_rng(77)
+    res = {}
+    O, I, T = 4096, 4096, 256
+    w = wl.matrix(wl.Q8_0, rng, O, I, sigma=0.02)
+    x = rng.standard_normal((T, I), dtype=np.float32)
+    wd, xd = torch.from_numpy(w).to(dev), torch.from_numpy(x).to(dev)
+    yd = torch.empty((T, O), dtype=torch.float32, device=dev)
+    st = fmx.stream_handle()
+
+    def gemm():
+        fmx.call("fmx_gemm_quant", wl.Q8_0, wd.data_ptr(), xd.data_ptr(), yd.data_ptr(), T, O, I, st)
+
+    gemm()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        gemm()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    tf = 2.0 * T * O * I / (ms * 1e-3) / 1e12
+    g = {"kernel": "gemm_quant_kernel", "shape": f"Q8_0 [{O} x {I}] x {T} tokens", "mean_us": round(ms * 1e3, 2),
+         "achieved_TFLOPs": round(tf, 2), "peak_TFLOPs": FP32_PEAK_TFLOPS, "frac": round(tf / FP32_PEAK_TFLOPS, 4),
+         "bound": "fp32 FMA (exact dot_avx2 chains)"}
+    if cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import fmoracle as fo
+        n = 32
+        t0 = time.perf_counter()
+        ref = fo.ref_gemm(wl.Q8_0, w, x[:n], O, I, fo.ISA_AVX2, threads=2)
+        dt = time.perf_counter() - t0
+        g["cpu_baseline"] = {"value": round(2.0 * n * O * I / dt / 1e9, 2), "unit": "GFLOP/s", "cores": 2,
+                             "kind": "reference", "sample": f"the first {n} of the {T} tokens through gemm_quant"}
+        g["bitwise_equal"] = bool(np.array_equal(yd[:n].cpu().numpy().view(np.uint32), ref.view(np.uint32)))
+    res["gemm_quant"] = g
+    del wd, xd, yd
+
+    R, C = 14336, 4096
+    w6 = wl.matrix(wl.Q6_K, rng, R, C, sigma=0.02)
+    w6d = torch.from_numpy(w6).to(dev)
+    xv = torch.from_numpy(rng.standard_normal(C, dtype=np.float32)).to(dev)
+    yv = torch.empty(R, dtype=torch.float32, device=dev)
+
+    def mv():
+        fmx.call("fmx_matvec", wl.Q6_K, w6d.data_ptr(), xv.data_ptr(), yv.data_ptr(), R, C, st)
+
+    mv()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(reps):
+        mv()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) / reps * 1e3
+    gbs = w6.nbytes / (us * 1e-6) / 1e9
+    res["matvec_q6_k"] = {"kernel": "matvec_q6_k_kernel", "shape": f"Q6_K [{R} x {C}]", "mean_us": round(us, 2),
+                          "achieved_GBs": round(gbs, 1), "peak_GBs": HBM_PEAK_GBS,
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm"}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,6 +332,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the 512-token Q8_0 prefill leg")
     ap.add_argument("--prefill-only", action="store_true", help="run only the prefill leg (for profiling)")
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="run only the per-matrix legs (gemm_quant, Q6_K matvec)")
     ap.add_argument("--ragged-only", action="store_true",
                     help="run only the fine-grained ragged prefill leg (for profiling)")
     ap.add_argument("--copy-bytes", type=int, default=0,
@@ -279,6 +358,9 @@ def main() -> int:
     info = fmx.DeviceInfo()
     fmx.call("fmx_device_info_get", 0, ctypes.byref(info))
 
+    if args.kernels_only:
+        print(json.dumps({"kernels": kernels_leg(dev, reps=args.steps, cpu=not args.no_cpu_baseline)}))
+        return 0
     if args.prefill_only:
         res = prefill_leg(dev, reps=args.steps, cpu=not args.no_cpu_baseline)
         print(json.dumps({"prefill": res}))
@@ -402,6 +484,11 @@ def main() -> int:
                                                    cpu_seconds=8.0)
         except Exception as e:  # reported, never silently dropped
             result["prefill_ragged"] = {"error": f"{type(e).__name__}: {e}"}
+        print("[bench] per-matrix legs", file=sys.stderr, flush=True)
+        try:
+            result["kernels"] = kernels_leg(dev, cpu=not args.no_cpu_baseline)
+        except Exception as e:  # reported, never silently dropped
+            result["kernels"] = {"error": f"{type(e).__name__}: {e}"}
     print(json.dumps(result))
     return 0
 
