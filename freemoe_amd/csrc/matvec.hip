@@ -67,20 +67,7 @@ __global__ __launch_bounds__(kThreads) void matvec_f32_kernel(const float *__res
     if (c == 0 && r < rows) y[r] = total;
 }
 
-// Q6_K: 16 lanes per row over raw blocks. For block b, lane c runs chain
-// k = c mod 16 of dot_avx2 over the block's 256 decoded values (elements
-// 16 m + c), the 16 chains meet as in f32_row_chains, and the block's dot is
-// added to the row total in block order.
-__device__ inline float q6_k_value(const uint8_t *blk, uint32_t e) {
-    const uint32_t n = e >> 7, r = e & 127, l = r & 31, qt = r >> 5; // half, quarter of the half
-    const uint32_t ql = blk[64 * n + l + 32 * (qt & 1)];
-    const uint32_t qh = blk[128 + 32 * n + l];
-    const int q = static_cast<int>(((qt >= 2 ? ql >> 4 : ql & 0x0Fu)) | (((qh >> (2 * qt)) & 3u) << 4)) - 32;
-    const float d = half_bits_to_float(blk[208] | (blk[209] << 8));
-    const float sc = static_cast<float>(static_cast<int8_t>(blk[192 + 8 * n + l / 16 + 2 * qt]));
-    return d * sc * static_cast<float>(q);
-}
-
+// Q6_K: 16 lanes per row over raw blocks (q6_k_row_chains).
 __global__ __launch_bounds__(kThreads) void matvec_q6_k_kernel(const uint8_t *__restrict__ w,
                                                                const float *__restrict__ x,
                                                                float *__restrict__ y, uint32_t rows,
@@ -88,17 +75,7 @@ __global__ __launch_bounds__(kThreads) void matvec_q6_k_kernel(const uint8_t *__
     const uint32_t tid = threadIdx.x, c = tid & 15;
     const uint32_t r = blockIdx.x * (kThreads / 16) + (tid >> 4);
     const uint32_t rr = r < rows ? r : rows - 1;
-    const uint8_t *row = w + static_cast<uint64_t>(rr) * blocks * 210;
-    float total = 0.0f;
-    for (uint32_t b = 0; b < blocks; ++b) {
-        const uint8_t *blk = row + static_cast<uint64_t>(b) * 210;
-        const float *xb = x + static_cast<uint64_t>(b) * 256;
-        float acc = 0.0f;
-#pragma unroll 4
-        for (uint32_t m = 0; m < 16; ++m) acc = fma_rn(q6_k_value(blk, 16 * m + c), xb[16 * m + c], acc);
-        const float t = acc + lane_xor(acc, 8);
-        total = total + hsum8_lanes(t);
-    }
+    const float total = q6_k_row_chains(w + static_cast<uint64_t>(rr) * blocks * 210, x, blocks, c);
     if (c == 0 && r < rows) y[r] = total;
 }
 

@@ -1,4 +1,5 @@
-// matvec.hpp — the F32 row dot of gemv_avx2_row (kernels.cpp:147-167) on 16 lanes.
+// matvec.hpp — 16-lane row dots: F32 in gemv_avx2_row's order
+// (kernels.cpp:147-167), Q6_K in row_dot_fused_scalar's (kernels.cpp:574-590).
 #pragma once
 
 #include "fmx_internal.hpp"
@@ -23,5 +24,52 @@ __device__ inline float f32_row_chains(const float *__restrict__ row, const floa
     for (uint32_t k = tail8 ? n16 + 8 : n16; k < n; ++k) total = fma_rn(row[k], x[k], total);
     return total;
 }
+
+// Element e (< 256) of a raw Q6_K block (quant.cpp:347-371): half n = e / 128;
+// in the half, l = e % 32 and quarter qt = (e % 128) / 32 take the low (qt < 2)
+// or high nibble of ql[64 n + l + 32 (qt % 2)], the bit pair qt of
+// qh[32 n + l], sub-block scale sc[8 n + l / 16 + 2 qt]; (d * sc) * (q - 32).
+__device__ inline float q6_k_value(const uint8_t *blk, uint32_t e) {
+    const uint32_t n = e >> 7, r = e & 127, l = r & 31, qt = r >> 5;
+    const uint32_t ql = blk[64 * n + l + 32 * (qt & 1)];
+    const uint32_t qh = blk[128 + 32 * n + l];
+    const int q = static_cast<int>((qt >= 2 ? ql >> 4 : ql & 0x0Fu) | (((qh >> (2 * qt)) & 3u) << 4)) - 32;
+    const float d = half_bits_to_float(blk[208] | (blk[209] << 8));
+    const float sc = static_cast<float>(static_cast<int8_t>(blk[192 + 8 * n + l / 16 + 2 * qt]));
+    return d * sc * static_cast<float>(q);
+}
+
+// One Q6_K row dot on 16 consecutive lanes (c = lane & 15): for each block,
+// lane c runs chain c of dot_avx2 over the block's 256 decoded values
+// (elements 16 m + c), the chains meet as in f32_row_chains, and the block's
+// dot is added to the row total in block order. Every lane returns the row's
+// value.
+__device__ inline float q6_k_row_chains(const uint8_t *__restrict__ row, const float *x, uint32_t blocks,
+                                        uint32_t c) {
+    float total = 0.0f;
+    for (uint32_t b = 0; b < blocks; ++b) {
+        const uint8_t *blk = row + static_cast<uint64_t>(b) * 210;
+        const float *xb = x + static_cast<uint64_t>(b) * 256;
+        float acc = 0.0f;
+#pragma unroll 4
+        for (uint32_t m = 0; m < 16; ++m) acc = fma_rn(q6_k_value(blk, 16 * m + c), xb[16 * m + c], acc);
+        const float t = acc + lane_xor(acc, 8);
+        total = total + hsum8_lanes(t);
+    }
+    return total;
+}
+
+// Row dots on 16 lanes by type, for kernels that take F32 or Q6_K rows: the
+// value of row r of matrix m ([rows x n], raw rows) against x.
+template <uint32_t kType>
+struct RowDot16 {
+    __device__ static float dot(const void *m, uint32_t r, const float *x, uint32_t n, uint32_t c) {
+        if constexpr (kType == FMX_TYPE_Q6_K)
+            return q6_k_row_chains(static_cast<const uint8_t *>(m) + static_cast<uint64_t>(r) * (n / 256) * 210, x,
+                                   n / 256, c);
+        else
+            return f32_row_chains(static_cast<const float *>(m) + static_cast<uint64_t>(r) * n, x, n, c);
+    }
+};
 
 } // namespace fmx

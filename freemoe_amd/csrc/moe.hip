@@ -818,12 +818,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1),
     }
 }
 
-// F32 experts: 16 lanes per row, x read through the cache.
-__global__ __launch_bounds__(kThreads) void gate_up_f32_kernel(ExpertArgs a, const float *__restrict__ h,
-                                                               const float *__restrict__ logits,
-                                                               uint32_t *__restrict__ ids, float *__restrict__ w,
-                                                               float *__restrict__ act,
-                                                               uint32_t *__restrict__ status) {
+// F32 and Q6_K experts: 16 lanes per row (RowDot16: F32 in gemv_avx2_row's
+// order, Q6_K in row_dot_fused_scalar's), x read through the cache.
+template <uint32_t kT>
+__global__ __launch_bounds__(kThreads) void gate_up_rows16_kernel(ExpertArgs a, const float *__restrict__ h,
+                                                                  const float *__restrict__ logits,
+                                                                  uint32_t *__restrict__ ids, float *__restrict__ w,
+                                                                  float *__restrict__ act,
+                                                                  uint32_t *__restrict__ status) {
     const uint32_t tid = threadIdx.x, c = tid & 15;
     const uint32_t rank = blockIdx.y;
     const uint32_t e = expert_of_rank(a.route, logits, ids, rank, blockIdx.x == 0 && rank == 0, ids, w, status);
@@ -834,19 +836,18 @@ __global__ __launch_bounds__(kThreads) void gate_up_f32_kernel(ExpertArgs a, con
     const uint32_t F = a.ffn, H = a.hidden;
     const uint32_t j = blockIdx.x * (kThreads / 16) + (tid >> 4);
     const uint32_t jr = j < F ? j : F - 1;
-    const float *gate = static_cast<const float *>(a.gate[e]) + static_cast<uint64_t>(jr) * H;
-    const float *up = static_cast<const float *>(a.up[e]) + static_cast<uint64_t>(jr) * H;
-    const float g = f32_row_chains(gate, h, H, c);
-    const float u = f32_row_chains(up, h, H, c);
+    const float g = RowDot16<kT>::dot(a.gate[e], jr, h, H, c);
+    const float u = RowDot16<kT>::dot(a.up[e], jr, h, H, c);
     if (c == 0 && j < F) act[static_cast<uint64_t>(rank) * F + j] = swiglu(g, u);
 }
 
-__global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const float *__restrict__ x,
-                                                            const float *__restrict__ act,
-                                                            const uint32_t *__restrict__ ids,
-                                                            const float *__restrict__ w,
-                                                            float *__restrict__ out,
-                                                            uint32_t *__restrict__ status) {
+template <uint32_t kT>
+__global__ __launch_bounds__(kThreads) void down_rows16_kernel(ExpertArgs a, const float *__restrict__ x,
+                                                               const float *__restrict__ act,
+                                                               const uint32_t *__restrict__ ids,
+                                                               const float *__restrict__ w,
+                                                               float *__restrict__ out,
+                                                               uint32_t *__restrict__ status) {
     __shared__ float dres[kThreads / 16];
     const uint32_t tid = threadIdx.x, c = tid & 15, slot = tid >> 4; // 16 slots
     const uint32_t K = a.top_k, H = a.hidden, F = a.ffn;
@@ -861,8 +862,7 @@ __global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const 
         if (c == 0) atomicOr(status, STATUS_BAD_EXPERT);
         e = 0;
     }
-    const float *row = static_cast<const float *>(a.down[e]) + static_cast<uint64_t>(jr) * F;
-    const float v = f32_row_chains(row, act + static_cast<uint64_t>(rank) * F, F, c);
+    const float v = RowDot16<kT>::dot(a.down[e], jr, act + static_cast<uint64_t>(rank) * F, F, c);
     if (c == 0 && slot < K * jpw) dres[slot] = bad ? 0.0f : v;
     __syncthreads();
     if (tid < jpw) {
@@ -880,48 +880,88 @@ __global__ __launch_bounds__(kThreads) void down_f32_kernel(ExpertArgs a, const 
 // Prefetch depth (chunks in flight per row) of each pass.
 constexpr int kGateUpPF = 1;
 constexpr int kDownPF = 7;
+constexpr int kRJ = 1;
 
-// Gate/up rows in block type TG, down rows in TD.
-template <class TG, class TD>
-int launch_experts_q(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
-                     float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
-                     const hipEvent_t *kev) {
-    constexpr int RJ = 1;
-    const size_t lds_gu = static_cast<size_t>(a.gu_tile) * TG::kLdsFloatsPerBlock * sizeof(float);
-    const size_t lds_dn = static_cast<size_t>(a.dn_tile) * TD::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
-    if (lds_gu > kMaxLds || lds_dn > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
-    auto gu = gate_up_kernel<TG, RJ, kGateUpPF>;
-    auto dn = down_kernel<TD, kDownPF>;
-    if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds_gu)) return rc;
-    if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds_dn)) return rc;
-    const dim3 gu_grid(div_up(a.ffn, (kThreads / 8) * RJ), a.top_k);
+// Dynamic LDS of the chain kernels (gate/up: one tile of h; down: one tile
+// of every rank's activations); 0 for the 16-lane kernels.
+size_t gate_up_lds(const ExpertArgs &a) {
+    switch (a.type_gu) {
+    case FMX_TYPE_Q4_0: return static_cast<size_t>(a.gu_tile) * Q40::kLdsFloatsPerBlock * sizeof(float);
+    case FMX_TYPE_Q8_0: return static_cast<size_t>(a.gu_tile) * Q80::kLdsFloatsPerBlock * sizeof(float);
+    case FMX_TYPE_Q4_K: return static_cast<size_t>(a.gu_tile) * Q4K::kLdsFloatsPerBlock * sizeof(float);
+    }
+    return 0;
+}
+size_t down_lds(const ExpertArgs &a) {
+    switch (a.type_dn) {
+    case FMX_TYPE_Q4_0: return static_cast<size_t>(a.dn_tile) * Q40::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
+    case FMX_TYPE_Q8_0: return static_cast<size_t>(a.dn_tile) * Q80::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
+    case FMX_TYPE_Q4_K: return static_cast<size_t>(a.dn_tile) * Q4K::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
+    }
+    return 0;
+}
+
+// Launches `k` on (grid, kThreads, lds), recording kev[0] / kev[1] at its
+// start and end when kev is given.
+template <class K, class... Args>
+int launch_timed(K k, dim3 grid, size_t lds, hipStream_t s, const hipEvent_t *kev, Args... args) {
     if (kev)
-        hipExtLaunchKernelGGL(gu, gu_grid, dim3(kThreads), lds_gu, s, kev[0], kev[1], 0, a, h, logits, ids, w, ws.act,
-                              status);
+        hipExtLaunchKernelGGL(k, grid, dim3(kThreads), lds, s, kev[0], kev[1], 0, args...);
     else
-        hipLaunchKernelGGL(gu, gu_grid, dim3(kThreads), lds_gu, s, a, h, logits, ids, w, ws.act, status);
-    FMX_LAUNCH_CHECK();
-    const uint32_t jpw = (kThreads / 8) / a.top_k;
-    const dim3 dn_grid(div_up(a.hidden, jpw));
-    if (kev)
-        hipExtLaunchKernelGGL(dn, dn_grid, dim3(kThreads), lds_dn, s, kev[2], kev[3], 0, a, x, ws.act, ids, w, out,
-                              status);
-    else
-        hipLaunchKernelGGL(dn, dn_grid, dim3(kThreads), lds_dn, s, a, x, ws.act, ids, w, out, status);
+        hipLaunchKernelGGL(k, grid, dim3(kThreads), lds, s, args...);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
 
-// The down block type for gate/up in TG (they may differ, as in the
-// reference's Q4_K gate/up with Q6_K down experts).
+// Gate/up rows of every routed expert in block type TG (the lane chains).
 template <class TG>
-int launch_experts_gu(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
-                      float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
-                      const hipEvent_t *kev) {
+int launch_gate_up_q(const ExpertArgs &a, const float *h, const float *logits, uint32_t *ids, float *w, float *act,
+                     uint32_t *status, hipStream_t s, const hipEvent_t *kev) {
+    auto gu = gate_up_kernel<TG, kRJ, kGateUpPF>;
+    const size_t lds = gate_up_lds(a);
+    if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds)) return rc;
+    return launch_timed(gu, dim3(div_up(a.ffn, (kThreads / 8) * kRJ), a.top_k), lds, s, kev, a, h, logits, ids, w,
+                        act, status);
+}
+
+// Down rows of every routed expert in block type TD, combine and residual.
+template <class TD>
+int launch_down_q(const ExpertArgs &a, const float *x, const float *act, const uint32_t *ids, const float *w,
+                  float *out, uint32_t *status, hipStream_t s, const hipEvent_t *kev) {
+    auto dn = down_kernel<TD, kDownPF>;
+    const size_t lds = down_lds(a);
+    if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds)) return rc;
+    const uint32_t jpw = (kThreads / 8) / a.top_k;
+    return launch_timed(dn, dim3(div_up(a.hidden, jpw)), lds, s, kev, a, x, act, ids, w, out, status);
+}
+
+int launch_gate_up(const ExpertArgs &a, const float *h, const float *logits, uint32_t *ids, float *w, float *act,
+                   uint32_t *status, hipStream_t s, const hipEvent_t *kev) {
+    const dim3 grid16(div_up(a.ffn, kThreads / 16), a.top_k);
+    switch (a.type_gu) {
+    case FMX_TYPE_F32:
+        return launch_timed(gate_up_rows16_kernel<FMX_TYPE_F32>, grid16, 0, s, kev, a, h, logits, ids, w, act, status);
+    case FMX_TYPE_Q6_K:
+        return launch_timed(gate_up_rows16_kernel<FMX_TYPE_Q6_K>, grid16, 0, s, kev, a, h, logits, ids, w, act,
+                            status);
+    case FMX_TYPE_Q4_0: return launch_gate_up_q<Q40>(a, h, logits, ids, w, act, status, s, kev);
+    case FMX_TYPE_Q8_0: return launch_gate_up_q<Q80>(a, h, logits, ids, w, act, status, s, kev);
+    case FMX_TYPE_Q4_K: return launch_gate_up_q<Q4K>(a, h, logits, ids, w, act, status, s, kev);
+    }
+    return FMX_ERR_UNSUPPORTED_QUANTISATION;
+}
+
+int launch_down(const ExpertArgs &a, const float *x, const float *act, const uint32_t *ids, const float *w,
+                float *out, uint32_t *status, hipStream_t s, const hipEvent_t *kev) {
+    const dim3 grid16(div_up(a.hidden, (kThreads / 16) / a.top_k));
     switch (a.type_dn) {
-    case FMX_TYPE_Q4_0: return launch_experts_q<TG, Q40>(a, x, h, logits, ids, w, ws, out, status, s, kev);
-    case FMX_TYPE_Q8_0: return launch_experts_q<TG, Q80>(a, x, h, logits, ids, w, ws, out, status, s, kev);
-    case FMX_TYPE_Q4_K: return launch_experts_q<TG, Q4K>(a, x, h, logits, ids, w, ws, out, status, s, kev);
+    case FMX_TYPE_F32:
+        return launch_timed(down_rows16_kernel<FMX_TYPE_F32>, grid16, 0, s, kev, a, x, act, ids, w, out, status);
+    case FMX_TYPE_Q6_K:
+        return launch_timed(down_rows16_kernel<FMX_TYPE_Q6_K>, grid16, 0, s, kev, a, x, act, ids, w, out, status);
+    case FMX_TYPE_Q4_0: return launch_down_q<Q40>(a, x, act, ids, w, out, status, s, kev);
+    case FMX_TYPE_Q8_0: return launch_down_q<Q80>(a, x, act, ids, w, out, status, s, kev);
+    case FMX_TYPE_Q4_K: return launch_down_q<Q4K>(a, x, act, ids, w, out, status, s, kev);
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }
@@ -1097,12 +1137,6 @@ int prepare_expert_args(const fmx_moe_layer *L, const RouteArgs &route, ExpertAr
     e.up = L->up;
     e.down = L->down;
     if (L->up_type != L->gate_type) return FMX_ERR_UNSUPPORTED_QUANTISATION;
-    // the fused expert kernels: F32, Q4_0, Q8_0, Q4_K (Q6_K matrices run
-    // through fmx_matvec / fmx_gemm_quant only)
-    auto fused = [](uint32_t t) {
-        return t == FMX_TYPE_F32 || t == FMX_TYPE_Q4_0 || t == FMX_TYPE_Q8_0 || t == FMX_TYPE_Q4_K;
-    };
-    if (!fused(L->gate_type) || !fused(L->down_type)) return FMX_ERR_UNSUPPORTED_QUANTISATION;
     if (int rc = packed_geometry(L->gate_type, L->ffn, L->hidden, &e.gu)) return rc;
     if (int rc = packed_geometry(L->down_type, L->hidden, L->ffn, &e.dn)) return rc;
     // LDS tiles (blocks): gate/up stages one tile of h, down one tile of every
@@ -1129,31 +1163,18 @@ int prepare_expert_args(const fmx_moe_layer *L, const RouteArgs &route, ExpertAr
 int launch_experts(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
                    float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
                    const hipEvent_t *kev) {
-    float *act = ws.act;
-    if (a.type_gu == FMX_TYPE_F32) {
-        if (a.top_k > kThreads / 16 || a.type_dn != FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
-        if (kev) FMX_HIP_TRY(hipEventRecord(kev[0], s));
-        hipLaunchKernelGGL(gate_up_f32_kernel, dim3(div_up(a.ffn, kThreads / 16), a.top_k), dim3(kThreads), 0, s,
-                           a, h, logits, ids, w, act, status);
-        FMX_LAUNCH_CHECK();
-        if (kev) FMX_HIP_TRY(hipEventRecord(kev[1], s));
-    }
-    if (a.type_gu == FMX_TYPE_F32 && a.type_dn == FMX_TYPE_F32) {
-        const uint32_t jpw = (kThreads / 16) / a.top_k;
-        if (kev) FMX_HIP_TRY(hipEventRecord(kev[2], s));
-        hipLaunchKernelGGL(down_f32_kernel, dim3(div_up(a.hidden, jpw)), dim3(kThreads), 0, s, a, x, act, ids,
-                           w, out, status);
-        FMX_LAUNCH_CHECK();
-        if (kev) FMX_HIP_TRY(hipEventRecord(kev[3], s));
-        return FMX_OK;
-    }
-    if (a.type_gu == FMX_TYPE_F32 || a.type_dn == FMX_TYPE_F32) return FMX_ERR_UNSUPPORTED_QUANTISATION;
-    switch (a.type_gu) {
-    case FMX_TYPE_Q4_0: return launch_experts_gu<Q40>(a, x, h, logits, ids, w, ws, out, status, s, kev);
-    case FMX_TYPE_Q8_0: return launch_experts_gu<Q80>(a, x, h, logits, ids, w, ws, out, status, s, kev);
-    case FMX_TYPE_Q4_K: return launch_experts_gu<Q4K>(a, x, h, logits, ids, w, ws, out, status, s, kev);
-    }
-    return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    auto known = [](uint32_t t) {
+        return t == FMX_TYPE_F32 || t == FMX_TYPE_Q4_0 || t == FMX_TYPE_Q8_0 || t == FMX_TYPE_Q4_K ||
+               t == FMX_TYPE_Q6_K;
+    };
+    if (!known(a.type_gu) || !known(a.type_dn)) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    // the 16-lane down kernel gives each rank at least one of its 16 row slots
+    const bool dn16 = a.type_dn == FMX_TYPE_F32 || a.type_dn == FMX_TYPE_Q6_K;
+    if (dn16 && a.top_k > kThreads / 16) return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    // both kernels' LDS checked before either launches
+    if (gate_up_lds(a) > kMaxLds || down_lds(a) > kMaxLds) return FMX_ERR_SHAPE_MISMATCH;
+    if (int rc = launch_gate_up(a, h, logits, ids, w, ws.act, status, s, kev)) return rc;
+    return launch_down(a, x, ws.act, ids, w, out, status, s, kev ? kev + 2 : nullptr);
 }
 
 } // namespace fmx

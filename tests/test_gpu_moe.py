@@ -276,14 +276,29 @@ def test_block_type_router(gpu, name):
     tp.check_prefill(gpu, lw, x)
 
 
-@pytest.mark.parametrize("gate_type,down_type", [(wl.Q4_K, wl.Q8_0), (wl.Q8_0, wl.Q4_0), (wl.Q4_0, wl.Q4_K)])
+@pytest.mark.parametrize("gate_type,down_type", [(wl.Q4_K, wl.Q8_0), (wl.Q8_0, wl.Q4_0), (wl.Q4_0, wl.Q4_K),
+                                                 (wl.Q4_K, wl.Q6_K), (wl.Q6_K, wl.Q8_0), (wl.Q6_K, wl.Q6_K),
+                                                 (wl.F32, wl.Q4_0)])
 def test_decode_mixed_block_types(gpu, gate_type, down_type):
     """Gate/up and down of different block types (the reference runs Q4_K
     gate/up with Q6_K down, tests.cpp:1479-1544): each projection keeps its
-    own lane chains, the layer stays bit for bit."""
+    own row order (the lane chains; Q6_K and F32 on 16 lanes per row), the
+    layer stays bit for bit, and prefill (which runs the decode kernels for a
+    type the grouped GEMMs do not take) matches it."""
+    import test_gpu_prefill as tp
     lw = wl.make_layer(512, 512, 6, 2, gate_type, 91, down_type=down_type)
     x = wl.inputs(512, 8, 92)
     assert check_layer(gpu, lw, x) == 0
+    if wl.Q6_K in (gate_type, down_type) or wl.F32 in (gate_type, down_type):
+        import torch
+        dl = DeviceLayer(lw, gpu)
+        out, ids, w = dl.prefill(torch.from_numpy(x).to(gpu))
+        torch.cuda.synchronize()
+        want_out, want_ids, _ = host_layer(lw).forward_batch(x)
+        assert np.array_equal(to_np(ids).astype(np.uint32), want_ids)
+        assert np.abs(to_np(out).astype(np.float64) - want_out).max() <= 1e-4
+    else:
+        tp.check_prefill(gpu, lw, x)
 
 
 def test_route_exact_probability_ties(gpu):
