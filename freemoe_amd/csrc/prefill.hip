@@ -45,6 +45,24 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
+// float((int8_t)(byte B of w)) in one instruction: v_cvt_f32_i32 reading the
+// byte through its sign-extending operand select (SDWA). Written out because
+// the compiler otherwise shifts, sign-extends and converts (three
+// instructions per byte).
+template <int B>
+__device__ __forceinline__ float i8_to_f32(uint32_t w) {
+    float r;
+    if constexpr (B == 0)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+    else if constexpr (B == 1)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+    else if constexpr (B == 2)
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+    return r;
+}
+
 // ------------------------------------------------------------ block types --
 // kChunkK: elements per packed chunk (eight 16-byte lane slices). elem(p) /
 // pos(e): element held at packed position p of a chunk, and its inverse.
@@ -65,6 +83,7 @@ struct GQ80 {
         uint4 q[4];
         uint2 d;
     };
+    static constexpr uint32_t kStepLoads = 5; // load instructions of load_step
     __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
                                      uint32_t step, uint32_t h) {
         const uint8_t *q = packed + g.scale_bytes + (static_cast<uint64_t>(r) * g.chunks + step) * 128 + h * 64;
@@ -83,20 +102,17 @@ struct GQ80 {
         c.d[3] = half_bits_to_float(w.d.y >> 16);
     }
     // Positions 64 h + 8 kk .. +8 of the step: bytes 8 (kk % 2) .. +8 of the
-    // lane's slice kk / 2, i.e. blocks 2 (kk % 2) and 2 (kk % 2) + 1.
+    // lane's slice kk / 2, i.e. blocks 2 (kk % 2) and 2 (kk % 2) + 1. Each
+    // int8 is converted straight from its byte of the dword (i8_to_f32).
     __device__ static bf16x8 dequant_kk(const WStep &w, const Dec &c, int kk) {
         const uint4 q = w.q[kk >> 1];
         const uint32_t lo = (kk & 1) ? q.z : q.x, hi = (kk & 1) ? q.w : q.y;
         const float d0 = c.d[2 * (kk & 1)], d1 = c.d[2 * (kk & 1) + 1];
         uint32_t v[4];
-        v[0] = pack_bf16x2(d0 * static_cast<float>(static_cast<int8_t>(lo)),
-                           d0 * static_cast<float>(static_cast<int8_t>(lo >> 8)));
-        v[1] = pack_bf16x2(d0 * static_cast<float>(static_cast<int8_t>(lo >> 16)),
-                           d0 * static_cast<float>(static_cast<int8_t>(lo >> 24)));
-        v[2] = pack_bf16x2(d1 * static_cast<float>(static_cast<int8_t>(hi)),
-                           d1 * static_cast<float>(static_cast<int8_t>(hi >> 8)));
-        v[3] = pack_bf16x2(d1 * static_cast<float>(static_cast<int8_t>(hi >> 16)),
-                           d1 * static_cast<float>(static_cast<int8_t>(hi >> 24)));
+        v[0] = pack_bf16x2(d0 * i8_to_f32<0>(lo), d0 * i8_to_f32<1>(lo));
+        v[1] = pack_bf16x2(d0 * i8_to_f32<2>(lo), d0 * i8_to_f32<3>(lo));
+        v[2] = pack_bf16x2(d1 * i8_to_f32<0>(hi), d1 * i8_to_f32<1>(hi));
+        v[3] = pack_bf16x2(d1 * i8_to_f32<2>(hi), d1 * i8_to_f32<3>(hi));
         return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
     }
 };
@@ -120,6 +136,7 @@ struct GQ40 {
         uint4 q[2];
         uint4 d;
     };
+    static constexpr uint32_t kStepLoads = 3; // load instructions of load_step
     __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
                                      uint32_t step, uint32_t h) {
         const uint32_t c = step >> 1, s0 = 4 * (step & 1) + 2 * h;
@@ -177,6 +194,7 @@ struct GQ4K {
         uint4 q[2];
         uint4 hd;
     };
+    static constexpr uint32_t kStepLoads = 3; // load instructions of load_step
     __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
                                      uint32_t step, uint32_t h) {
         const uint32_t c = step >> 1, s0 = 4 * (step & 1) + 2 * h;
@@ -235,8 +253,8 @@ struct GQ4K {
 // 8 positions (one MFMA K slice) at a time as the B operand. Each weight byte
 // is read once per row tile, and a row tile holds all of an expert's pairs up
 // to 192. Activations: the tile's rows for the next step are loaded during
-// this one and stored to the other of two LDS buffers, where all eight
-// wavefronts read their A operands.
+// this one straight into the other of two LDS buffers (direct-to-LDS loads),
+// where all eight wavefronts read their A operands.
 //
 // v_mfma_f32_32x32x16_bf16: A lane l = tile row 32 mb + l % 32, B lane l =
 // column l % 32, both at positions 64 (l / 32) + 8 kk .. +8 of the step (a GEMM
@@ -266,45 +284,63 @@ __device__ inline bool row_tile(const uint32_t *tiles, uint32_t mt, uint32_t exp
     return e < experts && rows > 0 && rows <= kPrefillTileRows && row0 <= pairs && rows <= pairs - row0;
 }
 
-// One GEMM of a workgroup: weight steps in a ring of three register slots,
-// this thread's share of the activation steps to come (kXBufs register
-// buffers), the accumulators of NMB row blocks (the kernels instantiate one
-// per possible block count, so no MFMA sits under a branch).
-// Thread t stages granule t % 16 of tile rows t / 16 + 32 i (i < NMB); the
-// activation matrix has at least 192 readable rows past every tile's first
-// row (the workspace pads it), and rows past the tile (up to 32 NMB) only
-// feed output rows that are never written.
+typedef const __attribute__((address_space(1))) void *fmx_gptr;
+typedef __attribute__((address_space(3))) void *fmx_lptr;
+
+// 16 bytes per lane from global `src` to LDS `dst_base` + 16 lane (dst_base
+// wave-uniform): global_load_lds_dwordx4.
+__device__ __forceinline__ void load_lds16(const void *src, char *dst_base) {
+    __builtin_amdgcn_global_load_lds((fmx_gptr)src, (fmx_lptr)dst_base, 16, 0, 0);
+}
+
+// The workgroup barrier of a K step, after wait_vm_lgkm0 has waited for this
+// wavefront's LDS reads and for its direct-to-LDS loads: s_barrier without
+// __syncthreads' fence, whose release would also wait for the weight loads
+// in flight (the fence counts every outstanding load, since direct loads
+// write LDS). The empty asm statements keep the compiler from moving memory
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0) (expcnt not waited for), n < 64.
+template <uint32_t N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N < 64, "vmcnt has six bits");
+    __builtin_amdgcn_s_waitcnt((N & 15u) | ((N >> 4) << 14) | (7u << 4));
+}
+
+// One GEMM of a workgroup: weight steps in a ring of three register slots
+// and the accumulators of NMB row blocks (the kernels instantiate one per
+// possible block count, so no MFMA sits under a branch). The activations go
+// from global memory straight into LDS (global_load_lds_dwordx4: no
+// registers, no LDS store instructions): a wavefront's load fills 1 KiB of
+// LDS, 16 bytes per lane in lane order, so thread t (wavefront w, lane l)
+// fills slot l % 16 of tile row sr = 4 w + l / 16 (+ 32 i for row block i)
+// and loads the granule the swizzle puts there, granule (l % 16) ^ (sr % 16).
+// The activation matrix has at least 192 readable rows past every tile's
+// first row (the workspace pads it), and rows past the tile (up to 32 NMB)
+// only feed output rows that are never written.
 //
 // Request order and the in-order vector memory counter: step st requests the
-// weights of step st + 2 first and, at its end, the activations of step
-// st + 1 + kXBufs. Waiting for the activations that step st stores (those of
-// st + 1) also waits for everything requested before them; with two register
-// buffers those were requested two steps earlier and only weights up to step
-// st + 1 precede them, so the weights keep two steps in flight. With one
-// buffer (tiles of more than four row blocks, for the registers) the
-// activations have one step.
+// activations of step st + 1 (into the LDS buffer that step st - 1 read) and
+// then the weights of step st + 2; at its end it waits until at most the
+// weight requests it just made are outstanding (T::kStepLoads), so the
+// activations of st + 1 are in LDS, and the weights keep two steps in flight.
 template <class T, uint32_t NMB>
 struct GemmWave {
-    static constexpr uint32_t kRowStride = kGThreads / 16; // tile rows between a thread's staged rows
-    static constexpr uint32_t kXBufs = NMB <= 4 ? 2 : 1;
-    static constexpr uint32_t kPass = 3 * kXBufs; // steps per pass: ring slots and buffers both turn
+    static constexpr uint32_t kPass = 6; // steps per pass: the ring (3) and the buffers (2) both turn
     typename T::WStep w[3];
-    uint4 xv[kXBufs][NMB];
     f32x16 acc[NMB];
 
-    // rows of the tile's NMB row blocks only (kRowStride = 32: one row per
-    // block)
-    static_assert(kRowStride == 32, "one staged row per row block");
-    __device__ __forceinline__ void load_x(uint32_t b, const __bf16 *src, uint64_t ld, uint32_t k0) {
+    // This thread's granules of step k0's activations into LDS buffer `dst`
+    // (the wavefront's 1 KiB of row block 0 of the buffer: wave-uniform).
+    __device__ __forceinline__ void load_x(char *dst, const __bf16 *src, uint64_t ld, uint32_t k0) {
 #pragma unroll
         for (uint32_t i = 0; i < NMB; ++i)
-            xv[b][i] = ld16(src + static_cast<uint64_t>(kRowStride * i) * ld + k0);
-    }
-    // st: byte address of this thread's granule in row t / 16 of the buffer
-    __device__ __forceinline__ void store_x(uint32_t b, char *st) const {
-#pragma unroll
-        for (uint32_t i = 0; i < NMB; ++i)
-            *reinterpret_cast<uint4 *>(st + i * kRowStride * kGRowBytes) = xv[b][i];
+            load_lds16(src + static_cast<uint64_t>(32 * i) * ld + k0, dst + i * 32 * kGRowBytes);
     }
 
     // The MFMAs of one K step from ring slot `slot`; a_kk[kk]: byte address of
@@ -336,62 +372,58 @@ struct GemmWave {
         }
     }
 
-    // One step: request weights of step `nw` into `slot_next`, multiply step
-    // (ring slot `slot`, LDS buffer `buf`), stage the next step's activations
-    // (register buffer `xb`) into the other LDS buffer, request the
-    // activations of step `nx` into `xb`.
-    __device__ __forceinline__ void step(int slot, int slot_next, uint32_t buf, uint32_t xb, uint32_t nw,
-                                         uint32_t nx, const uint8_t *m0, uint32_t r0, const PackedGeometry &g,
-                                         const __bf16 *xsrc, uint64_t ldx, char *lds, uint32_t aoff0, uint32_t stoff,
+    // One step: request the activations of step `nx` into the other LDS
+    // buffer and the weights of step `nw` into `slot_next`, multiply step
+    // (ring slot `slot`, LDS buffer `buf`), wait for the activations, barrier.
+    __device__ __forceinline__ void step(int slot, int slot_next, uint32_t buf, uint32_t nw, uint32_t nx,
+                                         const uint8_t *m0, uint32_t r0, const PackedGeometry &g,
+                                         const __bf16 *xsrc, uint64_t ldx, char *lds, uint32_t wbase, uint32_t aoff0,
                                          uint32_t h) {
+        load_x(lds + (buf ^ 1) * kGBufBytes + wbase, xsrc, ldx, nx * kGStepK);
         T::load_step(w[slot_next], m0, g, r0, nw, h);
         __builtin_amdgcn_sched_barrier(0);
         const char *a_kk[8];
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) a_kk[kk] = lds + buf * kGBufBytes + (aoff0 ^ (kk << 4));
         multiply(slot, a_kk);
-        store_x(xb, lds + (buf ^ 1) * kGBufBytes + stoff);
-        load_x(xb, xsrc, ldx, nx * kGStepK);
-        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        wait_vm_lgkm0<T::kStepLoads>();
+        lds_barrier();
     }
 
     // K steps [s0, s0 + steps) against weight row (m0, r0).
     __device__ __forceinline__ void run(const uint8_t *m0, uint32_t r0, const PackedGeometry &g,
                                         const __bf16 *xsrc, uint64_t ldx, uint32_t s0, uint32_t steps, char *lds) {
         const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
+        const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const uint32_t last = s0 + steps - 1;
         auto clampk = [last](uint32_t k) { return k < last ? k : last; };
         // A operand of slice kk: row lane % 32 of the block, granule 8 h + kk
         const uint32_t ar = lane & 31;
         const uint32_t aoff0 = ar * kGRowBytes + (((8 * h) ^ xswz(ar)) << 4);
-        // staging: row tid / 16, granule tid % 16
-        const uint32_t sr = tid >> 4, sg = tid & 15;
-        const uint32_t stoff = sr * kGRowBytes + ((sg ^ xswz(sr)) << 4);
-        xsrc += static_cast<uint64_t>(sr) * ldx + 8 * sg;
+        // staging: row sr = 4 w + l / 16 (= tid / 16), slot l % 16
+        const uint32_t sr = tid >> 4;
+        xsrc += static_cast<uint64_t>(sr) * ldx + 8 * ((lane & 15) ^ xswz(sr));
+        const uint32_t wbase = 1024 * wave;
 #pragma unroll
         for (uint32_t mb = 0; mb < NMB; ++mb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
-        // prologue: weights of steps s0, s0 + 1; activations of s0 into LDS
-        // buffer 0; those of s0 + 1 (.. s0 + kXBufs) into the register
-        // buffers (step s0 + i is held by buffer (i + kXBufs - 1) % kXBufs ...
-        // step i stores buffer (i + 1) % kXBufs)
+        // prologue: activations of s0 into LDS buffer 0, weights of s0 and
+        // s0 + 1
+        load_x(lds + wbase, xsrc, ldx, s0 * kGStepK);
 #pragma unroll
         for (int p = 0; p < 2; ++p) T::load_step(w[p], m0, g, r0, clampk(s0 + p), h);
-        load_x(0, xsrc, ldx, s0 * kGStepK);
-        store_x(0, lds + stoff);
-#pragma unroll
-        for (uint32_t b = 1; b <= kXBufs; ++b) load_x(b % kXBufs, xsrc, ldx, clampk(s0 + b) * kGStepK);
+        wait_vm_lgkm0<0>();
         __syncthreads();
         uint32_t s = 0;
-        // steady state: kPass steps (whole turns of the weight ring and the
-        // register buffers) per pass
+        // steady state: kPass steps per pass
         for (; s + kPass <= steps; s += kPass) {
 #pragma unroll
             for (uint32_t u = 0; u < kPass; ++u) {
                 const uint32_t st = s0 + s + u;
-                step(u % 3, (u + 2) % 3, (s + u) & 1, (u + 1) % kXBufs, clampk(st + 2), clampk(st + 1 + kXBufs), m0,
-                     r0, g, xsrc, ldx, lds, aoff0, stoff, h);
+                step(u % 3, (u + 2) % 3, u & 1, clampk(st + 2), clampk(st + 1), m0, r0, g, xsrc, ldx, lds, wbase,
+                     aoff0, h);
             }
         }
         // the remaining steps (fewer than kPass)
@@ -399,8 +431,8 @@ struct GemmWave {
         for (uint32_t u = 0; u < kPass; ++u) {
             if (s + u >= steps) break;
             const uint32_t st = s0 + s + u;
-            step(u % 3, (u + 2) % 3, (s + u) & 1, (u + 1) % kXBufs, clampk(st + 2), clampk(st + 1 + kXBufs), m0, r0,
-                 g, xsrc, ldx, lds, aoff0, stoff, h);
+            step(u % 3, (u + 2) % 3, u & 1, clampk(st + 2), clampk(st + 1), m0, r0, g, xsrc, ldx, lds, wbase, aoff0,
+                 h);
         }
     }
 };
