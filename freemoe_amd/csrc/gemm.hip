@@ -6,15 +6,17 @@
 // < 8 and >= 8), their sum, the 8-lane tree, then an FMA tail. Every output is
 // the reference's bit for bit.
 //
-// Tiles. A workgroup (16 lane groups of 16) owns 16 weight rows x 32 tokens.
-// Lane c of a group runs chain k = c (mod 16) for 4 rows x 8 tokens at once,
+// Tiles. A workgroup (16 lane groups of 16) owns 32 weight rows x 32 tokens.
+// Lane c of a group runs chain k = c (mod 16) for 8 rows x 8 tokens at once,
 // so each LDS value it reads feeds several chains; the K loop stages 256
-// columns at a time: the 16 rows dequantised from their raw blocks, the 32
-// tokens' inputs. Chains persist in registers across the stages, so the K
-// order of every chain is the reference's. The group's rows are gr, gr + 4,
-// gr + 8, gr + 12 (gr = group % 4) and LDS rows are 272 floats apart, so the
-// four groups of a wavefront read 16 distinct banks each; they share tokens
-// (group / 4), which the LDS broadcasts.
+// columns at a time: the 32 rows dequantised from their raw blocks, the 32
+// tokens' inputs (requested a stage ahead). Chains persist in registers
+// across the stages, so the K order of every chain is the reference's. The
+// group's rows are gr, gr + 4, ..., gr + 28 (gr = group % 4) and LDS rows are
+// 272 floats apart, so the four groups of a wavefront read 16 distinct banks
+// each; they share tokens (group / 4), which the LDS broadcasts. Every
+// token's inputs are read once per 32 rows, the largest traffic of the
+// kernel.
 #include "fmx_internal.hpp"
 
 namespace fmx {
@@ -22,11 +24,11 @@ namespace fmx {
 namespace {
 
 constexpr uint32_t kGmThreads = 256;
-constexpr uint32_t kGmRows = 16;     // weight rows per workgroup
+constexpr uint32_t kGmRows = 32;     // weight rows per workgroup
 constexpr uint32_t kGmTokens = 32;   // tokens per workgroup
 constexpr uint32_t kGmK = 256;       // columns per stage (a multiple of every block size)
 constexpr uint32_t kGmWStride = 272; // LDS floats between weight rows
-constexpr uint32_t kGmMR = 4, kGmMT = 8;
+constexpr uint32_t kGmMR = 8, kGmMT = 8;
 
 // Elements 16 s .. 16 s + 15 of one raw block (dequantize_block): the same
 // expressions as the library's block dequantiser, so the values are exact.
@@ -83,7 +85,7 @@ __device__ inline void dequant_segment(uint32_t type_id, const uint8_t *blk, uin
     }
 }
 
-// grid: (ceil(out_dim / 16), ceil(tokens / 32)).
+// grid: (ceil(out_dim / 32), ceil(tokens / 32)).
 __global__ __launch_bounds__(kGmThreads) void gemm_quant_kernel(uint32_t type_id, const uint8_t *__restrict__ w,
                                                                 const float *__restrict__ x, float *__restrict__ y,
                                                                 uint32_t tokens, uint32_t out_dim, uint32_t in_dim,
@@ -100,12 +102,27 @@ __global__ __launch_bounds__(kGmThreads) void gemm_quant_kernel(uint32_t type_id
     for (uint32_t i = 0; i < kGmMR; ++i)
 #pragma unroll
         for (uint32_t j = 0; j < kGmMT; ++j) acc[i][j] = 0.0f;
+    // thread tid's column of the 32 tokens' inputs for the stage at k0 (all
+    // 32 loads requested before any is used)
+    static_assert(kGmThreads == kGmK, "one staged input column per thread");
+    float xs[kGmTokens];
+    auto load_x = [&](uint32_t k0) {
+        const uint32_t k = k0 + tid < in_dim ? k0 + tid : in_dim - 1;
+#pragma unroll
+        for (uint32_t p = 0; p < kGmTokens; ++p) {
+            const uint32_t t = t0 + p < tokens ? t0 + p : tokens - 1;
+            xs[p] = x[static_cast<uint64_t>(t) * in_dim + k];
+        }
+    };
+    load_x(0);
     for (uint32_t k0 = 0; k0 < in_dim; k0 += kGmK) {
         const uint32_t nk = in_dim - k0 < kGmK ? in_dim - k0 : kGmK;
         __syncthreads();
-        // weights: thread -> (row tid / 16, 16-column segment tid % 16)
-        {
-            const uint32_t r = tid >> 4, seg = tid & 15, col = 16 * seg;
+        // weights: thread -> (rows tid / 16 and tid / 16 + 16, 16-column
+        // segment tid % 16)
+#pragma unroll
+        for (uint32_t half = 0; half < kGmRows / 16; ++half) {
+            const uint32_t r = (tid >> 4) + 16 * half, seg = tid & 15, col = 16 * seg;
             const uint32_t o = o0 + r < out_dim ? o0 + r : out_dim - 1;
             float v[16];
             if (col < nk) {
@@ -126,13 +143,13 @@ __global__ __launch_bounds__(kGmThreads) void gemm_quant_kernel(uint32_t type_id
                 for (uint32_t j = 0; j < 16; ++j) wl[r * kGmWStride + col + j] = v[j];
             }
         }
-        // inputs: 32 tokens x nk columns, one float per thread and pass
-        for (uint32_t i = tid; i < kGmTokens * kGmK; i += kGmThreads) {
-            const uint32_t tt = i / kGmK, k = i % kGmK;
-            const uint32_t t = t0 + tt < tokens ? t0 + tt : tokens - 1;
-            if (k < nk) xl[i] = x[static_cast<uint64_t>(t) * in_dim + k0 + k];
+        // inputs: column tid of the 32 tokens, requested one stage ahead
+        if (tid < nk) {
+#pragma unroll
+            for (uint32_t p = 0; p < kGmTokens; ++p) xl[p * kGmK + tid] = xs[p];
         }
         __syncthreads();
+        if (k0 + kGmK < in_dim) load_x(k0 + kGmK);
         // the chains: k = k0 + 16 m + c over whole 16-groups below n16
         const uint32_t m_end = (n16 > k0 ? (n16 - k0 < nk ? n16 - k0 : nk) : 0) / 16;
         for (uint32_t m = 0; m < m_end; ++m) {
