@@ -107,6 +107,8 @@ extern "C" int fmx_matvec(uint32_t type_id, const void *packed, const float *x, 
     if (!packed || !x || !y) return FMX_ERR_INVALID_ARGUMENT;
     // block-type kernels stage x with 16-byte loads
     if (type_id != FMX_TYPE_F32 && (reinterpret_cast<uintptr_t>(x) & 15u)) return FMX_ERR_INVALID_ARGUMENT;
+    // Q6_K blocks: scales and d are read as 2-byte words
+    if (type_id == FMX_TYPE_Q6_K && (reinterpret_cast<uintptr_t>(packed) & 1u)) return FMX_ERR_INVALID_ARGUMENT;
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (type_id) {
     case FMX_TYPE_F32:

@@ -39,22 +39,71 @@ __device__ inline float q6_k_value(const uint8_t *blk, uint32_t e) {
     return d * sc * static_cast<float>(q);
 }
 
+// One lane's share of a raw Q6_K block for chain c: element e = 16 m + c
+// (m < 16) lies in half n = m / 8, at l = 16 (m % 2) + c of the half, quarter
+// qt = (m % 8) / 2; its quant byte is ql[64 n + 16 (m % 2 + 2 (qt % 2)) + c],
+// its bit pairs qh[128 + 32 n + 16 (m % 2) + c], its scale sc[8 n + m % 2 +
+// 2 qt]. The lane loads those 8 + 4 bytes, the 16 scales and d, and its 16
+// inputs x[16 m + c], all requested together.
+struct Q6Lane {
+    uint32_t ql[2][4], qh[2][2];
+    uint32_t sc[8]; // the 16 scales as 2-byte words (blocks start 2-byte aligned)
+    uint32_t d;
+    float xv[16];
+    __device__ __forceinline__ void load(const uint8_t *__restrict__ blk, const float *xb, uint32_t c) {
+#pragma unroll
+        for (uint32_t n = 0; n < 2; ++n) {
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k) ql[n][k] = blk[64 * n + 16 * k + c];
+#pragma unroll
+            for (uint32_t a = 0; a < 2; ++a) qh[n][a] = blk[128 + 32 * n + 16 * a + c];
+        }
+        const uint16_t *s16 = reinterpret_cast<const uint16_t *>(blk + 192);
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) sc[i] = s16[i];
+        d = *reinterpret_cast<const uint16_t *>(blk + 208);
+#pragma unroll
+        for (uint32_t m = 0; m < 16; ++m) xv[m] = xb[16 * m + c];
+    }
+    // Chain c of dot_avx2 over the block's decoded values (d * sc) * (q - 32).
+    __device__ __forceinline__ float chain() const {
+        const float df = half_bits_to_float(d);
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t m = 0; m < 16; ++m) {
+            const uint32_t n = m >> 3, a = m & 1, qt = (m & 7) >> 1;
+            const uint32_t qlb = ql[n][a + 2 * (qt & 1)];
+            const int q = static_cast<int>((qt >= 2 ? qlb >> 4 : qlb & 0x0Fu) | (((qh[n][a] >> (2 * qt)) & 3u) << 4)) - 32;
+            const uint32_t si = 8 * n + a + 2 * qt;
+            const float scf = static_cast<float>(static_cast<int8_t>((sc[si >> 1] >> (8 * (si & 1))) & 0xFFu));
+            acc = fma_rn(df * scf * static_cast<float>(q), xv[m], acc);
+        }
+        return acc;
+    }
+};
+
 // One Q6_K row dot on 16 consecutive lanes (c = lane & 15): for each block,
 // lane c runs chain c of dot_avx2 over the block's 256 decoded values
 // (elements 16 m + c), the chains meet as in f32_row_chains, and the block's
-// dot is added to the row total in block order. Every lane returns the row's
-// value.
+// dot is added to the row total in block order. The next block's bytes and
+// inputs are requested before this block's chain runs. Every lane returns the
+// row's value.
 __device__ inline float q6_k_row_chains(const uint8_t *__restrict__ row, const float *x, uint32_t blocks,
                                         uint32_t c) {
     float total = 0.0f;
-    for (uint32_t b = 0; b < blocks; ++b) {
-        const uint8_t *blk = row + static_cast<uint64_t>(b) * 210;
-        const float *xb = x + static_cast<uint64_t>(b) * 256;
-        float acc = 0.0f;
-#pragma unroll 4
-        for (uint32_t m = 0; m < 16; ++m) acc = fma_rn(q6_k_value(blk, 16 * m + c), xb[16 * m + c], acc);
-        const float t = acc + lane_xor(acc, 8);
-        total = total + hsum8_lanes(t);
+    Q6Lane q[2];
+    if (blocks > 0) q[0].load(row, x, c);
+    for (uint32_t b = 0; b < blocks; b += 2) {
+#pragma unroll
+        for (uint32_t u = 0; u < 2; ++u) {
+            if (b + u >= blocks) break;
+            if (b + u + 1 < blocks)
+                q[u ^ 1].load(row + static_cast<uint64_t>(b + u + 1) * 210, x + static_cast<uint64_t>(b + u + 1) * 256,
+                              c);
+            const float acc = q[u].chain();
+            const float t = acc + lane_xor(acc, 8);
+            total = total + hsum8_lanes(t);
+        }
     }
     return total;
 }

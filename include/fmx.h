@@ -166,7 +166,7 @@ typedef struct fmx_moe_layer {
     double weights_epsilon;       /* expert_weights_epsilon */
     double weights_scale;         /* expert_weights_scale */
     uint32_t gate_type, up_type, down_type;
-    const void *const *gate;      /* device array [experts] of packed matrices */
+    const void *const *gate;      /* device array [experts] of packed matrices (16-byte aligned) */
     const void *const *up;
     const void *const *down;
 } fmx_moe_layer;
