@@ -79,6 +79,31 @@ __global__ __launch_bounds__(kThreads) void matvec_q6_k_kernel(const uint8_t *__
     if (c == 0 && r < rows) y[r] = total;
 }
 
+// Q6_K with few rows: G lane groups per row, group g taking blocks
+// g, g + G, ... (each block's dot is independent); the block dots meet in LDS
+// and one lane adds them in block order from 0, as q6_k_row_chains does.
+// LDS: (16 / G) rows x blocks floats.
+template <uint32_t G>
+__global__ __launch_bounds__(kThreads) void matvec_q6_k_split_kernel(const uint8_t *__restrict__ w,
+                                                                     const float *__restrict__ x,
+                                                                     float *__restrict__ y, uint32_t rows,
+                                                                     uint32_t blocks) {
+    extern __shared__ float dots[];
+    constexpr uint32_t kRows = kThreads / 16 / G;
+    const uint32_t tid = threadIdx.x, c = tid & 15, grp = tid >> 4;
+    const uint32_t lr = grp / G, part = grp % G;
+    const uint32_t r = blockIdx.x * kRows + lr;
+    const uint32_t rr = r < rows ? r : rows - 1;
+    q6_k_block_dots(w + static_cast<uint64_t>(rr) * blocks * 210, x, blocks, part, G, c, dots + lr * blocks);
+    __syncthreads();
+    if (tid < kRows && blockIdx.x * kRows + tid < rows) {
+        const float *d = dots + tid * blocks;
+        float total = 0.0f;
+        for (uint32_t b = 0; b < blocks; ++b) total = total + d[b];
+        y[blockIdx.x * kRows + tid] = total;
+    }
+}
+
 template <class T, int NR>
 int launch_matvec(const PackedGeometry &g, const void *packed, const float *x, float *y,
                   hipStream_t s) {
@@ -120,6 +145,22 @@ extern "C" int fmx_matvec(uint32_t type_id, const void *packed, const float *x, 
     case FMX_TYPE_Q8_0: return launch_matvec<Q80, 2>(g, packed, x, y, s);
     case FMX_TYPE_Q4_K: return launch_matvec<Q4K, 1>(g, packed, x, y, s);
     case FMX_TYPE_Q6_K:
+        // one lane group per row leaves the device short of wavefronts below
+        // 32768 rows: split each row's blocks over 4 (fewer than 8192 rows)
+        // or 2 groups
+        if (out_dim < 32768 && g.blocks >= 8 && 4ull * g.blocks * sizeof(float) <= 64 * 1024) {
+            const bool four = out_dim < 8192;
+            const uint32_t rows_per_wg = four ? kThreads / 64 : kThreads / 32;
+            const size_t lds = static_cast<size_t>(rows_per_wg) * g.blocks * sizeof(float);
+            if (four)
+                hipLaunchKernelGGL(matvec_q6_k_split_kernel<4>, dim3(div_up(out_dim, rows_per_wg)), dim3(kThreads),
+                                   lds, s, static_cast<const uint8_t *>(packed), x, y, out_dim, g.blocks);
+            else
+                hipLaunchKernelGGL(matvec_q6_k_split_kernel<2>, dim3(div_up(out_dim, rows_per_wg)), dim3(kThreads),
+                                   lds, s, static_cast<const uint8_t *>(packed), x, y, out_dim, g.blocks);
+            FMX_LAUNCH_CHECK();
+            return FMX_OK;
+        }
         hipLaunchKernelGGL(matvec_q6_k_kernel, dim3(div_up(out_dim, kThreads / 16)), dim3(kThreads), 0, s,
                            static_cast<const uint8_t *>(packed), x, y, out_dim, g.blocks);
         FMX_LAUNCH_CHECK();

@@ -108,6 +108,30 @@ __device__ inline float q6_k_row_chains(const uint8_t *__restrict__ row, const f
     return total;
 }
 
+// Dots of blocks b0, b0 + stride, ... (< blocks) of one Q6_K row on 16
+// consecutive lanes, each as in q6_k_row_chains (chain c over elements
+// 16 m + c, the lanes' chains joined), the next block's share requested
+// before a block's chain runs; lane 0 writes block b's dot to out[b].
+__device__ inline void q6_k_block_dots(const uint8_t *__restrict__ row, const float *x, uint32_t blocks,
+                                       uint32_t b0, uint32_t stride, uint32_t c, float *out) {
+    Q6Lane q[2];
+    if (b0 < blocks) q[0].load(row + static_cast<uint64_t>(b0) * 210, x + static_cast<uint64_t>(b0) * 256, c);
+    for (uint32_t b = b0; b < blocks; b += 2 * stride) {
+#pragma unroll
+        for (uint32_t u = 0; u < 2; ++u) {
+            const uint32_t bu = b + u * stride;
+            if (bu >= blocks) break;
+            const uint32_t nb = bu + stride;
+            if (nb < blocks)
+                q[u ^ 1].load(row + static_cast<uint64_t>(nb) * 210, x + static_cast<uint64_t>(nb) * 256, c);
+            const float acc = q[u].chain();
+            const float t = acc + lane_xor(acc, 8);
+            const float dot = hsum8_lanes(t);
+            if (c == 0) out[bu] = dot;
+        }
+    }
+}
+
 // Row dots on 16 lanes by type, for kernels that take F32 or Q6_K rows: the
 // value of row r of matrix m ([rows x n], raw rows) against x.
 template <uint32_t kType>

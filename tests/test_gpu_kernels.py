@@ -77,7 +77,9 @@ MATVEC_CASES = [
     (2, 37, 512), (2, 11, 96), (2, 6, 4096), (2, 1000, 4096), (2, 513, 14336),
     (8, 37, 512), (8, 11, 96), (8, 6, 4096), (8, 1000, 4096), (8, 300, 14336),
     (12, 37, 512), (12, 6, 2048), (12, 768, 2048), (12, 2048, 768),
-    (14, 37, 256), (14, 9, 2048), (14, 300, 14336),
+    # Q6_K: one lane group per row (fewer than 8 blocks), blocks split over
+    # four (fewer than 8192 rows) or two lane groups per row
+    (14, 37, 256), (14, 9, 2048), (14, 300, 14336), (14, 8193, 512), (14, 4095, 4096), (14, 8200, 2048),
 ]
 
 
