@@ -83,7 +83,6 @@ struct GQ80 {
         uint4 q[4];
         uint2 d;
     };
-    static constexpr uint32_t kStepLoads = 5; // load instructions of load_step
     __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
                                      uint32_t step, uint32_t h) {
         const uint8_t *q = packed + g.scale_bytes + (static_cast<uint64_t>(r) * g.chunks + step) * 128 + h * 64;
@@ -136,7 +135,6 @@ struct GQ40 {
         uint4 q[2];
         uint4 d;
     };
-    static constexpr uint32_t kStepLoads = 3; // load instructions of load_step
     __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
                                      uint32_t step, uint32_t h) {
         const uint32_t c = step >> 1, s0 = 4 * (step & 1) + 2 * h;
@@ -194,7 +192,6 @@ struct GQ4K {
         uint4 q[2];
         uint4 hd;
     };
-    static constexpr uint32_t kStepLoads = 3; // load instructions of load_step
     __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
                                      uint32_t step, uint32_t h) {
         const uint32_t c = step >> 1, s0 = 4 * (step & 1) + 2 * h;
@@ -294,11 +291,9 @@ __device__ __forceinline__ void load_lds16(const void *src, char *dst_base) {
 }
 
 // The workgroup barrier of a K step, after wait_vm_lgkm0 has waited for this
-// wavefront's LDS reads and for its direct-to-LDS loads: s_barrier without
-// __syncthreads' fence, whose release would also wait for the weight loads
-// in flight (the fence counts every outstanding load, since direct loads
-// write LDS). The empty asm statements keep the compiler from moving memory
-// accesses across it.
+// wavefront's LDS reads and for its loads (the direct-to-LDS ones among
+// them): s_barrier itself, the empty asm statements keeping the compiler from
+// moving memory accesses across it.
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -324,11 +319,13 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // first row (the workspace pads it), and rows past the tile (up to 32 NMB)
 // only feed output rows that are never written.
 //
-// Request order and the in-order vector memory counter: step st requests the
-// activations of step st + 1 (into the LDS buffer that step st - 1 read) and
-// then the weights of step st + 2; at its end it waits until at most the
-// weight requests it just made are outstanding (T::kStepLoads), so the
-// activations of st + 1 are in LDS, and the weights keep two steps in flight.
+// Requests: step st requests the activations of step st + 1 (into the LDS
+// buffer that step st - 1 read) and the weights of step st + 2, and at its
+// end waits for all of its requests (vmcnt(0)): the activations must be in
+// LDS before the barrier, and the weights have had the step's MFMAs to
+// arrive (waiting only for the activations, with the weights left in flight
+// across the barrier, measured the same). No direct-to-LDS load is in flight
+// when the K loop ends, so the epilogue may reuse the LDS.
 template <class T, uint32_t NMB>
 struct GemmWave {
     static constexpr uint32_t kPass = 6; // steps per pass: the ring (3) and the buffers (2) both turn
@@ -387,7 +384,7 @@ struct GemmWave {
         for (int kk = 0; kk < 8; ++kk) a_kk[kk] = lds + buf * kGBufBytes + (aoff0 ^ (kk << 4));
         multiply(slot, a_kk);
         __builtin_amdgcn_sched_barrier(0);
-        wait_vm_lgkm0<T::kStepLoads>();
+        wait_vm_lgkm0<0>();
         lds_barrier();
     }
 
