@@ -124,6 +124,47 @@ def test_route_and_decode_at_rmsnorm_near_ties(gpu):
     assert check_layer(gpu, lw, x) == 0
 
 
+@pytest.mark.parametrize("kind", ["halves", "wide", "zeros", "hidden_2048"])
+def test_rmsnorm_in_order_sum_across_inputs(gpu, kind):
+    """The in-order fallback on near-tie tokens built from different inputs:
+    multiples of 1/2 (their squares' running sum meets many exact rounding
+    ties), values spread over 2^-40 .. 2^40, a token that is mostly zeros,
+    and hidden 2048. h, logits, ids and weights bit for bit on the batched
+    route and the decode layer."""
+    import torch
+    import near_ties as nt
+    H = 2048 if kind == "hidden_2048" else 4096
+    lw = wl.make_layer(H, 256, 8, 2, wl.Q4_0, 31)
+    rng = np.random.default_rng(37)
+    base = []
+    for t in range(4):
+        if kind == "halves":
+            v = rng.integers(-6, 7, H).astype(np.float32) * np.float32(0.5)
+        elif kind == "wide":
+            v = (rng.standard_normal(H) * np.exp2(rng.uniform(-40, 40, H))).astype(np.float32)
+        elif kind == "zeros":
+            v = np.zeros(H, np.float32)
+            v[rng.integers(0, H, 1500)] = rng.standard_normal(1500).astype(np.float32)
+        else:
+            v = rng.standard_normal(H).astype(np.float32) * np.float32(2.0)
+        # the crafted element moves the sum of squares: the largest for wide
+        v[-1] = np.abs(v).max() if kind == "wide" else np.float32(1.5)
+        base.append(v)
+    x = np.stack([nt.craft(v, lw.norm_weight, lw.rms_eps)[0] for v in base])
+    dl = DeviceLayer(lw, gpu)
+    h, logits, ids, w = dl.route(torch.from_numpy(x).to(gpu))
+    torch.cuda.synchronize()
+    assert dl.status() == 0
+    hl = host_layer(lw)
+    for i in range(len(x)):
+        hh, lg, pr, ii, ww = hl.route(x[i])
+        assert np.array_equal(bits(to_np(h[i])), bits(hh)), f"h token {i}"
+        assert np.array_equal(bits(to_np(logits[i])), bits(lg)), f"logits token {i}"
+        assert np.array_equal(to_np(ids[i]).astype(np.uint32), ii), f"ids token {i}"
+        assert np.array_equal(bits(to_np(w[i])), bits(ww)), f"weights token {i}"
+    assert check_layer(gpu, lw, x) == 0
+
+
 def large_value_layer(gain_log2, gate_scale_bits):
     """A Q4_0 layer whose h (or act) holds values of 2^70 .. 2^106: element 5
     of h is about 2^gain_log2 (its RMSNorm gain; x[:, 5] = 1 and the router
