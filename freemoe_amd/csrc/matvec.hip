@@ -144,14 +144,14 @@ extern "C" int fmx_matvec(uint32_t type_id, const void *packed, const float *x, 
     case FMX_TYPE_Q4_0: return launch_matvec<Q40, 2>(g, packed, x, y, s);
     case FMX_TYPE_Q8_0: return launch_matvec<Q80, 2>(g, packed, x, y, s);
     case FMX_TYPE_Q4_K: return launch_matvec<Q4K, 1>(g, packed, x, y, s);
-    case FMX_TYPE_Q6_K:
+    case FMX_TYPE_Q6_K: {
         // one lane group per row leaves the device short of wavefronts below
         // 32768 rows: split each row's blocks over 4 (fewer than 8192 rows)
         // or 2 groups
-        if (out_dim < 32768 && g.blocks >= 8 && 4ull * g.blocks * sizeof(float) <= 64 * 1024) {
-            const bool four = out_dim < 8192;
-            const uint32_t rows_per_wg = four ? kThreads / 64 : kThreads / 32;
-            const size_t lds = static_cast<size_t>(rows_per_wg) * g.blocks * sizeof(float);
+        const bool four = out_dim < 8192;
+        const uint32_t rows_per_wg = four ? kThreads / 64 : kThreads / 32;
+        const size_t lds = static_cast<size_t>(rows_per_wg) * g.blocks * sizeof(float);
+        if (out_dim < 32768 && g.blocks >= 8 && lds <= 64 * 1024) {
             if (four)
                 hipLaunchKernelGGL(matvec_q6_k_split_kernel<4>, dim3(div_up(out_dim, rows_per_wg)), dim3(kThreads),
                                    lds, s, static_cast<const uint8_t *>(packed), x, y, out_dim, g.blocks);
@@ -165,6 +165,7 @@ extern "C" int fmx_matvec(uint32_t type_id, const void *packed, const float *x, 
                            static_cast<const uint8_t *>(packed), x, y, out_dim, g.blocks);
         FMX_LAUNCH_CHECK();
         return FMX_OK;
+    }
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }
