@@ -236,6 +236,84 @@ struct GQ4K {
     }
 };
 
+// Q6_K raw blocks (256 elements in 210 bytes: ql[128], qh[64], sc[16], d).
+// Positions are elements (the identity order): K step s is half n = s % 2 of
+// block s / 2, elements 128 n + 0..127; lanes 0-31 take 128 n + 0..63 (ql
+// low nibbles, quarters 0 and 1), lanes 32-63 128 n + 64..127 (high
+// nibbles, quarters 2 and 3). Blocks are only 2-byte aligned, so the quant
+// bytes come in with unaligned 16-byte loads (each inside its block).
+typedef unsigned int fmx_u32x4_u1 __attribute__((ext_vector_type(4), aligned(1)));
+__device__ __forceinline__ uint4 ld16u(const uint8_t *p) {
+    const fmx_u32x4_u1 v = *(const __attribute__((address_space(1))) fmx_u32x4_u1 *)(p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+struct GQ6K {
+    static constexpr uint32_t kType = FMX_TYPE_Q6_K;
+    static constexpr uint32_t kChunkK = 256;
+    __host__ __device__ static uint32_t elem(uint32_t p) { return p; }
+    __host__ __device__ static uint32_t pos(uint32_t e) { return e; }
+    // The lane's half of a K step: the half block's 64 ql bytes and 32 qh
+    // bytes (both lane halves read them: low or high nibbles, other bit
+    // pairs), its four sub-block scales and d.
+    struct WStep {
+        uint4 ql[4], qh[2];
+        uint32_t sc, d;
+    };
+    __device__ static void load_step(WStep &w, const uint8_t *packed, const PackedGeometry &g, uint32_t r,
+                                     uint32_t step, uint32_t h) {
+        const uint32_t n = step & 1;
+        const uint8_t *blk = packed + (static_cast<uint64_t>(r) * g.blocks + (step >> 1)) * 210;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w.ql[i] = ld16u(blk + 64 * n + 16 * i);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) w.qh[i] = ld16u(blk + 128 + 32 * n + 16 * i);
+        // scales 8 n + 4 h .. +3 (quarters 2 h and 2 h + 1 of the half, two
+        // 16-element sub-blocks each)
+        const uint16_t *s16 = reinterpret_cast<const uint16_t *>(blk + 192 + 8 * n + 4 * h);
+        w.sc = s16[0] | (static_cast<uint32_t>(s16[1]) << 16);
+        w.d = *reinterpret_cast<const uint16_t *>(blk + 208);
+    }
+    // d sc (exact: 11 x 8 bits) and -32 d sc per sub-block, once per step.
+    struct Dec {
+        float dsc[4], nd[4];
+    };
+    __device__ static void decode(const WStep &w, Dec &c) {
+        const float d = half_bits_to_float(w.d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c.dsc[i] = d * static_cast<float>(static_cast<int8_t>((w.sc >> (8 * i)) & 0xFFu));
+            c.nd[i] = -32.0f * c.dsc[i];
+        }
+    }
+    // Positions 64 h + 8 kk .. +8 of the step: ql bytes 8 kk .. +8 of the
+    // half, qh bytes 8 (kk % 4) .. +8 at bit pair 2 h + kk / 4, scale
+    // (kk % 4) / 2 + 2 (kk / 4) of the lane's four. (d sc) (q - 32) =
+    // fma(d sc, q, -32 d sc) exactly: the product has at most 24 bits.
+    __device__ static bf16x8 dequant_kk(const WStep &w, const Dec &c, int kk) {
+        const uint32_t h = (threadIdx.x & 63) >> 5;
+        const uint4 q = w.ql[kk >> 1];
+        const uint4 b = w.qh[(kk & 3) >> 1];
+        const uint32_t q0 = (kk & 1) ? q.z : q.x, q1 = (kk & 1) ? q.w : q.y;
+        const uint32_t b0 = ((kk & 3) & 1) ? b.z : b.x, b1 = ((kk & 3) & 1) ? b.w : b.y;
+        const uint32_t sh = 4 * h + 2 * (kk >> 2);
+        const uint32_t v0 = ((h ? q0 >> 4 : q0) & 0x0F0F0F0Fu) | (((b0 >> sh) & 0x03030303u) << 4);
+        const uint32_t v1 = ((h ? q1 >> 4 : q1) & 0x0F0F0F0Fu) | (((b1 >> sh) & 0x03030303u) << 4);
+        const int si = ((kk & 3) >> 1) + 2 * (kk >> 2);
+        const float ds = c.dsc[si], nd = c.nd[si];
+        uint32_t v[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t vv = i ? v1 : v0;
+            v[2 * i] = pack_bf16x2(__builtin_fmaf(ds, static_cast<float>(vv & 0xFFu), nd),
+                                   __builtin_fmaf(ds, static_cast<float>((vv >> 8) & 0xFFu), nd));
+            v[2 * i + 1] = pack_bf16x2(__builtin_fmaf(ds, static_cast<float>((vv >> 16) & 0xFFu), nd),
+                                       __builtin_fmaf(ds, static_cast<float>(vv >> 24), nd));
+        }
+        return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
+    }
+};
+
 // ------------------------------------------------------------ the GEMMs --
 //
 // One workgroup (8 wavefronts, two per SIMD, so one wavefront's dequantising
@@ -466,6 +544,18 @@ __global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ h
     }
 }
 
+// Column of activation element f (an ffn index) in the down projection's
+// packed K order (the down matrices' block type decides it; the activations
+// are written straight into that order).
+__device__ __forceinline__ uint32_t down_k_position(uint32_t down_type, uint32_t f) {
+    switch (down_type) {
+    case FMX_TYPE_Q8_0: return f / GQ80::kChunkK * GQ80::kChunkK + GQ80::pos(f % GQ80::kChunkK);
+    case FMX_TYPE_Q4_0: return f / GQ40::kChunkK * GQ40::kChunkK + GQ40::pos(f % GQ40::kChunkK);
+    case FMX_TYPE_Q4_K: return f / GQ4K::kChunkK * GQ4K::kChunkK + GQ4K::pos(f % GQ4K::kChunkK);
+    default: return f; // Q6_K: the identity order
+    }
+}
+
 // Gate and up of 128 ffn rows (32 per wavefront) for one row tile of NMB row
 // blocks, SwiGLU, and the activations written as bf16 in the down
 // projection's packed K order.
@@ -473,7 +563,7 @@ __global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ h
 // rows; after the K loop the gate wavefronts hand their results through LDS
 // (the activation buffers, free by then) to the up wavefronts of the same
 // columns, which apply SwiGLU.
-template <class T, class TD, uint32_t NMB>
+template <class T, uint32_t NMB>
 __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, uint32_t row0, uint32_t rows,
                              const __bf16 *__restrict__ x, __bf16 *__restrict__ act, char *lds) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -493,7 +583,7 @@ __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, ui
     __syncthreads();
     if (!is_up) return;
     const uint32_t F = a.ffn;
-    const uint32_t col = f / TD::kChunkK * TD::kChunkK + TD::pos(f % TD::kChunkK);
+    const uint32_t col = down_k_position(a.type_dn, f);
 #pragma unroll
     for (uint32_t mb = 0; mb < NMB; ++mb) {
 #pragma unroll
@@ -508,7 +598,7 @@ __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, ui
 
 // grid: (ffn / 128, max row tiles): the row tiles past the bucketing's count
 // (their workgroups return at once) come last in dispatch order.
-template <class T, class TD>
+template <class T>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gate_up_gemm_kernel(
     ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, const __bf16 *__restrict__ x,
     __bf16 *__restrict__ act) {
@@ -516,12 +606,12 @@ __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2)
     uint32_t e, row0, rows;
     if (!row_tile(tiles, blockIdx.y, a.experts, pairs, e, row0, rows)) return;
     switch ((rows + 31) / 32) {
-    case 1: gate_up_tile<T, TD, 1>(a, e, row0, rows, x, act, xlds); break;
-    case 2: gate_up_tile<T, TD, 2>(a, e, row0, rows, x, act, xlds); break;
-    case 3: gate_up_tile<T, TD, 3>(a, e, row0, rows, x, act, xlds); break;
-    case 4: gate_up_tile<T, TD, 4>(a, e, row0, rows, x, act, xlds); break;
-    case 5: gate_up_tile<T, TD, 5>(a, e, row0, rows, x, act, xlds); break;
-    default: gate_up_tile<T, TD, 6>(a, e, row0, rows, x, act, xlds); break;
+    case 1: gate_up_tile<T, 1>(a, e, row0, rows, x, act, xlds); break;
+    case 2: gate_up_tile<T, 2>(a, e, row0, rows, x, act, xlds); break;
+    case 3: gate_up_tile<T, 3>(a, e, row0, rows, x, act, xlds); break;
+    case 4: gate_up_tile<T, 4>(a, e, row0, rows, x, act, xlds); break;
+    case 5: gate_up_tile<T, 5>(a, e, row0, rows, x, act, xlds); break;
+    default: gate_up_tile<T, 6>(a, e, row0, rows, x, act, xlds); break;
     }
 }
 
@@ -611,7 +701,7 @@ int launch_gather(const float *h, uint32_t hidden, uint32_t tokens, uint32_t K, 
 template <class T, class TD>
 int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s, hipEvent_t *kev) {
     const size_t lds = 2ull * kGBufBytes; // two activation buffers
-    auto gu = gate_up_gemm_kernel<T, TD>;
+    auto gu = gate_up_gemm_kernel<T>;
     auto dn = down_gemm_kernel<TD>;
     if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds)) return rc;
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds)) return rc;
@@ -636,11 +726,24 @@ int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tile
     return FMX_OK;
 }
 
+template <class T>
+int launch_for_down(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s,
+                    hipEvent_t *kev) {
+    switch (a.type_dn) {
+    case FMX_TYPE_Q8_0: return launch_gemms<T, GQ80>(a, b, max_tiles, s, kev);
+    case FMX_TYPE_Q4_0: return launch_gemms<T, GQ40>(a, b, max_tiles, s, kev);
+    case FMX_TYPE_Q4_K: return launch_gemms<T, GQ4K>(a, b, max_tiles, s, kev);
+    case FMX_TYPE_Q6_K: return launch_gemms<T, GQ6K>(a, b, max_tiles, s, kev);
+    }
+    return FMX_ERR_UNSUPPORTED_QUANTISATION;
+}
+
 uint32_t chunk_k_of(uint32_t type) {
     switch (type) {
     case FMX_TYPE_Q8_0: return GQ80::kChunkK;
     case FMX_TYPE_Q4_0: return GQ40::kChunkK;
     case FMX_TYPE_Q4_K: return GQ4K::kChunkK;
+    case FMX_TYPE_Q6_K: return GQ6K::kChunkK;
     }
     return 0;
 }
@@ -658,27 +761,10 @@ int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_
                            hipEvent_t *kev) {
     if (!prefill_gemm_supported(a)) return FMX_ERR_SHAPE_MISMATCH;
     switch (a.type_gu) {
-    case FMX_TYPE_Q8_0:
-        switch (a.type_dn) {
-        case FMX_TYPE_Q8_0: return launch_gemms<GQ80, GQ80>(a, b, max_tiles, s, kev);
-        case FMX_TYPE_Q4_0: return launch_gemms<GQ80, GQ40>(a, b, max_tiles, s, kev);
-        case FMX_TYPE_Q4_K: return launch_gemms<GQ80, GQ4K>(a, b, max_tiles, s, kev);
-        }
-        break;
-    case FMX_TYPE_Q4_0:
-        switch (a.type_dn) {
-        case FMX_TYPE_Q8_0: return launch_gemms<GQ40, GQ80>(a, b, max_tiles, s, kev);
-        case FMX_TYPE_Q4_0: return launch_gemms<GQ40, GQ40>(a, b, max_tiles, s, kev);
-        case FMX_TYPE_Q4_K: return launch_gemms<GQ40, GQ4K>(a, b, max_tiles, s, kev);
-        }
-        break;
-    case FMX_TYPE_Q4_K:
-        switch (a.type_dn) {
-        case FMX_TYPE_Q8_0: return launch_gemms<GQ4K, GQ80>(a, b, max_tiles, s, kev);
-        case FMX_TYPE_Q4_0: return launch_gemms<GQ4K, GQ40>(a, b, max_tiles, s, kev);
-        case FMX_TYPE_Q4_K: return launch_gemms<GQ4K, GQ4K>(a, b, max_tiles, s, kev);
-        }
-        break;
+    case FMX_TYPE_Q8_0: return launch_for_down<GQ80>(a, b, max_tiles, s, kev);
+    case FMX_TYPE_Q4_0: return launch_for_down<GQ40>(a, b, max_tiles, s, kev);
+    case FMX_TYPE_Q4_K: return launch_for_down<GQ4K>(a, b, max_tiles, s, kev);
+    case FMX_TYPE_Q6_K: return launch_for_down<GQ6K>(a, b, max_tiles, s, kev);
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }

@@ -324,13 +324,14 @@ def test_decode_mixed_block_types(gpu, gate_type, down_type):
     """Gate/up and down of different block types (the reference runs Q4_K
     gate/up with Q6_K down, tests.cpp:1479-1544): each projection keeps its
     own row order (the lane chains; Q6_K and F32 on 16 lanes per row), the
-    layer stays bit for bit, and prefill (which runs the decode kernels for a
-    type the grouped GEMMs do not take) matches it."""
+    layer stays bit for bit, and prefill matches it: the grouped GEMMs within
+    their bf16 tolerance, or, for F32 (which they do not take), the decode
+    kernels within 1e-4."""
     import test_gpu_prefill as tp
     lw = wl.make_layer(512, 512, 6, 2, gate_type, 91, down_type=down_type)
     x = wl.inputs(512, 8, 92)
     assert check_layer(gpu, lw, x) == 0
-    if wl.Q6_K in (gate_type, down_type) or wl.F32 in (gate_type, down_type):
+    if wl.F32 in (gate_type, down_type):
         import torch
         dl = DeviceLayer(lw, gpu)
         out, ids, w = dl.prefill(torch.from_numpy(x).to(gpu))

@@ -4,7 +4,7 @@ Routing (ids, weights) must be bit-identical to the reference's per-token
 routing. The expert FFN runs as grouped GEMMs on bf16 MFMA, so the layer's
 FFN contribution (out - x) is checked against the oracle's within 2e-2
 relative, both as a norm ratio and as max-abs over the largest reference
-value. Shapes the GEMMs do not tile run the decode kernels and stay
+value. Shapes the GEMMs do not tile (F32 experts) run the decode kernels and stay
 bit-identical."""
 import os
 
@@ -30,6 +30,9 @@ CASES = {
     # tiles
     "q8_0_32_experts": (256, 256, 32, 4, wl.Q8_0, 300, None),
     "q4_0_24_experts_zipf": (512, 256, 24, 3, wl.Q4_0, 200, 1.2),
+    # raw Q6_K blocks (identity K order, unaligned 16-byte loads)
+    "q6_k": (256, 512, 4, 2, wl.Q6_K, 64, None),
+    "q6_k_six_row_blocks": (1024, 1024, 4, 2, wl.Q6_K, 380, None),
 }
 
 # the oracle runs the reference's per-token loop; large cases split it over
@@ -98,8 +101,10 @@ def test_prefill_finegrained_q4_k_1100_tokens(gpu):
 
 def test_prefill_mixed_block_types(gpu):
     """Gate/up and down in different block types (Q4_K gate/up with Q8_0 down,
-    Q8_0 gate/up with Q4_0 down)."""
-    for seed, (gt, dt) in enumerate(((wl.Q4_K, wl.Q8_0), (wl.Q8_0, wl.Q4_0))):
+    Q8_0 gate/up with Q4_0 down, Q4_K gate/up with Q6_K down as in FreeMoe's
+    mixed checkpoints, Q6_K gate/up with Q8_0 down)."""
+    for seed, (gt, dt) in enumerate(((wl.Q4_K, wl.Q8_0), (wl.Q8_0, wl.Q4_0), (wl.Q4_K, wl.Q6_K),
+                                     (wl.Q6_K, wl.Q8_0))):
         lw = wl.make_layer(512, 512, 8, 2, gt, 60 + seed, down_type=dt)
         x = wl.inputs(512, 80, 70 + seed)
         check_prefill(gpu, lw, x)
