@@ -23,6 +23,9 @@ ROUTE_CASES = {
     "sixteen_experts_odd_tokens": (256, 64, 16, 4, wl.F32, 37, None),
     "twelve_experts": (128, 64, 12, 3, wl.F32, 21, None),
     "forty_experts_partial_tiles": (260, 64, 40, 6, wl.F32, 45, 1.2),
+    # 256 experts, top-8, hidden 7168 (a DeepSeek-V3-sized router): hidden
+    # beyond 4096 takes the 1024-thread RMSNorm and routing kernels
+    "256_experts_hidden_7168": (7168, 32, 256, 8, wl.Q4_0, 24, 1.2),
 }
 
 
@@ -60,6 +63,7 @@ DECODE_CASES = {
     "q8_0": (256, 512, 4, 2, wl.Q8_0, 12, None),
     "q4_k": (512, 256, 8, 4, wl.Q4_K, 8, None),
     "q4_k_top8_zipf": (256, 768, 16, 8, wl.Q4_K, 8, 1.2),
+    "256_experts_top8_hidden_7168": (7168, 64, 256, 8, wl.Q4_0, 4, 1.2),
 }
 
 

@@ -30,6 +30,8 @@ CASES = {
     # tiles
     "q8_0_32_experts": (256, 256, 32, 4, wl.Q8_0, 300, None),
     "q4_0_24_experts_zipf": (512, 256, 24, 3, wl.Q4_0, 200, 1.2),
+    # 256 experts (the bucketing's maximum), top-8
+    "q8_0_256_experts_top8": (1024, 128, 256, 8, wl.Q8_0, 100, 1.2),
     # raw Q6_K blocks (identity K order, unaligned 16-byte loads)
     "q6_k": (256, 512, 4, 2, wl.Q6_K, 64, None),
     "q6_k_six_row_blocks": (1024, 1024, 4, 2, wl.Q6_K, 380, None),
