@@ -953,12 +953,15 @@ int launch_gate_up(const ExpertArgs &a, const float *h, const float *logits, uin
 
 int launch_down(const ExpertArgs &a, const float *x, const float *act, const uint32_t *ids, const float *w,
                 float *out, uint32_t *status, hipStream_t s, const hipEvent_t *kev) {
-    const dim3 grid16(div_up(a.hidden, (kThreads / 16) / a.top_k));
+    // the 16-lane kernel's rows per workgroup: its 16 slots over the ranks
+    // (launch_experts admits it only for top_k <= 16)
+    auto grid16 = [&a]() { return dim3(div_up(a.hidden, (kThreads / 16) / a.top_k)); };
     switch (a.type_dn) {
     case FMX_TYPE_F32:
-        return launch_timed(down_rows16_kernel<FMX_TYPE_F32>, grid16, 0, s, kev, a, x, act, ids, w, out, status);
+        return launch_timed(down_rows16_kernel<FMX_TYPE_F32>, grid16(), 0, s, kev, a, x, act, ids, w, out, status);
     case FMX_TYPE_Q6_K:
-        return launch_timed(down_rows16_kernel<FMX_TYPE_Q6_K>, grid16, 0, s, kev, a, x, act, ids, w, out, status);
+        return launch_timed(down_rows16_kernel<FMX_TYPE_Q6_K>, grid16(), 0, s, kev, a, x, act, ids, w, out,
+                            status);
     case FMX_TYPE_Q4_0: return launch_down_q<Q40>(a, x, act, ids, w, out, status, s, kev);
     case FMX_TYPE_Q8_0: return launch_down_q<Q80>(a, x, act, ids, w, out, status, s, kev);
     case FMX_TYPE_Q4_K: return launch_down_q<Q4K>(a, x, act, ids, w, out, status, s, kev);

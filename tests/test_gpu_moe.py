@@ -64,6 +64,9 @@ DECODE_CASES = {
     "q4_k": (512, 256, 8, 4, wl.Q4_K, 8, None),
     "q4_k_top8_zipf": (256, 768, 16, 8, wl.Q4_K, 8, 1.2),
     "256_experts_top8_hidden_7168": (7168, 64, 256, 8, wl.Q4_0, 4, 1.2),
+    # the largest top-k the boundary takes (32: every expert chosen) and 16
+    "q4_0_top32_all_experts": (256, 256, 32, 32, wl.Q4_0, 4, None),
+    "q8_0_top16": (512, 512, 24, 16, wl.Q8_0, 4, 1.2),
 }
 
 
@@ -345,6 +348,20 @@ def test_decode_mixed_block_types(gpu, gate_type, down_type):
         assert np.abs(to_np(out).astype(np.float64) - want_out).max() <= 1e-4
     else:
         tp.check_prefill(gpu, lw, x)
+
+
+def test_decode_refuses_16_lane_down_past_16_ranks(gpu):
+    """A Q6_K (or F32) down projection runs 16 lanes per row with 16 row slots
+    per workgroup shared by the ranks: more than 16 ranks is refused with
+    FMX_ERR_UNSUPPORTED_QUANTISATION before anything launches, while the same
+    top-k with Q4_0 down runs (top-32 above)."""
+    import torch
+    from freemoe_amd import fmx
+    lw = wl.make_layer(256, 256, 20, 17, wl.Q4_0, 93, down_type=wl.Q6_K)
+    dl = DeviceLayer(lw, gpu)
+    with pytest.raises(fmx.FmxError):
+        dl.decode(torch.from_numpy(wl.inputs(256, 2, 94)).to(gpu))
+    torch.cuda.synchronize()
 
 
 def test_route_exact_probability_ties(gpu):
