@@ -1,20 +1,24 @@
 // moe.hip — the MoE block of Engine::forward_token on gfx950.
 //
-//   route_kernel    RMSNorm (engine.cpp:723-740) -> router logits (F32, the
-//                   gemv_avx2_row order) -> logit bias (engine.cpp:1611-1616) ->
-//                   softmax (engine.cpp:378-393) -> stable top-k
-//                   (engine.cpp:395-411) -> weights (engine.cpp:1680-1702).
-//                   One workgroup per token: 256 threads per token for batches,
-//                   1024 threads with the router rows staged in LDS for decode.
-//   gate_up_kernel  gate and up rows of each routed expert, fused with SwiGLU
-//                   (engine.cpp:1738-1761; activation.hpp:33, 84).
-//   down_kernel     down rows of all routed experts of a token, the combine in
-//                   rank order (engine.cpp:1770) and the residual add
-//                   (engine.cpp:813-816, 1822).
+// Decode, per token:
+//   route_rows_kernel  one workgroup per router row: RMSNorm (engine.cpp:723-740)
+//                      of the token, then that row's logit (F32, the
+//                      gemv_avx2_row order) and its bias (engine.cpp:1611-1616).
+//   gate_up_kernel     softmax (engine.cpp:378-393), stable top-k
+//                      (engine.cpp:395-411) and the weights (engine.cpp:1680-1702)
+//                      in one wavefront from the logits, then gate and up rows
+//                      of each routed expert fused with SwiGLU
+//                      (engine.cpp:1738-1761; activation.hpp:33, 84).
+//   down_pair_kernel / down_kernel
+//                      down rows of all routed experts, the combine in rank order
+//                      (engine.cpp:1770) and the residual add (engine.cpp:813-816,
+//                      1822).
+// Batches (prefill routing): rmsnorm_kernel once per token, router_tile_kernel
+// (token x row tiles) or router_quant_kernel, route_finish_kernel.
 //
 // gfx950 gives a workgroup up to 160 KiB of LDS; the decode kernels stage the
-// whole router, the whole of h, and every routed expert's activations at once
-// so that no pass waits twice on HBM latency.
+// whole of h and every routed expert's activations at once so that no pass
+// waits twice on HBM latency.
 //
 // RMSNorm's sum of squares is a sequential double sum in the reference. Here it
 // is a parallel sum plus a certificate: every normalised value is checked to
