@@ -19,7 +19,8 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libfmx.so"
 
-SOURCES = ["capi.cpp", "quant.hip", "matvec.hip", "gemm.hip", "moe.hip", "bucket.hip", "prefill.hip"]
+SOURCES = ["capi.cpp", "quant.hip", "matvec.hip", "gemm.hip", "moe.hip", "down_pair_q4k.hip", "bucket.hip",
+           "prefill.hip"]
 
 HIP_FLAGS = [
     "--offload-arch=gfx950",

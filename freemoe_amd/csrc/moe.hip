@@ -27,6 +27,7 @@
 // one lane redo the sum in the reference's order. Either way h is the
 // reference's h bit for bit.
 #include "chains.hpp"
+#include "down_pair.hpp"
 #include "matvec.hpp"
 #include "moe.hpp"
 
@@ -822,182 +823,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1),
     }
 }
 
-// Q4_0 down rows as down_kernel, on twice the lanes: 16 per row slot, 512
-// threads, two wavefronts per SIMD. Lane l < 8 of a slot runs the reference's
-// lane chain l over every block of the row, exactly as down_kernel; per chunk
-// (8 blocks) it computes the blocks' values c (all of a block's arithmetic
-// but the chain's fma: c = (lo + hi) - 8 * sum x) for blocks 0-3, lane l + 8
-// those of blocks 4-7 from the other half of lane l's 16-byte slice, and a
-// DPP rotation of the 16-lane row by 8 hands them to lane l, whose chain then
-// takes blocks 0-7 in order. Every rank's activations fill the LDS as one
-// tile (the host checks that they fit).
-constexpr uint32_t kPairThreads = 512;
-
-// Lane (i + 8) mod 16's value within each row of 16 lanes (DPP row_ror:8).
-__device__ __forceinline__ float row_swap8(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
-}
-
-struct PairChunk {
-    uint2 q; // dwords 2 hf, 2 hf + 1 of the lane's slice: blocks 4 hf .. 4 hf + 3
-    uint4 s; // the chunk's eight block scales
-};
-
-// c of blocks 4 hf + q, q < 4, of one chunk: xs4 / s8 point at the chunk's
-// first block of the tile (this lane's quad and sum; block stride 8).
-template <bool kScaled>
-__device__ __forceinline__ void pair_block_values(const PairChunk &k, const float4 *xs4, const float *s8, uint32_t hf,
-                                                  float (&c)[4]) {
-#pragma unroll
-    for (uint32_t jj = 0; jj < 2; ++jj) {
-        const uint32_t qw = jj ? k.q.y : k.q.x;
-        const uint32_t lo4 = qw & 0x0F0F0F0Fu, hi4 = (qw >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-        for (uint32_t h = 0; h < 2; ++h) {
-            const uint32_t q = 2 * jj + h, b = 4 * hf + q;
-            const float4 xv = xs4[b * 8];
-            float qa, qb, qc, qd;
-            if constexpr (kScaled) {
-                const float2 lq = h ? fp8_pair<true>(lo4) : fp8_pair<false>(lo4);
-                const float2 hq = h ? fp8_pair<true>(hi4) : fp8_pair<false>(hi4);
-                qa = lq.x;
-                qb = lq.y;
-                qc = hq.x;
-                qd = hq.y;
-            } else {
-                qa = h ? ubyte2(lo4) : ubyte0(lo4);
-                qb = h ? ubyte3(lo4) : ubyte1(lo4);
-                qc = h ? ubyte2(hi4) : ubyte0(hi4);
-                qd = h ? ubyte3(hi4) : ubyte1(hi4);
-            }
-            const float lo = fma_rn(qa, xv.x, qb * xv.y);
-            const float hi = fma_rn(qc, xv.z, qd * xv.w);
-            c[q] = (lo + hi) - s8[b * 8];
-        }
-    }
-}
-
-// The chain over one chunk's eight blocks: own values for blocks 0-3, the
-// partner's (lane + 8) for blocks 4-7 (meaningful on lanes l < 8 only).
-__device__ __forceinline__ float pair_chain(const PairChunk &k, const float (&c)[4], float t) {
-    float r[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) r[q] = row_swap8(c[q]);
-    const uint32_t sw[4] = {k.s.x, k.s.y, k.s.z, k.s.w};
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-        const float cb = b < 4 ? c[b] : r[b - 4];
-        const float d = half_bits_to_float((b & 1) ? (sw[b >> 1] >> 16) : (sw[b >> 1] & 0xFFFFu));
-        t = fma_rn(cb, d, t);
-    }
-    return t;
-}
-
-// The row's chunks in rings of PF + 1 register slots, chunk c + PF requested
-// while chunk c is computed. The last one or two rings run with each request
-// under a (wavefront-uniform) test, so nothing past the row's end is read.
-template <int PF, bool kScaled>
-__device__ __forceinline__ float pair_stream(const uint8_t *qp, const uint8_t *sp, uint32_t c_end, const float *tile,
-                                             uint32_t nb_tile, uint32_t l, uint32_t hf, PairChunk (&buf)[PF + 1]) {
-    constexpr uint32_t kSlots = PF + 1;
-    const float4 *xs4 = reinterpret_cast<const float4 *>(tile) + l;
-    const float *s8 = tile + nb_tile * 32 + l;
-    float t = 0.0f;
-    uint32_t c = 0;
-    for (; c + 2 * kSlots <= c_end; c += kSlots) {
-#pragma unroll
-        for (uint32_t p = 0; p < kSlots; ++p) {
-            PairChunk &nx = buf[(p + PF) % kSlots];
-            nx.q = ld8(qp + (p + PF) * 128);
-            nx.s = ld16(sp + (p + PF) * 16);
-            __builtin_amdgcn_sched_barrier(0);
-            float cv[4];
-            pair_block_values<kScaled>(buf[p], xs4 + (c + p) * 64, s8 + (c + p) * 64, hf, cv);
-            t = pair_chain(buf[p], cv, t);
-        }
-        qp += kSlots * 128;
-        sp += kSlots * 16;
-    }
-    // the last chunks (fewer than two rings), in slot order
-#pragma unroll
-    for (uint32_t p = 0; p < 2 * kSlots; ++p) {
-        if (c + p >= c_end) break;
-        if (c + p + PF < c_end) {
-            PairChunk &nx = buf[(p + PF) % kSlots];
-            nx.q = ld8(qp + (p + PF) * 128);
-            nx.s = ld16(sp + (p + PF) * 16);
-        }
-        float cv[4];
-        pair_block_values<kScaled>(buf[p % kSlots], xs4 + (c + p) * 64, s8 + (c + p) * 64, hf, cv);
-        t = pair_chain(buf[p % kSlots], cv, t);
-    }
-    return t;
-}
-
-template <int PF>
-__global__ __launch_bounds__(kPairThreads) __attribute__((amdgpu_waves_per_eu(2, 2), aligned(kHotAlign))) void down_pair_kernel(
-    ExpertArgs a, const float *__restrict__ x, const float *__restrict__ act, const uint32_t *__restrict__ ids,
-    const float *__restrict__ w, float *__restrict__ out, uint32_t *__restrict__ status) {
-    extern __shared__ __align__(16) float lds[];
-    __shared__ float dres[kPairThreads / 16];
-    const uint32_t tid = threadIdx.x, l = tid & 7, hf = (tid >> 3) & 1, slot = tid >> 4;
-    const uint32_t K = a.top_k, H = a.hidden;
-    const uint32_t jpw = (kPairThreads / 16) / K;
-    const uint32_t rank = slot / jpw < K ? slot / jpw : K - 1;
-    const uint32_t j = blockIdx.x * jpw + slot % jpw;
-    const uint32_t jr = j < H ? j : H - 1;
-    uint32_t e = ids[rank];
-    const bool bad = e >= a.experts;
-    if (bad) {
-        if ((tid & 15) == 0) atomicOr(status, STATUS_BAD_EXPERT);
-        e = 0;
-    }
-    const Q40::Row rw = Q40::row(static_cast<const uint8_t *>(a.down[e]), a.dn.scale_bytes, a.dn.blocks_padded,
-                                 a.dn.chunks, jr, l);
-    const uint8_t *qp = rw.quants + 8 * hf;
-    const uint8_t *sp = rw.scales;
-    const uint32_t blocks = a.dn.blocks, c_end = blocks / Q40::kPerChunk;
-    const uint32_t tile_floats = blocks * Q40::kLdsFloatsPerBlock;
-    const uint32_t n = blocks * Q40::kBlock;
-    // every rank's activations requested first (staging waits for its loads
-    // in issue order), then the first weight chunks, then the staging
-    constexpr int kB = 8;
-    XBatch<kB> b0, b1;
-    load_batch<Q40>(b0, act, 0, n, tid, kPairThreads);
-    if (K > 1) load_batch<Q40>(b1, act + a.ffn, 0, n, tid, kPairThreads);
-    PairChunk buf[PF + 1];
-#pragma unroll
-    for (int p = 0; p < PF; ++p) {
-        const uint32_t c = static_cast<uint32_t>(p) < c_end ? p : c_end - 1;
-        buf[p].q = ld8(qp + c * 128);
-        buf[p].s = ld16(sp + c * 16);
-    }
-    bool big = Q40::stage_scaled<kB, true>(act, 0, blocks, lds, tid, kPairThreads, b0);
-    if (K > 1) big |= Q40::stage_scaled<kB, true>(act + a.ffn, 0, blocks, lds + tile_floats, tid, kPairThreads, b1);
-    for (uint32_t r = 2; r < K; ++r)
-        big |= Q40::stage_scaled<kB>(act + static_cast<uint64_t>(r) * a.ffn, 0, blocks, lds + r * tile_floats, tid,
-                                     kPairThreads);
-    const bool scaled = !__syncthreads_or(big);
-    if (!scaled)
-        for (uint32_t r = 0; r < K; ++r)
-            Q40::stage<kB>(act + static_cast<uint64_t>(r) * a.ffn, 0, blocks, lds + r * tile_floats, tid, kPairThreads);
-    __syncthreads();
-    const float *tile = lds + rank * tile_floats;
-    const float t = scaled ? pair_stream<PF, true>(qp, sp, c_end, tile, blocks, l, hf, buf)
-                           : pair_stream<PF, false>(qp, sp, c_end, tile, blocks, l, hf, buf);
-    const float v = hsum8_lanes(t);
-    if ((tid & 15) == 0) dres[slot] = bad ? 0.0f : v;
-    __syncthreads();
-    if (tid < jpw) {
-        const uint32_t jo = blockIdx.x * jpw + tid;
-        if (jo < H) {
-            float ffn = 0.0f;
-            for (uint32_t r = 0; r < K; ++r) ffn = ffn + w[r] * dres[r * jpw + tid];
-            out[jo] = x[jo] + ffn;
-        }
-    }
-}
-
 // F32 and Q6_K experts: 16 lanes per row (RowDot16: F32 in gemv_avx2_row's
 // order, Q6_K in row_dot_fused_scalar's), x read through the cache.
 template <uint32_t kT>
@@ -1060,7 +885,6 @@ __global__ __launch_bounds__(kThreads) void down_rows16_kernel(ExpertArgs a, con
 // Prefetch depth (chunks in flight per row) of each pass.
 constexpr int kGateUpPF = 1;
 constexpr int kDownPF = 7;
-constexpr int kPairPF = 7;
 constexpr int kRJ = 1;
 
 // Dynamic LDS of the chain kernels (gate/up: one tile of h; down: one tile
@@ -1132,13 +956,6 @@ int launch_gate_up(const ExpertArgs &a, const float *h, const float *logits, uin
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }
 
-// The 16-lane Q4_0 down kernel serves a layer when every rank's activations
-// fit the LDS as one tile and the rows are whole chunks.
-bool pair_down_fits(const ExpertArgs &a) {
-    return a.type_dn == FMX_TYPE_Q4_0 && a.top_k <= kPairThreads / 16 && a.dn.blocks % Q40::kPerChunk == 0 &&
-           static_cast<size_t>(a.dn.blocks) * Q40::kLdsFloatsPerBlock * sizeof(float) * a.top_k <= kMaxLds;
-}
-
 int launch_down(const ExpertArgs &a, const float *x, const float *act, const uint32_t *ids, const float *w,
                 float *out, uint32_t *status, hipStream_t s, const hipEvent_t *kev) {
     // the 16-lane kernel's rows per workgroup: its 16 slots over the ranks
@@ -1151,23 +968,12 @@ int launch_down(const ExpertArgs &a, const float *x, const float *act, const uin
         return launch_timed(down_rows16_kernel<FMX_TYPE_Q6_K>, grid16(), 0, s, kev, a, x, act, ids, w, out,
                             status);
     case FMX_TYPE_Q4_0:
-        if (pair_down_fits(a)) {
-            auto dn = down_pair_kernel<kPairPF>;
-            const size_t lds = static_cast<size_t>(a.dn.blocks) * Q40::kLdsFloatsPerBlock * sizeof(float) * a.top_k;
-            if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds)) return rc;
-            const uint32_t jpw = (kPairThreads / 16) / a.top_k;
-            if (kev)
-                hipExtLaunchKernelGGL(dn, dim3(div_up(a.hidden, jpw)), dim3(kPairThreads), lds, s, kev[0], kev[1], 0, a,
-                                      x, act, ids, w, out, status);
-            else
-                hipLaunchKernelGGL(dn, dim3(div_up(a.hidden, jpw)), dim3(kPairThreads), lds, s, a, x, act, ids, w, out,
-                                   status);
-            FMX_LAUNCH_CHECK();
-            return FMX_OK;
-        }
+        if (pair_down_fits<PairQ40>(a)) return launch_down_pair<PairQ40>(a, x, act, ids, w, out, status, s, kev);
         return launch_down_q<Q40>(a, x, act, ids, w, out, status, s, kev);
     case FMX_TYPE_Q8_0: return launch_down_q<Q80>(a, x, act, ids, w, out, status, s, kev);
-    case FMX_TYPE_Q4_K: return launch_down_q<Q4K>(a, x, act, ids, w, out, status, s, kev);
+    case FMX_TYPE_Q4_K:
+        if (pair_down_fits<PairQ4K>(a)) return launch_down_pair_q4k(a, x, act, ids, w, out, status, s, kev);
+        return launch_down_q<Q4K>(a, x, act, ids, w, out, status, s, kev);
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }

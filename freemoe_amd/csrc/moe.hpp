@@ -58,6 +58,9 @@ int prepare_route_args(const fmx_moe_layer *L, RouteArgs *a);
 // `kev`, when given, holds four events: the gate/up kernel's start and end
 // and the down kernel's start and end, recorded by the launches themselves
 // (hipExtLaunchKernelGGL), so that they bracket each kernel's execution.
+// The 16-lane Q4_K down kernel (down_pair.hpp) for layers its fit test admits.
+int launch_down_pair_q4k(const ExpertArgs &a, const float *x, const float *act, const uint32_t *ids, const float *w,
+                         float *out, uint32_t *status, hipStream_t s, const hipEvent_t *kev);
 int launch_experts(const ExpertArgs &a, const float *x, const float *h, const float *logits, uint32_t *ids,
                    float *w, const DecodeScratch &ws, float *out, uint32_t *status, hipStream_t s,
                    const hipEvent_t *kev = nullptr);

@@ -67,6 +67,9 @@ DECODE_CASES = {
     # the largest top-k the boundary takes (32: every expert chosen) and 16
     "q4_0_top32_all_experts": (256, 256, 32, 32, wl.Q4_0, 4, None),
     "q8_0_top16": (512, 512, 24, 16, wl.Q8_0, 4, 1.2),
+    # Mixtral-shaped Q4_K: the 16-lane down kernel's whole prefetch rings
+    # (56 super-blocks per row) besides its tail
+    "q4_k_mixtral_shape": (4096, 14336, 8, 2, wl.Q4_K, 3, None),
 }
 
 
