@@ -104,18 +104,36 @@ __device__ __forceinline__ float2 fp8_pair(uint32_t v) {
     return make_float2(r.x, r.y);
 }
 
-// Value held by lane (lane ^ mask), mask < 8, inside a wavefront.
-__device__ __forceinline__ float lane_xor(float v, int mask) {
-    return __shfl_xor(v, mask, 64);
+// Value held by lane (lane ^ M), M in {1, 2, 4, 8}, by DPP moves inside each
+// row of 16 lanes (VALU only; a shuffle through ds_bpermute would take the
+// LDS pipeline and a wait): M = 1, 2 as quad permutations; M = 4 as
+// row_shr:4 (lanes 4-7 of each 8 take lane - 4) overwritten on banks 0 and 2
+// (lanes 0-3, 8-11) by row_shl:4 (lane + 4); M = 8 as row_ror:8.
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    int r;
+    if constexpr (M == 1) {
+        r = __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false); // quad_perm [1,0,3,2]
+    } else if constexpr (M == 2) {
+        r = __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false); // quad_perm [2,3,0,1]
+    } else if constexpr (M == 4) {
+        const int hi = __builtin_amdgcn_mov_dpp(b, 0x114, 0xF, 0xF, false); // row_shr:4
+        r = __builtin_amdgcn_update_dpp(hi, b, 0x104, 0xF, 0x5, false);     // row_shl:4, banks 0, 2
+    } else {
+        static_assert(M == 8, "lane_xor: mask 1, 2, 4 or 8");
+        r = __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false); // row_ror:8
+    }
+    return __builtin_bit_cast(float, r);
 }
 
 // Horizontal sum of t_l over the 8 lanes l = lane & 7 in the tree of the
 // reference's _mm256 reduction: s_i = t_i + t_{i+4}; (s0 + s1) + (s2 + s3).
 // Addition is commutative, so every lane of the group ends with the same bits.
 __device__ __forceinline__ float hsum8_lanes(float t) {
-    const float s = t + lane_xor(t, 4);
-    const float a = s + lane_xor(s, 1);
-    return a + lane_xor(a, 2);
+    const float s = t + lane_xor<4>(t);
+    const float a = s + lane_xor<1>(s);
+    return a + lane_xor<2>(a);
 }
 
 // Global-memory loads through an address-space-1 pointer. Expert slots are

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kGmThreads) void gemm_quant_kernel(uint32_t type_id
             for (uint32_t i = 0; i < kGmMR; ++i) {
 #pragma unroll
                 for (uint32_t j = 0; j < kGmMT; ++j) {
-                    const float s = acc[i][j] + lane_xor(acc[i][j], 8);
+                    const float s = acc[i][j] + lane_xor<8>(acc[i][j]);
                     float total = hsum8_lanes(s);
                     for (uint32_t k = kt; k < in_dim; ++k)
                         total = fma_rn(wl[(gr + 4 * i) * kGmWStride + k - k0], xl[(gt * kGmMT + j) * kGmK + k - k0],

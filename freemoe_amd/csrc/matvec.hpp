@@ -19,7 +19,7 @@ __device__ inline float f32_row_chains(const float *__restrict__ row, const floa
     for (uint32_t k = 0; k < n16; k += 16) acc = fma_rn(row[k + c], x[k + c], acc);
     const bool tail8 = n - n16 >= 8;
     if (tail8 && c < 8) acc = fma_rn(row[n16 + c], x[n16 + c], acc);
-    const float t = acc + lane_xor(acc, 8);
+    const float t = acc + lane_xor<8>(acc);
     float total = hsum8_lanes(t);
     for (uint32_t k = tail8 ? n16 + 8 : n16; k < n; ++k) total = fma_rn(row[k], x[k], total);
     return total;
@@ -101,7 +101,7 @@ __device__ inline float q6_k_row_chains(const uint8_t *__restrict__ row, const f
                 q[u ^ 1].load(row + static_cast<uint64_t>(b + u + 1) * 210, x + static_cast<uint64_t>(b + u + 1) * 256,
                               c);
             const float acc = q[u].chain();
-            const float t = acc + lane_xor(acc, 8);
+            const float t = acc + lane_xor<8>(acc);
             total = total + hsum8_lanes(t);
         }
     }
@@ -125,7 +125,7 @@ __device__ inline void q6_k_block_dots(const uint8_t *__restrict__ row, const fl
             if (nb < blocks)
                 q[u ^ 1].load(row + static_cast<uint64_t>(nb) * 210, x + static_cast<uint64_t>(nb) * 256, c);
             const float acc = q[u].chain();
-            const float t = acc + lane_xor(acc, 8);
+            const float t = acc + lane_xor<8>(acc);
             const float dot = hsum8_lanes(t);
             if (c == 0) out[bu] = dot;
         }

@@ -395,7 +395,7 @@ __device__ inline float chain_layout_logit(const float *hs, const float *rs, uin
     for (uint32_t s = S / 4 * 4; s < S; ++s) acc = fma_rn(rs[c * cs + s], hs[c * cs + s], acc);
     const bool tail8 = H - n16 >= 8;
     if (tail8 && c < 8) acc = fma_rn(rs[c * cs + S], hs[c * cs + S], acc);
-    const float tt = acc + lane_xor(acc, 8);
+    const float tt = acc + lane_xor<8>(acc);
     float total = hsum8_lanes(tt);
     for (uint32_t k = tail8 ? n16 + 8 : n16; k < H; ++k)
         total = fma_rn(rs[(k - n16) * cs + S], hs[(k - n16) * cs + S], total);
@@ -597,7 +597,7 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
             const float *wr = a.router + static_cast<uint64_t>(r < E ? r : E - 1) * H;
             float v = acc[i][j];
             if (tail8 && c < 8) v = fma_rn(wr[n16 + c], hr[n16 + c], v);
-            const float tt = v + lane_xor(v, 8);
+            const float tt = v + lane_xor<8>(v);
             float total = hsum8_lanes(tt);
             for (uint32_t kk = tail8 ? n16 + 8 : n16; kk < H; ++kk) total = fma_rn(wr[kk], hr[kk], total);
             if (c == 0 && t < tokens && r < E)
