@@ -110,8 +110,8 @@ __device__ __forceinline__ float2 fp8_pair(uint32_t v) {
 // row_shr:4 (lanes 4-7 of each 8 take lane - 4) overwritten on banks 0 and 2
 // (lanes 0-3, 8-11) by row_shl:4 (lane + 4); M = 8 as row_ror:8.
 template <int M>
-__device__ __forceinline__ float lane_xor(float v) {
-    const int b = __builtin_bit_cast(int, v);
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v) {
+    const int b = static_cast<int>(v);
     int r;
     if constexpr (M == 1) {
         r = __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false); // quad_perm [1,0,3,2]
@@ -124,7 +124,43 @@ __device__ __forceinline__ float lane_xor(float v) {
         static_assert(M == 8, "lane_xor: mask 1, 2, 4 or 8");
         r = __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false); // row_ror:8
     }
-    return __builtin_bit_cast(float, r);
+    return static_cast<uint32_t>(r);
+}
+template <int M>
+__device__ __forceinline__ float lane_xor(float v) {
+    return __builtin_bit_cast(float, lane_xor_u32<M>(__builtin_bit_cast(uint32_t, v)));
+}
+template <int M>
+__device__ __forceinline__ uint64_t lane_xor_u64(uint64_t v) {
+    return (static_cast<uint64_t>(lane_xor_u32<M>(static_cast<uint32_t>(v >> 32))) << 32) |
+           lane_xor_u32<M>(static_cast<uint32_t>(v));
+}
+
+// The values of lanes i and i ^ M (M = 16 or 32), the lower lane's first,
+// through the gfx950 permlane swaps (VALU): given v in both operands,
+// v_permlane32_swap leaves v[i & 31] and v[32 + (i & 31)], v_permlane16_swap
+// the even and the odd 16-lane row of i's half. A commutative operation on
+// the two gives every lane the result of op(v_i, v_(i ^ M)).
+template <int M>
+__device__ __forceinline__ void lane_pair_u32(uint32_t v, uint32_t &a, uint32_t &b) {
+    if constexpr (M == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        a = r[0];
+        b = r[1];
+    } else {
+        static_assert(M == 16, "lane_pair: mask 16 or 32");
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        a = r[0];
+        b = r[1];
+    }
+}
+template <int M>
+__device__ __forceinline__ void lane_pair_u64(uint64_t v, uint64_t &a, uint64_t &b) {
+    uint32_t alo, blo, ahi, bhi;
+    lane_pair_u32<M>(static_cast<uint32_t>(v), alo, blo);
+    lane_pair_u32<M>(static_cast<uint32_t>(v >> 32), ahi, bhi);
+    a = (static_cast<uint64_t>(ahi) << 32) | alo;
+    b = (static_cast<uint64_t>(bhi) << 32) | blo;
 }
 
 // Horizontal sum of t_l over the 8 lanes l = lane & 7 in the tree of the

@@ -55,9 +55,20 @@ constexpr int down_rings() {
     return T::kType == FMX_TYPE_Q4_0 ? 7 : 1;
 }
 
+// Wavefront reductions in the butterfly order m = 32, 16, ..., 1 (lane i
+// combines its value with lane i ^ m's at each step), by VALU lane moves
+// (lane_pair / lane_xor) rather than ds_bpermute shuffles. The operations
+// are commutative, so every lane ends with the same bits.
 __device__ inline double wave_sum_double(double v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+    uint64_t a, b;
+    lane_pair_u64<32>(__builtin_bit_cast(uint64_t, v), a, b);
+    v = __builtin_bit_cast(double, a) + __builtin_bit_cast(double, b);
+    lane_pair_u64<16>(__builtin_bit_cast(uint64_t, v), a, b);
+    v = __builtin_bit_cast(double, a) + __builtin_bit_cast(double, b);
+    v += __builtin_bit_cast(double, lane_xor_u64<8>(__builtin_bit_cast(uint64_t, v)));
+    v += __builtin_bit_cast(double, lane_xor_u64<4>(__builtin_bit_cast(uint64_t, v)));
+    v += __builtin_bit_cast(double, lane_xor_u64<2>(__builtin_bit_cast(uint64_t, v)));
+    v += __builtin_bit_cast(double, lane_xor_u64<1>(__builtin_bit_cast(uint64_t, v)));
     return v;
 }
 
@@ -99,18 +110,31 @@ __device__ inline double readlane_double(double v, uint32_t lane) {
 }
 
 __device__ inline uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = __shfl_xor(static_cast<unsigned long long>(v), m, 64);
-        v = o > v ? o : v;
-    }
-    return v;
+    uint64_t a, b;
+    lane_pair_u64<32>(v, a, b);
+    v = a > b ? a : b;
+    lane_pair_u64<16>(v, a, b);
+    v = a > b ? a : b;
+    uint64_t o = lane_xor_u64<8>(v);
+    v = o > v ? o : v;
+    o = lane_xor_u64<4>(v);
+    v = o > v ? o : v;
+    o = lane_xor_u64<2>(v);
+    v = o > v ? o : v;
+    o = lane_xor_u64<1>(v);
+    return o > v ? o : v;
 }
 
 __device__ inline float wave_max_float(float v) {
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
-    return v;
+    uint32_t a, b;
+    lane_pair_u32<32>(__builtin_bit_cast(uint32_t, v), a, b);
+    v = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    lane_pair_u32<16>(__builtin_bit_cast(uint32_t, v), a, b);
+    v = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+    v = fmaxf(v, lane_xor<8>(v));
+    v = fmaxf(v, lane_xor<4>(v));
+    v = fmaxf(v, lane_xor<2>(v));
+    return fmaxf(v, lane_xor<1>(v));
 }
 
 struct Routing {
