@@ -533,10 +533,13 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *_
 constexpr uint32_t kRtPad = 20; // floats per (token or row, chain) in LDS: 16 steps + 4
 template <uint32_t PT, uint32_t PR, uint32_t GT>
 __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const float *__restrict__ h,
-                                                          uint32_t tokens, float *__restrict__ logits) {
+                                                          uint32_t tokens, float *__restrict__ logits,
+                                                          uint32_t *__restrict__ ids, float *__restrict__ weights,
+                                                          uint32_t *__restrict__ status) {
     constexpr uint32_t GR = 16 / GT, TT = GT * PT, TR = GR * PR;
     __shared__ __align__(16) float hl[TT][16][kRtPad];
     __shared__ __align__(16) float wl[TR][16][kRtPad];
+    __shared__ float lg[TT][TR];
     const uint32_t H = a.hidden, E = a.experts, tid = threadIdx.x;
     const uint32_t c = tid & 15, g = tid >> 4;
     const uint32_t tg = (g % GT) * PT, rg = (g / GT) * PR;
@@ -624,9 +627,27 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
             const float tt = v + lane_xor<8>(v);
             float total = hsum8_lanes(tt);
             for (uint32_t kk = tail8 ? n16 + 8 : n16; kk < H; ++kk) total = fma_rn(wr[kk], hr[kk], total);
-            if (c == 0 && t < tokens && r < E)
-                logits[static_cast<uint64_t>(t) * E + r] = a.router_bias ? total + a.router_bias[r] : total;
+            const float logit = a.router_bias ? total + a.router_bias[r < E ? r : E - 1] : total;
+            if (c == 0 && t < tokens && r < E) logits[static_cast<uint64_t>(t) * E + r] = logit;
+            if (c == 0) lg[tg + i][rg + j] = logit;
         }
+    }
+    // with ids (the host passes them when one row tile holds every expert):
+    // each token's routing from its logits in LDS, one wavefront per token,
+    // as route_finish_kernel does it
+    if (!ids) return;
+    __syncthreads();
+    for (uint32_t w = tid >> 6; w < TT; w += 4) {
+        const uint32_t t = t0 + w;
+        if (t >= tokens) break;
+        bool bad;
+        const Routing rt = wave_route(a, lg[w], &bad);
+        const uint32_t lane = tid & 63;
+        if (lane < a.top_k) {
+            ids[static_cast<uint64_t>(t) * a.top_k + lane] = rt.id;
+            weights[static_cast<uint64_t>(t) * a.top_k + lane] = rt.weight;
+        }
+        if (bad && lane == 0) atomicOr(status, STATUS_NONFINITE_SCORE);
     }
 }
 
@@ -1096,29 +1117,39 @@ int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, flo
 // Batched routing: RMSNorm once per token into h, then the router logits in
 // token x row tiles shaped by the expert count (a workgroup per router row and
 // token would redo each token's RMSNorm once per expert).
+// With ids (and weights, status), an F32 router of at most 32 experts (one
+// row tile) also routes each token in the same launch; *routed tells whether
+// it did.
 int launch_route_batched(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
-                         hipStream_t s) {
+                         hipStream_t s, uint32_t *ids = nullptr, float *weights = nullptr,
+                         uint32_t *status = nullptr, bool *routed = nullptr) {
+    if (routed) *routed = false;
     if (a.hidden > kMaxHidden || a.hidden % 4 || a.experts == 0) return FMX_ERR_SHAPE_MISMATCH;
     if (int rc = launch_rmsnorm(a, x, tokens, h, s)) return rc;
     if (a.router_type != FMX_TYPE_F32) return launch_router_quant(a, h, tokens, logits, s);
+    const bool fuse = ids && weights && status && routed && a.experts <= 32;
+    uint32_t *fi = fuse ? ids : nullptr;
     if (a.experts <= 8)
         hipLaunchKernelGGL((router_tile_kernel<1, 1, 2>), dim3(div_up(tokens, 2), div_up(a.experts, 8)), dim3(256), 0,
-                           s, a, h, tokens, logits);
+                           s, a, h, tokens, logits, fi, weights, status);
     else if (a.experts <= 16)
         hipLaunchKernelGGL((router_tile_kernel<1, 2, 2>), dim3(div_up(tokens, 2), div_up(a.experts, 16)), dim3(256), 0,
-                           s, a, h, tokens, logits);
+                           s, a, h, tokens, logits, fi, weights, status);
     else
         hipLaunchKernelGGL((router_tile_kernel<4, 8, 4>), dim3(div_up(tokens, 16), div_up(a.experts, 32)), dim3(256),
-                           0, s, a, h, tokens, logits);
+                           0, s, a, h, tokens, logits, fi, weights, status);
     FMX_LAUNCH_CHECK();
+    if (fuse) *routed = true;
     return FMX_OK;
 }
 
 int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                  uint32_t *ids, float *weights, uint32_t *status, hipStream_t s) {
-    if (int rc = h && tokens > 1 ? launch_route_batched(a, x, tokens, h, logits, s)
+    bool routed = false;
+    if (int rc = h && tokens > 1 ? launch_route_batched(a, x, tokens, h, logits, s, ids, weights, status, &routed)
                                  : launch_route_logits(a, x, tokens, h, logits, s))
         return rc;
+    if (routed) return FMX_OK;
     hipLaunchKernelGGL(route_finish_kernel, dim3(tokens), dim3(64), 0, s, a, logits, ids, weights, status);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
