@@ -154,16 +154,27 @@ struct Routing {
 // A logit that is not finite (the reference raises INTERNAL_ERROR) sets *bad
 // and yields expert r with weight 0, which keeps every later kernel in bounds.
 // kSlots: experts per lane, 64 kSlots >= experts.
+// The logits lane `lane` takes (expert lane + 64 j), read from `logits`.
 template <int kSlots = 4>
-__device__ Routing wave_route(const RouteArgs &a, const float *__restrict__ logits, bool *bad) {
+__device__ __forceinline__ void route_logits_load(const RouteArgs &a, const float *__restrict__ logits,
+                                                  float (&v)[kSlots]) {
+    const uint32_t E = a.experts, lane = threadIdx.x & 63;
+#pragma unroll
+    for (int j = 0; j < kSlots; ++j) {
+        const uint32_t e = lane + 64 * j;
+        v[j] = e < E ? logits[e] : 0.0f;
+    }
+}
+
+// wave_route from logits already loaded by route_logits_load.
+template <int kSlots = 4>
+__device__ Routing wave_route_values(const RouteArgs &a, const float (&v)[kSlots], bool *bad) {
     const uint32_t E = a.experts, K = a.top_k, lane = threadIdx.x & 63;
-    float v[kSlots];
     bool nonfinite = false;
     float m = -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < kSlots; ++j) {
         const uint32_t e = lane + 64 * j;
-        v[j] = e < E ? logits[e] : 0.0f;
         if (e < E) {
             nonfinite |= !__builtin_isfinite(v[j]);
             m = fmaxf(m, v[j]);
@@ -222,6 +233,13 @@ __device__ Routing wave_route(const RouteArgs &a, const float *__restrict__ logi
     }
     r.weight = static_cast<float>(static_cast<double>(wv) * a.weights_scale);
     return r;
+}
+
+template <int kSlots = 4>
+__device__ Routing wave_route(const RouteArgs &a, const float *__restrict__ logits, bool *bad) {
+    float v[kSlots];
+    route_logits_load(a, logits, v);
+    return wave_route_values(a, v, bad);
 }
 
 // RMSNorm (engine.cpp:723-740) of one token held P float4 per thread
@@ -698,6 +716,25 @@ __global__ __launch_bounds__(kThreads) void router_quant_kernel(RouteArgs a, con
 // The expert of rank `rank` for an expert kernel: from the routing computed
 // in this wavefront when `logits` is given (the first workgroup also stores
 // ids, weights and the error flag for the kernels after it), else from ids.
+// The expert of rank `rank` from logits already loaded (route_logits_load);
+// the first block also stores the token's routing (ids_out / w_out) and flags
+// a non-finite logit.
+__device__ inline uint32_t expert_of_rank_values(const RouteArgs &ra, const float (&lv)[4], uint32_t rank,
+                                                 bool first_block, uint32_t *__restrict__ ids_out,
+                                                 float *__restrict__ w_out, uint32_t *__restrict__ status) {
+    bool bad;
+    const Routing r = wave_route_values(ra, lv, &bad);
+    const uint32_t lane = threadIdx.x & 63;
+    if (first_block && threadIdx.x < 64) {
+        if (lane < ra.top_k) {
+            ids_out[lane] = r.id;
+            w_out[lane] = r.weight;
+        }
+        if (bad && lane == 0) atomicOr(status, STATUS_NONFINITE_SCORE);
+    }
+    return __builtin_amdgcn_readlane(static_cast<int>(r.id), rank);
+}
+
 __device__ inline uint32_t expert_of_rank(const RouteArgs &ra, const float *__restrict__ logits,
                                           const uint32_t *__restrict__ ids, uint32_t rank, bool first_block,
                                           uint32_t *__restrict__ ids_out, float *__restrict__ w_out,
@@ -735,10 +772,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4 / RJ
     const uint32_t tid = threadIdx.x, l = tid & 7, slot = tid >> 3;
     const uint32_t rank = blockIdx.y;
     const uint32_t blocks = a.gu.blocks;
-    // h's first tile is requested before the routing, whose loads it overlaps
+    // the logits are requested first, then h's first tile, so that the
+    // routing waits only for the logits (loads complete in issue order) and
+    // h arrives while it runs; without logits (routing given) ids[rank]
+    float lv[4];
+    route_logits_load(a.route, logits ? logits : h, lv);
+    const uint32_t given = logits ? 0u : ids[rank];
+    __builtin_amdgcn_sched_barrier(0);
     XBatch<4> hb;
     load_batch<T>(hb, h, 0, (blocks < a.gu_tile ? blocks : a.gu_tile) * T::kBlock, tid, kThreads);
-    const uint32_t e = expert_of_rank(a.route, logits, ids, rank, blockIdx.x == 0 && rank == 0, ids, w, status);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t e = logits ? expert_of_rank_values(a.route, lv, rank, blockIdx.x == 0 && rank == 0, ids, w, status)
+                              : given;
     if (e >= a.experts) {
         if (tid == 0 && blockIdx.x == 0) atomicOr(status, STATUS_BAD_EXPERT);
         return;
