@@ -71,7 +71,6 @@ __device__ __forceinline__ float i8_to_f32(uint32_t w) {
 // consecutive positions of it into the bf16 B operand of one MFMA.
 
 struct GQ80 {
-    static constexpr uint32_t kType = FMX_TYPE_Q8_0;
     static constexpr uint32_t kChunkK = 128;
     // position p = 16 l + 4 j + k holds element 32 j + 8 k + l
     __host__ __device__ static uint32_t elem(uint32_t p) { return 32 * ((p & 15) >> 2) + 8 * (p & 3) + (p >> 4); }
@@ -117,7 +116,6 @@ struct GQ80 {
 };
 
 struct GQ40 {
-    static constexpr uint32_t kType = FMX_TYPE_Q4_0;
     static constexpr uint32_t kChunkK = 256;
     // position p = 32 l + 4 j + 2 which + nib holds element 32 j + 16 nib + 8 which + l
     __host__ __device__ static uint32_t elem(uint32_t p) {
@@ -176,7 +174,6 @@ struct GQ40 {
 };
 
 struct GQ4K {
-    static constexpr uint32_t kType = FMX_TYPE_Q4_K;
     static constexpr uint32_t kChunkK = 256;
     // position p = 32 l + 8 g + 2 k + nib holds element 64 g + 32 nib + 8 k + l
     __host__ __device__ static uint32_t elem(uint32_t p) {
@@ -249,7 +246,6 @@ __device__ __forceinline__ uint4 ld16u(const uint8_t *p) {
 }
 
 struct GQ6K {
-    static constexpr uint32_t kType = FMX_TYPE_Q6_K;
     static constexpr uint32_t kChunkK = 256;
     __host__ __device__ static uint32_t elem(uint32_t p) { return p; }
     __host__ __device__ static uint32_t pos(uint32_t e) { return e; }
@@ -337,7 +333,6 @@ struct GQ6K {
 // lane l = row 8 (r / 4) + 4 (l / 32) + r % 4, column l % 32.
 
 constexpr uint32_t kGThreads = 512;                           // 8 wavefronts, two per SIMD
-constexpr uint32_t kGBlocks = kPrefillTileRows / 32;         // 6 row blocks of 32
 constexpr uint32_t kGStepK = 128;                             // packed positions per K step
 constexpr uint32_t kGRowBytes = kGStepK * 2;                  // 256 bytes of a tile row
 constexpr uint32_t kGBufBytes = kPrefillTileRows * kGRowBytes; // one LDS activation buffer
