@@ -70,6 +70,13 @@ DECODE_CASES = {
     # Mixtral-shaped Q4_K: the 16-lane down kernel's whole prefetch rings
     # (56 super-blocks per row) besides its tail
     "q4_k_mixtral_shape": (4096, 14336, 8, 2, wl.Q4_K, 3, None),
+    # top-1 (all 32 row slots of a 16-lane down workgroup on one rank), top-3
+    # (10 rows per rank and workgroup: two idle slots, and hidden 224 leaves
+    # the last workgroup's rows partly unused), rows long enough for the down
+    # kernels' whole prefetch rings
+    "q4_0_top3_hidden_224": (224, 4096, 4, 3, wl.Q4_0, 3, None),
+    "q4_0_top1": (256, 4096, 4, 1, wl.Q4_0, 3, None),
+    "q4_k_top1": (256, 4096, 4, 1, wl.Q4_K, 3, None),
 }
 
 
