@@ -55,3 +55,43 @@ def test_decode_graph_replays_match_eager(gpu, type_id, down_type):
         dl.decode(other)  # eager work between replays, through the same workspace
         torch.cuda.synchronize()
     assert dl.status() == 0
+
+
+def test_prefill_graph_replays_match_eager(gpu):
+    """The batched layer (routing, bucketing, gather, grouped GEMMs, combine)
+    captured likewise: the GEMMs accumulate in a fixed order and the
+    bucketing places pairs by rank, so replays equal the eager pass bit for
+    bit."""
+    import torch
+    lw = wl.make_layer(1024, 2048, 8, 2, wl.Q8_0, 71)
+    x = torch.from_numpy(wl.inputs(1024, 256, 72)).to(gpu)
+    other = torch.from_numpy(wl.inputs(1024, 256, 73)).to(gpu)
+    dl = DeviceLayer(lw, gpu)
+    want_out, want_ids, want_w = dl.prefill(x)
+    torch.cuda.synchronize()
+    want = (bits(want_out), bits(want_ids), bits(want_w))
+    out = torch.empty_like(x)
+    ids = torch.empty_like(want_ids)
+    w = torch.empty_like(want_w)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        dl.prefill(x, out, ids, w)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        dl.prefill(x, out, ids, w)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        out.fill_(0.0)
+        ids.fill_(-1)
+        w.fill_(0.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (bits(out), bits(ids), bits(w))
+        for name, g, e in zip(("out", "ids", "weights"), got, want):
+            assert np.array_equal(g, e), f"replay {replay}: {name} differs from the eager prefill"
+        dl.prefill(other)
+        torch.cuda.synchronize()
+    assert dl.prefill_status() == 0
