@@ -37,9 +37,20 @@ UINT8, INT8, UINT16, INT16, UINT32, INT32, FLOAT32, BOOL, STRING, ARRAY, UINT64,
 _SCALAR = {UINT8: "<B", INT8: "<b", UINT16: "<H", INT16: "<h", UINT32: "<I", INT32: "<i", FLOAT32: "<f",
            BOOL: "<?", UINT64: "<Q", INT64: "<q", FLOAT64: "<d"}
 
-# block geometry (elements, bytes) of the tensor types written here
-F32, Q4_0, Q8_0, Q4_K = 0, 2, 8, 12
-GEOMETRY = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144)}
+# block geometry (elements, bytes) of the tensor types written and read here
+# (gguf.cpp:58-106): F32, Q4_0, Q8_0, Q4_K and Q6_K
+F32, Q4_0, Q8_0, Q4_K, Q6_K = 0, 2, 8, 12, 14
+GEOMETRY = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
+
+
+def geometry(type_id: int, name: str = "") -> tuple[int, int]:
+    """(elements, bytes) per block of `type_id`; a type outside GEOMETRY is
+    refused by name instead of failing as a missing key."""
+    try:
+        return GEOMETRY[type_id]
+    except KeyError:
+        raise ValueError(f"{name or 'tensor'}: block type {type_id} is not one of F32, Q4_0, Q8_0, Q4_K, "
+                         f"Q6_K") from None
 
 FNV64_OFFSET = 0xCBF29CE484222325
 FNV64_PRIME = 0x100000001B3
@@ -85,7 +96,7 @@ class Tensor:
     data: bytes | np.ndarray | None  # None: zeros (sparse writes only)
 
     def nbytes(self) -> int:
-        bs, bb = GEOMETRY[self.type_id]
+        bs, bb = geometry(self.type_id, self.name)
         n = int(np.prod(self.dims, dtype=np.int64))
         if self.dims[0] % bs:
             raise ValueError(f"{self.name}: innermost dimension {self.dims[0]} is not whole blocks of {bs}")
@@ -294,34 +305,45 @@ def mixtral_llama(*, hidden: int, ffn: int, layers: int, heads: int, kv_heads: i
                   vocab: int, expert_type: int, router_type: int = F32, down_type: int | None = None,
                   context: int = 4096,
                   rms_eps: float = 1e-5, rope_theta: float = 1e6, data: dict | None = None,
-                  alignment: int = 32) -> GGUFFile:
+                  alignment: int = 32, router_bias: bool = False, weights_norm: bool | None = True,
+                  weights_scale: float | None = None, arch: str = "llama") -> GGUFFile:
     """A Mixtral-style llama-family checkpoint (the vendor layout the llama
     adapter reads, gguf.cpp:2860-2965): ``llama.*`` hyper-parameters,
     ``blk.N.ffn_gate_inp.weight`` as the router and stacked
     ``ffn_{gate,up,down}_exps`` experts (down may hold another block type, as
     Q4_K gate/up with Q6_K down files do). `data` maps tensor names to raw bytes;
     a tensor without an entry is left to a sparse write. The tokenizer is a
-    plain llama (SentencePiece) table of `vocab` pieces."""
+    plain llama (SentencePiece) table of `vocab` pieces.
+
+    Routing options, as the llama adapter reads them: `router_bias` adds an F32
+    ``blk.N.ffn_gate_inp.bias`` [experts] per layer (added to the router logits
+    before the softmax, gguf.cpp:1535, engine.cpp:1611-1616);
+    ``llama.expert_weights_norm`` is written as `weights_norm` (None leaves
+    the key out, and the adapter's default, off, applies: gguf.cpp:1445);
+    ``llama.expert_weights_scale`` (F32) is written when `weights_scale` is
+    given (gguf.cpp:1446). `arch` names another family that shares the llama
+    block and reads the same keys under its own prefix (deepseek41, whose
+    renormalisation adds 1e-20 to the sum instead of clamping it, gguf.cpp:
+    1943-1947)."""
     data = data or {}
     g = GGUFFile(alignment=alignment)
     head_dim = hidden // heads
     md = [
-        ("general.architecture", STRING, "llama"),
+        ("general.architecture", STRING, arch),
         ("general.name", STRING, "fmx synthetic mixtral"),
         ("general.alignment", UINT32, alignment),
-        ("llama.block_count", UINT32, layers),
-        ("llama.context_length", UINT32, context),
-        ("llama.embedding_length", UINT32, hidden),
-        ("llama.feed_forward_length", UINT32, ffn),
-        ("llama.attention.head_count", UINT32, heads),
-        ("llama.attention.head_count_kv", UINT32, kv_heads),
-        ("llama.attention.layer_norm_rms_epsilon", FLOAT32, rms_eps),
-        ("llama.rope.freq_base", FLOAT32, rope_theta),
-        ("llama.rope.dimension_count", UINT32, head_dim),
-        ("llama.expert_count", UINT32, experts),
-        ("llama.expert_used_count", UINT32, top_k),
-        ("llama.expert_weights_norm", BOOL, True),
-        ("llama.vocab_size", UINT32, vocab),
+        (f"{arch}.block_count", UINT32, layers),
+        (f"{arch}.context_length", UINT32, context),
+        (f"{arch}.embedding_length", UINT32, hidden),
+        (f"{arch}.feed_forward_length", UINT32, ffn),
+        (f"{arch}.attention.head_count", UINT32, heads),
+        (f"{arch}.attention.head_count_kv", UINT32, kv_heads),
+        (f"{arch}.attention.layer_norm_rms_epsilon", FLOAT32, rms_eps),
+        (f"{arch}.rope.freq_base", FLOAT32, rope_theta),
+        (f"{arch}.rope.dimension_count", UINT32, head_dim),
+        (f"{arch}.expert_count", UINT32, experts),
+        (f"{arch}.expert_used_count", UINT32, top_k),
+        (f"{arch}.vocab_size", UINT32, vocab),
         ("tokenizer.ggml.model", STRING, "llama"),
         ("tokenizer.ggml.tokens", ARRAY, (STRING, ["<unk>", "<s>", "</s>"] +
                                           [f"<0x{i:02X}>" for i in range(256)] +
@@ -331,6 +353,10 @@ def mixtral_llama(*, hidden: int, ffn: int, layers: int, heads: int, kv_heads: i
         ("tokenizer.ggml.bos_token_id", UINT32, 1),
         ("tokenizer.ggml.eos_token_id", UINT32, 2),
     ]
+    if weights_norm is not None:
+        md.append((f"{arch}.expert_weights_norm", BOOL, bool(weights_norm)))
+    if weights_scale is not None:
+        md.append((f"{arch}.expert_weights_scale", FLOAT32, float(weights_scale)))
     for key, vtype, value in md:
         g.add(key, vtype, value)
 
@@ -348,6 +374,8 @@ def mixtral_llama(*, hidden: int, ffn: int, layers: int, heads: int, kv_heads: i
         t(p + "attn_output.weight", [hidden, hidden], F32)
         t(p + "ffn_norm.weight", [hidden], F32)
         t(p + "ffn_gate_inp.weight", [hidden, experts], router_type)
+        if router_bias:
+            t(p + "ffn_gate_inp.bias", [experts], F32)
         t(p + "ffn_gate_exps.weight", [hidden, ffn, experts], expert_type)
         t(p + "ffn_up_exps.weight", [hidden, ffn, experts], expert_type)
         t(p + "ffn_down_exps.weight", [ffn, hidden, experts], expert_type if down_type is None else down_type)
@@ -382,18 +410,35 @@ class GGUFReader:
     def expert_slices(self, layer: int, expert: int, router_name: str | None = None) -> dict:
         """Expert `expert` of layer `layer` in a stacked layout: gate, up and down
         as raw row-major matrices [(rows, row_bytes)], with their types. The
-        expert's slice of a stacked tensor is its outermost-axis index."""
+        expert's slice of a stacked tensor is its outermost-axis index. A fused
+        ``ffn_gate_up_exps`` tensor holds each expert's gate rows, then its up
+        rows (gguf.cpp:1988-2000, 2928-2958); a file with both the fused and
+        the separate names is refused, as the adapter refuses it."""
         out = {}
         p = f"blk.{layer}."
+        fused = self.tensors.get(p + "ffn_gate_up_exps.weight")
+        if fused is not None and p + "ffn_gate_exps.weight" in self.tensors:
+            raise ValueError(f"{p}: both ffn_gate_up_exps and ffn_gate_exps are present")
         for key in ("gate", "up", "down"):
-            t = self.tensors[p + f"ffn_{key}_exps.weight"]
-            cols, rows, experts = t.dims
-            bs, bb = GEOMETRY[t.type_id]
-            row_bytes = cols // bs * bb
-            stride = rows * row_bytes
-            if stride * experts != t.nbytes:
-                raise ValueError(f"{t.name}: stacked size does not divide by {experts} experts")
-            lo = t.offset + expert * stride
+            if fused is not None and key != "down":
+                t = fused
+                cols, rows2, experts = t.dims
+                rows = rows2 // 2
+                bs, bb = geometry(t.type_id, t.name)
+                row_bytes = cols // bs * bb
+                stride = rows * row_bytes
+                if 2 * stride * experts != t.nbytes or rows2 % 2:
+                    raise ValueError(f"{t.name}: fused size does not split into gate and up of {experts} experts")
+                lo = t.offset + expert * 2 * stride + (stride if key == "up" else 0)
+            else:
+                t = self.tensors[p + f"ffn_{key}_exps.weight"]
+                cols, rows, experts = t.dims
+                bs, bb = geometry(t.type_id, t.name)
+                row_bytes = cols // bs * bb
+                stride = rows * row_bytes
+                if stride * experts != t.nbytes:
+                    raise ValueError(f"{t.name}: stacked size does not divide by {experts} experts")
+                lo = t.offset + expert * stride
             out[key] = (self.data[lo:lo + stride].reshape(rows, row_bytes), t.type_id)
         return out
 
@@ -460,17 +505,51 @@ def read(path: str | os.PathLike) -> GGUFReader:
     return GGUFReader(str(path), md, tensors, data)
 
 
+# Families whose router weight normalisation is fixed by the architecture, not
+# by ``expert_weights_norm`` (gguf.cpp:2046-2058).
+_WEIGHTS_NORM_ON = ("dbrx", "ernie4-5-moe", "maple", "minimax-m2")
+_WEIGHTS_NORM_OFF = ("deepseek",)
+# Families whose MoE block is not plain SwiGLU experts under softmax routing
+# (GeGLU / gelu: gemma, gguf.cpp:1566-1571; relu: smallthinker, 2040-2043; the
+# clamped swiglu-oai and softmax-weight gating of gpt-oss / minimax-m3,
+# 1900, 1950-1956; sigmoid gating by default: glm4-moe, 1463-1469).
+_OTHER_BLOCKS = ("gemma", "gemma2", "gemma3", "smallthinker", "gpt-oss", "minimax-m3", "glm4-moe")
+
+
+def _opt(md: dict, arch: str, name: str, default):
+    """A metadata value as the llama adapter looks it up (gguf.cpp:1035-1037,
+    768-820): the first present of ``arch.name``, ``freemoe.name`` and
+    ``name`` in sorted order."""
+    for key in sorted({f"{arch}.{name}", f"freemoe.{name}", name}):
+        if key in md:
+            return md[key][1]
+    return default
+
+
 def moe_layer(r: GGUFReader, layer: int):
     """Layer `layer`'s MoE block of a checkpoint as workloads.LayerWeights (the
     arrays are views of the memory map): the norm gains (ffn_norm), the router
     (native ``ffn_router.weight`` or llama ``ffn_gate_inp.weight``, F32 or a
-    block type) and every expert's raw gate / up / down rows. Routing options
-    follow the adapters: the native layout renormalises the selected weights
-    (gguf.cpp:3030), a llama file says so in ``llama.expert_weights_norm``."""
+    block type) and every expert's raw gate / up / down rows.
+
+    Routing options follow the adapters. The native layout renormalises the
+    selected weights with scale 1 (gguf.cpp:3027-3028). A llama-family file
+    carries them as metadata and tensors: ``expert_weights_norm`` (default
+    off, gguf.cpp:1445; forced on or off for five families, 2046-2058),
+    ``expert_weights_scale`` (1445-1448; fixed at 1 for maple, 2062-2064),
+    the additive 1e-20 epsilon of deepseek41 (1943-1947) and an F32
+    ``ffn_gate_inp.bias`` added to the logits before the softmax (1535,
+    engine.cpp:1611-1616). A file whose MoE block needs anything else (another
+    gating function, a selection bias, group-limited routing, shared experts,
+    expert projection biases, another activation or zero-centred norms) is
+    refused with NotImplementedError rather than routed differently."""
     from .workloads import LayerWeights
 
     md = r.metadata
     arch = md["general.architecture"][1]
+    router_bias = None
+    weights_scale = 1.0
+    epsilon_additive, weights_epsilon = False, 6.103515625e-5
     if arch == "freemoe-tiny":
         hidden = md["freemoe.hidden_size"][1]
         ffn = md["freemoe.intermediate_size"][1]
@@ -485,10 +564,40 @@ def moe_layer(r: GGUFReader, layer: int):
         experts = md[f"{arch}.expert_count"][1]
         top_k = md[f"{arch}.expert_used_count"][1]
         eps = md[f"{arch}.attention.layer_norm_rms_epsilon"][1]
-        weights_norm = bool(md.get(f"{arch}.expert_weights_norm", (BOOL, False))[1])
         router_name = f"blk.{layer}.ffn_gate_inp.weight"
+        if arch in _OTHER_BLOCKS:
+            raise NotImplementedError(f"{arch}: its MoE block is not softmax-routed SwiGLU experts")
+        if int(_opt(md, arch, "expert_gating_func", 0)) not in (0, 1):
+            raise NotImplementedError(f"{arch}: expert_gating_func is not softmax")
+        if int(_opt(md, arch, "expert_group_count", 0)) > 1:
+            raise NotImplementedError(f"{arch}: group-limited routing")
+        if f"{arch}.swiglu_clamp_exp" in md:
+            raise NotImplementedError(f"{arch}: clamped SwiGLU")
+        for tail in ("ffn_exp_probs_b.bias", "ffn_gate_exps.bias", "ffn_up_exps.bias", "ffn_down_exps.bias",
+                     "ffn_gate_shexp.weight", "ffn_up_shexp.weight", "ffn_down_shexp.weight",
+                     "ffn_gate_inp_shexp.weight"):
+            if any(name.endswith(tail) for name in r.tensors):
+                raise NotImplementedError(f"{arch}: the MoE block carries {tail}")
+        weights_norm = bool(_opt(md, arch, "expert_weights_norm", False))
+        if arch in _WEIGHTS_NORM_ON:
+            weights_norm = True
+        if arch in _WEIGHTS_NORM_OFF:
+            weights_norm = False
+        weights_scale = float(_opt(md, arch, "expert_weights_scale", 1.0))
+        if not weights_scale > 0.0:
+            raise ValueError(f"{arch}: expert_weights_scale must be positive")
+        if arch == "maple":
+            weights_scale = 1.0
+        if arch == "deepseek41":
+            epsilon_additive, weights_epsilon = True, 1e-20
+        bias_name = f"blk.{layer}.ffn_gate_inp.bias"
+        if bias_name in r.tensors:
+            bt = r.tensors[bias_name]
+            if bt.type_id != F32 or bt.dims != [experts]:
+                raise NotImplementedError(f"{bias_name}: only an F32 [experts] router bias is read")
+            router_bias = np.array(r.tensor_bytes(bias_name).view(np.float32))
     rt = r.tensors[router_name]
-    bs, bb = GEOMETRY[rt.type_id]
+    bs, bb = geometry(rt.type_id, router_name)
     router_raw = r.tensor_bytes(router_name).reshape(experts, hidden // bs * bb)
     norm = r.tensor_bytes(f"blk.{layer}.ffn_norm.weight").view(np.float32)
     gate, up, down = [], [], []
@@ -500,7 +609,8 @@ def moe_layer(r: GGUFReader, layer: int):
         down.append(sl["down"][0])
         types = (sl["gate"][1], sl["down"][1])
     router_f32 = router_raw.view(np.float32).reshape(experts, hidden) if rt.type_id == F32 else None
-    return LayerWeights(hidden, ffn, experts, top_k, types[0], norm, router_f32, gate, up, down, None,
+    return LayerWeights(hidden, ffn, experts, top_k, types[0], norm, router_f32, gate, up, down, router_bias,
                         rms_eps=float(np.float32(eps)), weights_norm=weights_norm, down_type=types[1],
                         router_type=rt.type_id, router_raw=None if rt.type_id == F32 else router_raw,
-                        notes={"source": r.path, "layer": layer})
+                        epsilon_additive=epsilon_additive, weights_epsilon=weights_epsilon,
+                        weights_scale=weights_scale, notes={"source": r.path, "layer": layer})

@@ -512,21 +512,20 @@ static float swiglu(float gate, float up) {
     return (float)(g / (1.0 + exp(-g))) * up;
 }
 
-/* The MoE block of Engine::forward_token (engine.cpp:1602-1776) and the
- * residual add (engine.cpp:813-816, 1822). */
-int fmo_moe_layer(int isa, const fmo_layer *L, const float *x, float *out, uint32_t *ids,
-                  float *weights, float *h_out, float *act_out) {
+/* The expert half of the MoE block for a given routing (engine.cpp:1710-1776)
+ * and the residual add (engine.cpp:813-816, 1822): for each rank i in order,
+ * gate/up of expert ids[i] on h, SwiGLU, down, ffn += weights[i] * down (a
+ * multiply, then an add); out = x + ffn. */
+int fmo_moe_experts(int isa, const fmo_layer *L, const float *x, const float *h, const uint32_t *ids,
+                    const float *weights, float *out, float *act_out) {
     const uint32_t H = L->hidden, F = L->ffn, K = L->top_k;
-    float *h = (float *)malloc(sizeof(float) * H);
     float *ffn = (float *)calloc(H, sizeof(float));
     float *gate = (float *)malloc(sizeof(float) * F);
     float *up = (float *)malloc(sizeof(float) * F);
     float *act = (float *)malloc(sizeof(float) * F);
     float *down = (float *)malloc(sizeof(float) * H);
     int rc = FMO_ERR_INTERNAL;
-    if (!h || !ffn || !gate || !up || !act || !down) goto done;
-    rc = fmo_route(isa, L, x, h, NULL, NULL, ids, weights);
-    if (rc) goto done;
+    if (!ffn || !gate || !up || !act || !down) goto done;
     for (uint32_t i = 0; i < K; ++i) {
         const uint32_t e = ids[i];
         if (e >= L->experts) {
@@ -543,14 +542,26 @@ int fmo_moe_layer(int isa, const fmo_layer *L, const float *x, float *out, uint3
         for (uint32_t j = 0; j < H; ++j) ffn[j] += weights[i] * down[j];
     }
     for (uint32_t j = 0; j < H; ++j) out[j] = x[j] + ffn[j];
-    if (h_out) memcpy(h_out, h, sizeof(float) * H);
+    rc = FMO_OK;
 done:
-    free(h);
     free(ffn);
     free(gate);
     free(up);
     free(act);
     free(down);
+    return rc;
+}
+
+/* The MoE block of Engine::forward_token (engine.cpp:1602-1776) and the
+ * residual add: fmo_route, then fmo_moe_experts. */
+int fmo_moe_layer(int isa, const fmo_layer *L, const float *x, float *out, uint32_t *ids,
+                  float *weights, float *h_out, float *act_out) {
+    float *h = (float *)malloc(sizeof(float) * L->hidden);
+    if (!h) return FMO_ERR_INTERNAL;
+    int rc = fmo_route(isa, L, x, h, NULL, NULL, ids, weights);
+    if (!rc) rc = fmo_moe_experts(isa, L, x, h, ids, weights, out, act_out);
+    if (!rc && h_out) memcpy(h_out, h, sizeof(float) * L->hidden);
+    free(h);
     return rc;
 }
 

@@ -105,6 +105,11 @@ int fmo_route(int isa, const fmo_layer *L, const float *x, float *h, float *logi
 int fmo_moe_layer(int isa, const fmo_layer *L, const float *x, float *out, uint32_t *ids,
                   float *weights, float *h, float *act);
 
+/* The expert half for a given routing (ids, weights in rank order) and the
+ * residual: out = x + sum_i weights[i] * down_i(swiglu(gate_i h, up_i h)). */
+int fmo_moe_experts(int isa, const fmo_layer *L, const float *x, const float *h, const uint32_t *ids,
+                    const float *weights, float *out, float *act);
+
 /* Per-token loop over a batch (the reference has no batched MoE path). */
 int fmo_moe_layer_batch(int isa, const fmo_layer *L, const float *x, float *out,
                         uint32_t *ids, float *weights, uint32_t tokens);

@@ -54,7 +54,7 @@ def oracle() -> ctypes.CDLL:
         lib.fmo_fp16_to_f32.argtypes = [c_uint16]
         for name in ["fmo_dequantize_block", "fmo_dequantize_region", "fmo_gemv", "fmo_gemm", "fmo_rmsnorm",
                      "fmo_softmax", "fmo_topk", "fmo_route", "fmo_moe_layer", "fmo_moe_layer_batch",
-                     "fmo_moe_bucket", "fmo_quant_geometry"]:
+                     "fmo_moe_bucket", "fmo_quant_geometry", "fmo_moe_experts"]:
             getattr(lib, name).restype = c_int
         lib.fmo_dequantize_region.argtypes = [c_uint32, c_void_p, c_void_p, c_uint64]
         lib.fmo_gemv.argtypes = [c_int, c_uint32, c_void_p, c_void_p, c_void_p, c_uint32, c_uint32]
@@ -70,6 +70,8 @@ def oracle() -> ctypes.CDLL:
                                       c_void_p]
         lib.fmo_moe_layer_batch.argtypes = [c_int, POINTER(Layer), c_void_p, c_void_p, c_void_p, c_void_p,
                                             c_uint32]
+        lib.fmo_moe_experts.argtypes = [c_int, POINTER(Layer), c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_void_p]
         lib.fmo_moe_bucket.argtypes = [c_void_p, c_uint32, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p]
         _oracle = lib
     return _oracle
@@ -322,6 +324,21 @@ class HostLayer:
         check(oracle().fmo_moe_layer(isa, ctypes.byref(L), _p(x), _p(out), _p(ids), _p(w), _p(h), _p(act)),
               "fmo_moe_layer")
         return out, ids, w, h, act
+
+    def experts_for(self, x: np.ndarray, h: np.ndarray, ids, weights, isa: int = ISA_AVX2) -> np.ndarray:
+        """The expert half and the residual for a given routing (ids and
+        weights in rank order): x + sum_i w_i * down_i(SwiGLU(gate_i h, up_i h))."""
+        x = np.ascontiguousarray(x, np.float32)
+        h = np.ascontiguousarray(h, np.float32)
+        ids = np.ascontiguousarray(ids, np.uint32)
+        weights = np.ascontiguousarray(weights, np.float32)
+        if ids.size != self.top_k or weights.size != self.top_k:
+            raise ValueError("ids and weights must hold top_k entries")
+        out = np.empty(self.hidden, np.float32)
+        L = self.struct()
+        check(oracle().fmo_moe_experts(isa, ctypes.byref(L), _p(x), _p(h), _p(ids), _p(weights), _p(out), None),
+              "fmo_moe_experts")
+        return out
 
     def forward_batch(self, x: np.ndarray, isa: int = ISA_AVX2, threads: int = 1):
         """Every row of x as its own token. `threads` > 1 splits the rows over

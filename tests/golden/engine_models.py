@@ -1,4 +1,4 @@
-"""Seeded freemoe-tiny-v1 MoE checkpoints for pinning the oracle against the
+"""Seeded MoE checkpoints (native freemoe-tiny-v1 and llama-family) for pinning the oracle against the
 reference's whole fm::Engine, and the oracle's reproduction of that engine.
 
 Every checkpoint's attention output projections are zero, so the attention
@@ -10,6 +10,16 @@ experts (gate/up, SwiGLU, down) -> rank-order combine -> residual, per layer,
 then RMSNorm (output_norm) and the F32 head (engine.cpp:1825-1827), then
 greedy argmax (lowest id on ties) until EOS. The goldens hold the engine's
 prompt logits (bit patterns), its routing record and its greedy ids.
+
+LLAMA_CASES are llama-family (Mixtral vendor layout) checkpoints, read by the
+reference's llama adapter, that carry the routing options the native adapter
+fixes: an F32 ``ffn_gate_inp.bias`` added to the router logits before the
+softmax (gguf.cpp:1535, engine.cpp:1611-1616; a Zipf(1.2) bias as in the
+fine-grained workload), ``expert_weights_norm`` on, off or absent (gguf.cpp:
+1445) and ``expert_weights_scale`` (1446). Their attention output projections
+are zero as well. Their prompts are tokenised by the engine's SentencePiece
+tokenizer, which is not on the MoE path: the oracle takes the engine's input
+ids from the goldens and reproduces everything after the embedding lookup.
 """
 from __future__ import annotations
 
@@ -40,6 +50,22 @@ CASES = {
     "q4_k_router_q8_0_top4": (512, 256, 8, 4, 2, 8, wl.Q4_K, wl.Q8_0, 14),
 }
 
+LLAMA_VOCAB, LLAMA_BOS, LLAMA_EOS = 300, 1, 2
+
+LLAMA_CASES = {
+    # name: (hidden, ffn, experts, top_k, layers, heads, expert type, router type, seed,
+    #        router bias Zipf exponent or None, expert_weights_norm (None: key absent), expert_weights_scale,
+    #        architecture)
+    "llama_zipf_bias_q4_k_top4": (256, 256, 16, 4, 2, 4, wl.Q4_K, wl.F32, 21, 1.2, True, None, "llama"),
+    "llama_unnormalised_scale_q8_0": (128, 128, 8, 2, 2, 4, wl.Q8_0, wl.Q4_0, 22, None, False, 2.5, "llama"),
+    "llama_bias_norm_scale_q4_0": (256, 128, 8, 2, 1, 4, wl.Q4_0, wl.Q8_0, 23, 1.2, True, 0.75, "llama"),
+    "llama_keys_absent_q8_0": (128, 64, 4, 2, 1, 4, wl.Q8_0, wl.F32, 24, None, None, None, "llama"),
+    # the llama block under deepseek41, whose renormalisation adds 1e-20 to
+    # the sum of the selected weights instead of clamping it (gguf.cpp:1943-1947)
+    "deepseek41_additive_epsilon_q4_0": (128, 128, 8, 2, 1, 4, wl.Q4_0, wl.F32, 25, 1.2, True, None,
+                                         "deepseek41"),
+}
+
 PROMPT_LENGTHS = (1, 4, 9, 23)
 GENERATE = 6
 
@@ -55,9 +81,13 @@ class Model:
     layers: list              # LayerWeights per layer
     rms_eps: float
     file: gguf.GGUFFile
+    eos: int = EOS
+    family: str = "freemoe-tiny"
 
 
 def build(name: str) -> Model:
+    if name in LLAMA_CASES:
+        return build_llama(name)
     H, F, E, K, nl, heads, et, rt, seed = CASES[name]
     rng = np.random.default_rng(seed)
     embd = rng.standard_normal((VOCAB, H), dtype=np.float32)
@@ -81,6 +111,46 @@ def build(name: str) -> Model:
     return Model(name, H, K, embd, out_norm, head, layers, float(np.float32(1e-5)), f)
 
 
+def build_llama(name: str) -> Model:
+    """A llama-family Mixtral-layout checkpoint of LLAMA_CASES, every tensor
+    written; the MoE blocks are workloads.make_layer layers (router bias:
+    -s ln(rank) over a seeded permutation of the experts' ranks), the routing
+    options set as the case says, on each layer's LayerWeights too."""
+    H, F, E, K, nl, heads, et, rt, seed, zipf, wnorm, wscale, arch = LLAMA_CASES[name]
+    V = LLAMA_VOCAB
+    rng = np.random.default_rng(seed)
+    f32 = lambda a: np.ascontiguousarray(a, np.float32).view(np.uint8)
+    embd = rng.standard_normal((V, H), dtype=np.float32)
+    head = (rng.standard_normal((V, H)) / np.sqrt(H)).astype(np.float32)
+    out_norm = (1.0 + rng.standard_normal(H) * 0.02).astype(np.float32)
+    data = {"token_embd.weight": f32(embd), "output_norm.weight": f32(out_norm), "output.weight": f32(head)}
+    layers = []
+    for i in range(nl):
+        lw = wl.make_layer(H, F, E, K, et, seed * 100 + i, zipf_s=zipf, router_type=rt)
+        lw.weights_norm = bool(wnorm)
+        lw.weights_scale = 1.0 if wscale is None else float(np.float32(wscale))
+        if arch == "deepseek41":
+            lw.epsilon_additive, lw.weights_epsilon = True, 1e-20
+        layers.append(lw)
+        p = f"blk.{i}."
+        data[p + "attn_norm.weight"] = f32(1.0 + rng.standard_normal(H) * 0.02)
+        for nm in ("attn_q", "attn_k", "attn_v"):
+            data[p + nm + ".weight"] = f32(rng.standard_normal((H, H)) * 0.02)
+        data[p + "attn_output.weight"] = f32(np.zeros((H, H)))
+        data[p + "ffn_norm.weight"] = f32(lw.norm_weight)
+        data[p + "ffn_gate_inp.weight"] = lw.router_bytes
+        if zipf is not None:
+            data[p + "ffn_gate_inp.bias"] = f32(lw.router_bias)
+        data[p + "ffn_gate_exps.weight"] = gguf.stacked(lw.gate)
+        data[p + "ffn_up_exps.weight"] = gguf.stacked(lw.up)
+        data[p + "ffn_down_exps.weight"] = gguf.stacked(lw.down)
+    f = gguf.mixtral_llama(hidden=H, ffn=F, layers=nl, heads=heads, kv_heads=heads, experts=E, top_k=K, vocab=V,
+                           expert_type=et, router_type=rt, data=data, router_bias=zipf is not None,
+                           weights_norm=wnorm, weights_scale=wscale, arch=arch)
+    return Model(name, H, K, embd, out_norm, head, layers, float(np.float32(1e-5)), f, eos=LLAMA_EOS,
+                 family="llama")
+
+
 def write(m: Model, path: Path) -> str:
     """Writes the checkpoint; returns its SHA-256."""
     m.file.write(path)
@@ -88,27 +158,45 @@ def write(m: Model, path: Path) -> str:
 
 
 def prompts(name: str) -> list[bytes]:
+    """Seeded prompts: random bytes (byte tokenizer), or random printable
+    ASCII for the llama-family cases (SentencePiece, byte fallback)."""
+    if name in LLAMA_CASES:
+        rng = np.random.default_rng(LLAMA_CASES[name][8] + 7)
+        return [bytes(rng.integers(33, 127, n, dtype=np.uint8)) for n in PROMPT_LENGTHS]
     rng = np.random.default_rng(CASES[name][-1] + 7)
     return [bytes(rng.integers(0, 256, n, dtype=np.uint8)) for n in PROMPT_LENGTHS]
 
 
-def oracle_run_prompt(m: Model, prompt: bytes, generate: int):
+ALL_CASES = [*CASES, *LLAMA_CASES]
+
+
+def oracle_run_prompt(m: Model, prompt: bytes, generate: int, input_ids=None, layer_fn=None):
     """The oracle's reproduction of Engine::run_prompt on a checkpoint of
-    build(): (input ids, prompt logits, generated ids, routing rows)."""
+    build(): (input ids, prompt logits, generated ids, routing rows).
+    input_ids: the tokenised prompt (default: BOS then the bytes, the byte
+    tokenizer; llama-family cases pass the engine's). layer_fn(layer_index,
+    x) -> (out, ids) replaces the oracle's MoE layer (the GPU's, or a planted
+    variant)."""
     hls = [fo.host_layer(lw) for lw in m.layers]
     head_raw = m.head.view(np.uint8)
+    vocab = m.head.shape[0]
     routing = []
 
     def forward(tok: int, pos: int) -> np.ndarray:
         x = m.embd[tok].copy()
         for li, hl in enumerate(hls):
-            out, ids, _, _, _ = hl.forward(x)
-            routing.append([pos, li, *ids.tolist()])
+            if layer_fn is None:
+                out, ids, _, _, _ = hl.forward(x)
+            else:
+                out, ids = layer_fn(li, x)
+            routing.append([pos, li, *np.asarray(ids).tolist()])
             x = out
         hn = fo.rmsnorm(x, m.output_norm, m.rms_eps)
-        return fo.gemv(fo.TYPE_F32, head_raw, hn, VOCAB, m.hidden)
+        return fo.gemv(fo.TYPE_F32, head_raw, hn, vocab, m.hidden)
 
-    input_ids = [BOS] + list(prompt)
+    if input_ids is None:
+        input_ids = [BOS] + list(prompt)
+    input_ids = [int(t) for t in input_ids]
     logits = None
     for pos, tok in enumerate(input_ids):
         logits = forward(tok, pos)
@@ -118,7 +206,7 @@ def oracle_run_prompt(m: Model, prompt: bytes, generate: int):
     for _ in range(generate):
         tok = int(np.argmax(logits))  # first maximum: the lowest id wins ties
         generated.append(tok)
-        if tok == EOS:
+        if tok == m.eos:
             break
         logits = forward(tok, pos)
         pos += 1

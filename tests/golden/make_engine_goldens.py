@@ -49,7 +49,7 @@ def main() -> None:
         raise SystemExit("oracle/_ref/libfmref.so is not built (make -C oracle ref, with the FreeMoe tree)")
     data = {}
     with tempfile.TemporaryDirectory() as d:
-        for name in em.CASES:
+        for name in em.ALL_CASES:
             data.update(engine_outputs(name, Path(d) / f"{name}.gguf"))
     np.savez_compressed(OUT, **data)
     print(f"wrote {OUT} ({len(data)} arrays)")

@@ -127,3 +127,89 @@ def test_native_layout_at_mixtral_shape_accepted_by_reference_adapter(tmp_path):
     m = fo.ref_manifest(path)
     assert (m["experts"], m["top_k"], m["hidden"], m["records"]) == (E, K, H, E)
     assert m["slot_bytes"] == 99_090_432
+
+
+REF_FIXTURES = ["moe-fm", "quant-moe-q4_0", "quant-moe-q8_0", "quant-moe-q4_k", "quant-moe-q6_k",
+                "quant-expert-fused", "quant-expert-separate"]
+FIXTURE_DIR = Path(__file__).resolve().parent / "golden" / "freemoe_reference"
+
+
+@pytest.mark.parametrize("name", REF_FIXTURES)
+def test_reference_fixtures_load(name):
+    """FreeMoe's own conformance checkpoints (Q6_K experts and router, Q4_K
+    gate/up with Q6_K down as separate or fused gate_up tensors) read into
+    LayerWeights with the types and routing options their adapters give."""
+    r = gguf.read(FIXTURE_DIR / f"{name}.gguf")
+    lw = gguf.moe_layer(r, 0)
+    want = {
+        "moe-fm": (gguf.F32, gguf.F32, gguf.F32, True),
+        "quant-moe-q4_0": (gguf.Q4_0, gguf.Q4_0, gguf.Q4_0, True),
+        "quant-moe-q8_0": (gguf.Q8_0, gguf.Q8_0, gguf.Q8_0, True),
+        "quant-moe-q4_k": (gguf.Q4_K, gguf.Q4_K, gguf.Q4_K, True),
+        "quant-moe-q6_k": (gguf.Q6_K, gguf.Q6_K, gguf.Q6_K, True),
+        # qwen3moe files without the key: renormalisation off (gguf.cpp:1445)
+        "quant-expert-fused": (gguf.Q4_K, gguf.Q6_K, gguf.F32, False),
+        "quant-expert-separate": (gguf.Q4_K, gguf.Q6_K, gguf.F32, False),
+    }[name]
+    assert (lw.gate_type, lw.down_type, lw.router_type, lw.weights_norm) == want
+    assert lw.router_bias is None and lw.weights_scale == 1.0
+
+
+@needs_ref
+@pytest.mark.parametrize("name", REF_FIXTURES)
+def test_reference_fixture_slices_match_the_adapter(name):
+    """Every expert's gate / up / down slice sits at the offset, size and type
+    of the reference manifest's extents (the fused file's gate and up halves
+    included)."""
+    path = FIXTURE_DIR / f"{name}.gguf"
+    m = fo.ref_manifest(path)
+    r = gguf.read(path)
+    assert m["records"] > 0
+    for i, (l, e) in enumerate(m["who"]):
+        sl = r.expert_slices(int(l), int(e))
+        for j, key in enumerate(("gate", "up", "down")):
+            arr, t = sl[key]
+            off = arr.ctypes.data - r.data.ctypes.data
+            assert (off, arr.nbytes, t) == tuple(int(v) for v in m["extents"][i, j]), (name, l, e, key)
+
+
+def _llama_with(tmp_path, extra_tensor=None, arch="llama", **kw):
+    H, F, E, K = 64, 64, 4, 2
+    g = gguf.mixtral_llama(hidden=H, ffn=F, layers=1, heads=4, kv_heads=4, experts=E, top_k=K, vocab=300,
+                           expert_type=gguf.Q8_0, arch=arch, **kw)
+    if extra_tensor is not None:
+        g.add_tensor(f"blk.0.{extra_tensor}", [E], gguf.F32)
+    path = tmp_path / "x.gguf"
+    g.write(path, sparse=True)
+    return gguf.read(path)
+
+
+@pytest.mark.parametrize("extra", ["ffn_exp_probs_b.bias", "ffn_gate_exps.bias", "ffn_gate_inp_shexp.weight"])
+def test_reader_refuses_blocks_it_does_not_run(tmp_path, extra):
+    with pytest.raises(NotImplementedError):
+        gguf.moe_layer(_llama_with(tmp_path, extra), 0)
+
+
+@pytest.mark.parametrize("arch", ["gemma2", "gpt-oss", "glm4-moe", "smallthinker"])
+def test_reader_refuses_other_block_families(tmp_path, arch):
+    with pytest.raises(NotImplementedError):
+        gguf.moe_layer(_llama_with(tmp_path, arch=arch), 0)
+
+
+def test_reader_routing_options(tmp_path):
+    r = _llama_with(tmp_path, router_bias=True, weights_norm=False, weights_scale=2.5)
+    lw = gguf.moe_layer(r, 0)
+    assert lw.router_bias is not None and lw.router_bias.shape == (4,)
+    assert (lw.weights_norm, lw.weights_scale, lw.epsilon_additive) == (False, 2.5, False)
+    # families whose renormalisation the architecture fixes (gguf.cpp:2046-2058)
+    assert gguf.moe_layer(_llama_with(tmp_path, arch="dbrx", weights_norm=False), 0).weights_norm
+    assert not gguf.moe_layer(_llama_with(tmp_path, arch="deepseek", weights_norm=True), 0).weights_norm
+    assert gguf.moe_layer(_llama_with(tmp_path, arch="maple", weights_scale=3.0), 0).weights_scale == 1.0
+    ds = gguf.moe_layer(_llama_with(tmp_path, arch="deepseek41"), 0)
+    assert (ds.epsilon_additive, ds.weights_epsilon) == (True, 1e-20)
+
+
+def test_reader_refuses_unknown_block_types():
+    t = gguf.Tensor("blk.0.x", [32, 4], 99, None)
+    with pytest.raises(ValueError, match="block type 99"):
+        t.nbytes()

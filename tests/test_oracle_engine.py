@@ -2,13 +2,17 @@
 
 tests/golden/engine_goldens.npz holds what the compiled engine
 (oracle/_ref/libfmref.so, built from the FreeMoe sources) produced on the
-seeded freemoe-tiny-v1 checkpoints of tests/golden/engine_models.py, whose
-attention output projections are zero. The oracle's chain (RMSNorm, router,
-softmax, top-k, weights, experts, SwiGLU, combine, residual, final norm, F32
-head, greedy) must reproduce the engine's prompt logits bit for bit, its
-routing record and its greedy ids. Planted mistakes in the oracle's inputs
-(gate and up swapped, the weights left unnormalised, the additive epsilon)
-must break the match, so the goldens discriminate those functions.
+seeded checkpoints of tests/golden/engine_models.py (native freemoe-tiny-v1,
+and llama-family files carrying a router-logit bias, expert_weights_norm on,
+off or absent and expert_weights_scale), whose attention output projections
+are zero. The oracle's chain (RMSNorm, router, logit bias, softmax, top-k,
+weights, experts, SwiGLU, combine, residual, final norm, F32 head, greedy)
+must reproduce the engine's prompt logits bit for bit, its routing record and
+its greedy ids. Planted mistakes in the oracle (gate and up swapped, the
+weights left unnormalised, the additive epsilon; the logit bias added after
+the softmax, used only to select experts, or dropped; the weight scale
+dropped; the renormalisation switched) must break the match, so the goldens
+discriminate those functions and branches.
 """
 import copy
 import tempfile
@@ -33,20 +37,21 @@ def sha_of(name: str) -> str:
         return em.write(em.build(name), Path(d) / "m.gguf")
 
 
-def matches(m, name, goldens, i, prompt):
-    ids, logits, gen, routing = em.oracle_run_prompt(m, prompt, em.GENERATE)
+def matches(m, name, goldens, i, prompt, layer_fn=None):
     g = lambda k: goldens[f"{name}/{i}/{k}"]
+    given = g("input_ids") if m.family == "llama" else None
+    ids, logits, gen, routing = em.oracle_run_prompt(m, prompt, em.GENERATE, input_ids=given, layer_fn=layer_fn)
     return (np.array_equal(ids, g("input_ids")), np.array_equal(logits.view(np.uint32), g("logits").view(np.uint32)),
             np.array_equal(gen, g("generated")), np.array_equal(routing, g("routing")))
 
 
-@pytest.mark.parametrize("name", list(em.CASES))
+@pytest.mark.parametrize("name", em.ALL_CASES)
 def test_checkpoint_is_the_pinned_one(goldens, name):
     """The writer regenerates the exact checkpoint the goldens were taken on."""
     assert bytes(goldens[f"{name}/sha256"]).hex() == sha_of(name)
 
 
-@pytest.mark.parametrize("name", list(em.CASES))
+@pytest.mark.parametrize("name", em.ALL_CASES)
 def test_oracle_reproduces_the_compiled_engine(goldens, name):
     m = em.build(name)
     for i, p in enumerate(em.prompts(name)):
@@ -57,7 +62,7 @@ def test_oracle_reproduces_the_compiled_engine(goldens, name):
 def test_goldens_cover_ties_between_ranks_and_eos_free_runs(goldens):
     """Every case generates its full GENERATE tokens and routes at least 8
     token-layer pairs per prompt."""
-    for name in em.CASES:
+    for name in em.ALL_CASES:
         for i in range(len(em.PROMPT_LENGTHS)):
             assert len(goldens[f"{name}/{i}/generated"]) == em.GENERATE
             assert goldens[f"{name}/{i}/routing"].shape[0] >= 8
@@ -86,7 +91,7 @@ def test_planted_oracle_mistakes_break_the_match(goldens, mistake):
 
 
 @pytest.mark.skipif(not fo.ref_available(), reason="oracle/_ref not built (needs the FreeMoe tree at build time)")
-@pytest.mark.parametrize("name", list(em.CASES))
+@pytest.mark.parametrize("name", em.ALL_CASES)
 def test_live_engine_matches_goldens(goldens, name):
     """The compiled engine, run now, gives the committed goldens."""
     with tempfile.TemporaryDirectory() as d:
@@ -103,3 +108,129 @@ def test_live_engine_matches_goldens(goldens, name):
                 assert np.array_equal(routing, goldens[f"{name}/{i}/routing"])
         finally:
             eng.close()
+
+
+# ------------------------------------------------ the llama routing options --
+
+def composed_route(lw, x, bias_stage="logits", scale=True, norm=None):
+    """The routing of engine.cpp:1603-1702 composed from the oracle's
+    primitives (RMSNorm, router product, softmax, top-k), with the weight
+    arithmetic spelt out in float32 / double as the engine does it. The
+    keywords plant mistakes: bias_stage "logits" (the reference: added before
+    the softmax), "probs" (added to the probabilities, which then give both
+    selection and weights), "selection" (added after the softmax to choose the
+    experts only, the ffn_exp_probs_b semantics) or "none"; scale=False drops
+    expert_weights_scale; norm overrides expert_weights_norm."""
+    h = fo.rmsnorm(x, lw.norm_weight, lw.rms_eps, lw.norm_bias)
+    logits = fo.gemv(lw.router_type, lw.router_bytes, h, lw.experts, lw.hidden)
+    b = lw.router_bias
+    if b is not None and bias_stage == "logits":
+        logits = (logits + b).astype(np.float32)
+    probs = fo.softmax(logits)
+    if b is not None and bias_stage == "probs":
+        probs = (probs + b).astype(np.float32)
+    selection = probs
+    if b is not None and bias_stage == "selection":
+        selection = (probs + b).astype(np.float32)
+    ids = fo.topk(selection, lw.top_k)
+    w = [np.float32(probs[e]) for e in ids]
+    total = np.float32(0.0)
+    for v in w:
+        total = np.float32(total + v)
+    if (lw.weights_norm if norm is None else norm):
+        den = max(float(total), lw.weights_epsilon)
+        w = [np.float32(float(v) / den) for v in w]
+    if scale:
+        w = [np.float32(float(v) * lw.weights_scale) for v in w]
+    return h, ids, np.array(w, np.float32)
+
+
+def composed_layer_fn(m, **plant):
+    hls = [fo.host_layer(lw) for lw in m.layers]
+
+    def fn(li, x):
+        h, ids, w = composed_route(m.layers[li], x, **plant)
+        return hls[li].experts_for(x, h, ids, w), ids
+    return fn
+
+
+@pytest.mark.parametrize("name", list(em.LLAMA_CASES))
+def test_composed_routing_reproduces_the_engine(goldens, name):
+    """The routing spelt out step by step (the planted tests' baseline) gives
+    the engine's results on every llama-family case."""
+    m = em.build(name)
+    fn = composed_layer_fn(m)
+    for i, p in enumerate(em.prompts(name)):
+        assert matches(m, name, goldens, i, p, fn) == (True, True, True, True), (name, i)
+
+
+def test_llama_cases_cover_the_options():
+    """Bias present and absent, renormalisation on, off and key-absent (off),
+    scale 1 and not 1, read back by freemoe_amd.gguf.moe_layer as built."""
+    import tempfile
+    from freemoe_amd import gguf
+    seen = set()
+    for name in em.LLAMA_CASES:
+        m = em.build(name)
+        with tempfile.TemporaryDirectory() as d:
+            em.write(m, Path(d) / "m.gguf")
+            r = gguf.read(Path(d) / "m.gguf")
+            for li, lw in enumerate(m.layers):
+                got = gguf.moe_layer(r, li)
+                assert got.weights_norm == lw.weights_norm and got.weights_scale == lw.weights_scale
+                assert (got.epsilon_additive, got.weights_epsilon) == (lw.epsilon_additive, lw.weights_epsilon)
+                assert (got.router_bias is None) == (lw.router_bias is None)
+                if lw.router_bias is not None:
+                    assert np.array_equal(got.router_bias, lw.router_bias)
+        wnorm = em.LLAMA_CASES[name][10]
+        seen.add(("bias", m.layers[0].router_bias is not None))
+        seen.add(("norm", wnorm))
+        seen.add(("scale", m.layers[0].weights_scale != 1.0))
+    assert seen >= {("bias", True), ("bias", False), ("norm", True), ("norm", False), ("norm", None),
+                    ("scale", True), ("scale", False)}
+
+
+PLANTED_ROUTING = {
+    "bias_added_after_softmax": ("llama_zipf_bias_q4_k_top4", dict(bias_stage="probs")),
+    "bias_steers_selection_only": ("llama_zipf_bias_q4_k_top4", dict(bias_stage="selection")),
+    "bias_dropped": ("llama_bias_norm_scale_q4_0", dict(bias_stage="none")),
+    "scale_dropped": ("llama_unnormalised_scale_q8_0", dict(scale=False)),
+    "scale_dropped_with_norm": ("llama_bias_norm_scale_q4_0", dict(scale=False)),
+    "renormalised_when_off": ("llama_unnormalised_scale_q8_0", dict(norm=True)),
+    "renormalised_when_key_absent": ("llama_keys_absent_q8_0", dict(norm=True)),
+    "not_renormalised_when_on": ("llama_zipf_bias_q4_k_top4", dict(norm=False)),
+}
+
+
+@pytest.mark.parametrize("mistake", list(PLANTED_ROUTING))
+def test_planted_routing_mistakes_break_the_match(goldens, mistake):
+    name, plant = PLANTED_ROUTING[mistake]
+    m = em.build(name)
+    fn = composed_layer_fn(m, **plant)
+    broken = [not all(matches(m, name, goldens, i, p, fn)) for i, p in enumerate(em.prompts(name))]
+    assert any(broken), f"{mistake}: every prompt still matches the engine"
+
+
+def test_additive_epsilon_equals_the_clamp_under_softmax():
+    """deepseek41's denominator, double(total) + 1e-20, and the clamp,
+    max(double(total), 2^-14), give the same double whenever total >= 2^-13:
+    there half an ulp of the double is at least 2^-66 (1.36e-20) > 1e-20, so
+    the add rounds back to total. Softmax top-k weights sum to at least
+    k / experts, above 2^-13 for fewer than 8192 k experts, so on this path
+    the two branches give the same bits; the deepseek41 case pins the branch
+    against the engine, and this checks the arithmetic fact on float32 values
+    from the boundary up. Between 2^-14 and 2^-13 the add moves the double by
+    one ulp, and below 2^-14 the clamp differs outright: only a gating other
+    than softmax gets there."""
+    eps_clamp = 6.103515625e-5
+    assert eps_clamp == 2.0 ** -14
+    lo = np.float32(2.0 ** -13)
+    vals = [lo, np.nextafter(lo, np.float32(1)), np.float32(1 / 128), np.float32(0.5), np.float32(1.0)]
+    vals += list(np.random.default_rng(3).uniform(2.0 ** -13, 1.0, 1000).astype(np.float32))
+    for v in vals:
+        t = float(v)
+        assert t + 1e-20 == max(t, eps_clamp) == t
+    t = 2.0 ** -14
+    assert t + 1e-20 == t + 2.0 ** -66 != max(t, eps_clamp)
+    t = float(np.float32(1e-6))
+    assert t + 1e-20 != max(t, eps_clamp)
