@@ -98,8 +98,9 @@ int validate_layer(const fmx_moe_layer *L) {
     // the routing kernels read x, the router rows and the norm gains as float4
     if (!aligned16(L->router) || (L->norm_weight && !aligned16(L->norm_weight))) return FMX_ERR_INVALID_ARGUMENT;
     if (L->router_type != FMX_TYPE_F32 && L->router_type != FMX_TYPE_Q4_0 && L->router_type != FMX_TYPE_Q8_0 &&
-        L->router_type != FMX_TYPE_Q4_K)
+        L->router_type != FMX_TYPE_Q4_K && L->router_type != FMX_TYPE_Q6_K)
         return FMX_ERR_UNSUPPORTED_QUANTISATION;
+    if (L->router_type == FMX_TYPE_Q6_K && L->hidden % 256) return FMX_ERR_SHAPE_MISMATCH;
     return FMX_OK;
 }
 
@@ -385,12 +386,13 @@ int fmx_moe_route(const fmx_moe_layer *L, const float *x, uint32_t tokens, float
     float *lg = logits ? logits : reinterpret_cast<float *>(base + ws.logits);
     RouteArgs ra;
     if (int rc = prepare_route_args(L, &ra)) return rc;
+    const bool per_token = !h && ra.router_type != FMX_TYPE_F32;
+    // a block-type router without a caller's h runs one token at a time
+    // through the workspace's h: checked before anything is launched
+    if (per_token && workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
     FMX_LAUNCH_CHECK();
-    if (h || ra.router_type == FMX_TYPE_F32) return launch_route(ra, x, tokens, h, lg, ids, weights, status, s);
-    // a block-type router needs h: one token at a time through the
-    // workspace's h
-    if (workspace_bytes < ws.total) return FMX_ERR_INVALID_ARGUMENT;
+    if (!per_token) return launch_route(ra, x, tokens, h, lg, ids, weights, status, s);
     float *hw = reinterpret_cast<float *>(base + ws.h);
     const uint64_t H = L->hidden, E = L->experts, K = L->top_k;
     for (uint32_t t = 0; t < tokens; ++t)

@@ -713,6 +713,19 @@ __global__ __launch_bounds__(kThreads) void router_quant_kernel(RouteArgs a, con
     if (l == 0 && r < E) logits[static_cast<uint64_t>(t) * E + r] = a.router_bias ? v + a.router_bias[r] : v;
 }
 
+// Router logits of a Q6_K router (raw 210-byte blocks, as FreeMoe stores
+// them): one 16-lane group per router row runs the Q6_K row dot of fmx_matvec
+// (the reference's gemv_quant order, bit for bit), then the logit bias
+// (engine.cpp:1611-1616). grid: (tokens, ceil(experts / 16)).
+__global__ __launch_bounds__(kThreads) void router_q6k_kernel(RouteArgs a, const float *__restrict__ h,
+                                                              float *__restrict__ logits) {
+    const uint32_t tid = threadIdx.x, c = tid & 15;
+    const uint32_t t = blockIdx.x, r = blockIdx.y * (kThreads / 16) + (tid >> 4), E = a.experts;
+    const float v = RowDot16<FMX_TYPE_Q6_K>::dot(a.router_packed, r < E ? r : E - 1,
+                                                 h + static_cast<uint64_t>(t) * a.hidden, a.hidden, c);
+    if (c == 0 && r < E) logits[static_cast<uint64_t>(t) * E + r] = a.router_bias ? v + a.router_bias[r] : v;
+}
+
 // The expert of rank `rank` for an expert kernel: from the routing computed
 // in this wavefront when `logits` is given (the first workgroup also stores
 // ids, weights and the error flag for the kernels after it), else from ids.
@@ -1128,6 +1141,11 @@ int launch_router_quant(const RouteArgs &a, const float *h, uint32_t tokens, flo
     case FMX_TYPE_Q4_0: return launch_router_quant_t<Q40>(a, h, tokens, logits, s);
     case FMX_TYPE_Q8_0: return launch_router_quant_t<Q80>(a, h, tokens, logits, s);
     case FMX_TYPE_Q4_K: return launch_router_quant_t<Q4K>(a, h, tokens, logits, s);
+    case FMX_TYPE_Q6_K:
+        hipLaunchKernelGGL(router_q6k_kernel, dim3(tokens, div_up(a.experts, kThreads / 16)), dim3(kThreads), 0, s, a,
+                           h, logits);
+        FMX_LAUNCH_CHECK();
+        return FMX_OK;
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
 }
@@ -1225,6 +1243,11 @@ int prepare_route_args(const fmx_moe_layer *L, RouteArgs *out) {
                                                     : tile_blocks_for<Q4K>(a.rg.blocks, kBudget);
         break;
     }
+    case FMX_TYPE_Q6_K:
+        // raw rows (the packed layout of Q6_K is the raw one)
+        if (L->hidden % 256) return FMX_ERR_SHAPE_MISMATCH;
+        a.router_packed = L->router;
+        break;
     default: return FMX_ERR_UNSUPPORTED_QUANTISATION;
     }
     a.router_bias = L->router_bias;

@@ -1,6 +1,7 @@
 // hip_backend.cpp — fm::Backend on MI355X through libfmx (see hip_backend.hpp).
 #include "hip_backend.hpp"
 
+#include "fm/kernels.hpp"
 #include "fmx.h"
 
 #include <cstring>
@@ -142,6 +143,13 @@ std::vector<HipBackend *> g_backends;
 
 HipBackend::HipBackend(BackendConfig config, TraceWriter *trace)
     : Backend(std::move(config), trace), state_(std::make_shared<State>()) {
+    // The device kernels reproduce the summation order KernelIsa::Auto
+    // resolves to on an AVX2+FMA host (kernels.cpp:147-174, 639-771); the
+    // scalar and AVX-512 orders exist only on the CPU backend, so asking for
+    // them here is refused rather than answered in another order.
+    if (config_.kernel_isa != KernelIsa::Auto && config_.kernel_isa != KernelIsa::Avx2Fma)
+        fail(ErrorCode::INVALID_ARGUMENT, std::string("hip-gfx950 computes the avx2_fma order; kernel ISA '") +
+                                              kernel_isa_name(config_.kernel_isa) + "' runs on the CPU backend");
     fmx_device_info fi;
     state_->have_device = fmx_device_info_get(0, &fi) == FMX_OK;
     std::lock_guard<std::mutex> lock(g_backends_mutex);
@@ -370,17 +378,33 @@ void HipBackend::gemm_quant(uint32_t type_id, const void *weights, const float *
     record_operation({op_name, name(), w_bytes + x_bytes, y_bytes});
 }
 
-void HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, uint32_t *ids, float *weights) {
+bool HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, uint32_t *ids, float *weights) {
     if (fault_ == BackendFault::DeviceLoss) fail(ErrorCode::DEVICE_LOSS, "injected device loss");
     const uint32_t H = L.hidden, F = L.ffn, E = L.experts, K = L.top_k;
     if (!x || !out || !ids || !weights || !L.router || H == 0 || F == 0 || E == 0 || K == 0 || K > E ||
         L.expert_payloads.size() != E)
         fail(ErrorCode::INVALID_ARGUMENT, "invalid MoE layer arguments");
-    if (L.up_type != L.gate_type) fail(ErrorCode::UNSUPPORTED_QUANTISATION, "gate and up of different types");
+    // a layer the fused kernels do not take is declined (false): the engine
+    // then runs its own per-expert loop, whose projections still come here
+    if (L.up_type != L.gate_type) return false;
     const uint64_t gate_bytes = raw_bytes(L.gate_type, F, H), down_bytes = raw_bytes(L.down_type, H, F);
     const uint64_t router_bytes = raw_bytes(L.router_type, E, H);
-    if (gate_bytes == 0 || down_bytes == 0 || router_bytes == 0)
-        fail(ErrorCode::SHAPE_MISMATCH, "projection is not a whole number of blocks");
+    if (gate_bytes == 0 || down_bytes == 0 || router_bytes == 0) return false;
+    {
+        // the library's own layer checks, on stand-in addresses
+        alignas(16) static const uint64_t probe[4] = {};
+        fmx_moe_layer d{};
+        d.hidden = H;
+        d.ffn = F;
+        d.experts = E;
+        d.top_k = K;
+        d.router_type = L.router_type;
+        d.router = probe;
+        d.gate_type = d.up_type = L.gate_type;
+        d.down_type = L.down_type;
+        d.gate = d.up = d.down = reinterpret_cast<const void *const *>(probe);
+        if (fmx_moe_workspace_bytes(&d, 1) == 0) return false;
+    }
     const std::string l = std::to_string(L.layer);
 
     std::lock_guard<std::mutex> lock(state_->mutex);
@@ -485,6 +509,7 @@ void HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, ui
 
     // the reference's operation log for this block (engine.cpp:1603-1776)
     record_operation({"router.L" + l, name(), router_bytes + H * 4ull, E * 4ull});
+    if (L.router_bias) record_control("router_logit_bias.L" + l, E * 4ull, 0, name());
     record_control("router_gating.L" + l, E * 4ull, E * 4ull, name());
     record_control("router_topk.L" + l, E * 4ull, K * 4ull, name());
     for (uint32_t i = 0; i < K; ++i) {
@@ -495,6 +520,7 @@ void HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, ui
         record_operation({"expert_down" + ex, name(), down_bytes + F * 4ull, H * 4ull});
     }
     record_control("expert_combine.L" + l, K * H * 4ull, H * 4ull, name());
+    return true;
 }
 
 void HipBackend::inject_fault(BackendFault fault) {

@@ -20,6 +20,7 @@
 #pragma once
 
 #include "fm/backend.hpp"
+#include "moe_layer_view.hpp"
 
 #include <cstdint>
 #include <map>
@@ -30,27 +31,6 @@
 #include <vector>
 
 namespace fm {
-
-// One routed MoE layer for HipBackend::moe_layer (the block of
-// engine.cpp:1602-1776), described by host pointers as the engine holds them:
-// weights inside this backend's buffers (the fixed-weight buffer, the expert
-// slots); the norm gains may also be ordinary host memory (FreeMoe decodes
-// block-type norm vectors into host vectors, engine.cpp:223-266).
-struct MoeLayerView {
-    uint32_t layer = 0;
-    uint32_t hidden = 0, ffn = 0, experts = 0, top_k = 0;
-    const float *norm_weight = nullptr; // [hidden]
-    double rms_eps = 1e-5, norm_bias = 0.0;
-    uint32_t router_type = 0;
-    const void *router = nullptr;       // [experts x hidden] raw rows
-    const float *router_bias = nullptr; // [experts] host, or nullptr
-    bool weights_norm = false, epsilon_additive = false;
-    double weights_epsilon = 6.103515625e-5, weights_scale = 1.0;
-    // Every expert's slot payload (gate | up | down, raw rows, the layout of
-    // residency's slots), all resident: the kernels route on the device.
-    std::vector<const void *> expert_payloads;
-    uint32_t gate_type = 0, up_type = 0, down_type = 0;
-};
 
 class HipBackend final : public Backend {
 public:
@@ -71,6 +51,10 @@ public:
     // gemv_quant (include/fm/kernels.hpp:79) for a block-type matrix that lives
     // in one of this backend's buffers: the engine's quantised branch of
     // matvec_view (engine.cpp:358-366) calls this instead of the CPU kernels.
+    // Logged under this backend's label with the engine's operation name. A
+    // matrix outside this backend's buffers is an INVALID_ARGUMENT: there is
+    // no CPU fallback. Where FreeMoe's Backend declares the same virtual (the
+    // integration's edit), this overrides it.
     void matvec_quant(uint32_t type_id, const void *weights, const float *x, float *y, uint32_t out_dim,
                       uint32_t in_dim, const std::string &op_name);
 
@@ -78,11 +62,13 @@ public:
     // out[hidden] = x + sum_i w_i down_i(SwiGLU(gate_i h, up_i h)) with
     // h = RMSNorm(x); ids / weights receive the routing in rank order (the
     // RoutingEvent's experts). Logs the reference's operation names
-    // (router.L*, router_gating.L*, router_topk.L*, expert_gate/up/down.L*.E*,
-    // expert_swiglu.L*, expert_combine.L*) under this backend's label. Meant
-    // for a call at the top of the engine's routed branch (engine.cpp:1602),
-    // which skips the per-expert loop when the layer ran here.
-    void moe_layer(const MoeLayerView &layer, const float *x, float *out, uint32_t *ids, float *weights);
+    // (router.L*, router_logit_bias.L* with a bias, router_gating.L*,
+    // router_topk.L*, expert_gate/up/down.L*.E*, expert_swiglu.L*,
+    // expert_combine.L*) under this backend's label. Meant for a call at the
+    // top of the engine's routed branch (engine.cpp:1602), which skips the
+    // per-expert loop when the layer ran here; returns true (the layer ran)
+    // or throws.
+    bool moe_layer(const MoeLayerView &layer, const float *x, float *out, uint32_t *ids, float *weights);
 
     // gemm_quant (include/fm/kernels.hpp:68) for a matrix (raw rows, any
     // supported type) inside one of this backend's buffers: y[t][o] for

@@ -156,7 +156,7 @@ typedef struct fmx_moe_layer {
     const float *norm_weight;     /* [hidden] RMSNorm gain, NULL = unit gain (16-byte aligned) */
     double rms_eps;               /* ModelConfig::rms_eps */
     double norm_bias;             /* 1.0 when norm weights are zero-centred */
-    uint32_t router_type;         /* FMX_TYPE_F32, _Q4_0, _Q8_0 or _Q4_K */
+    uint32_t router_type;         /* FMX_TYPE_F32, _Q4_0, _Q8_0, _Q4_K or _Q6_K (raw rows, hidden % 256 == 0) */
     const void *router;           /* [experts x hidden], 16-byte aligned: F32 raw row-major;
                                      a block type packed (fmx_pack), its logits then the
                                      gemv_quant row dots (engine.cpp:358-366) */

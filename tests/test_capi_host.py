@@ -115,3 +115,19 @@ def test_decode_static_refuses_oversized_layers():
     assert lib.fmx_moe_workspace_bytes(ctypes.byref(layer), 1) > (4 << 20)
     rc = lib.fmx_moe_decode_static(ctypes.byref(layer), p, p, 1, p, p, 0, None)
     assert rc == 3  # FMX_ERR_SHAPE_MISMATCH
+
+
+def test_route_checks_its_workspace_before_launching():
+    """fmx_moe_route with a block-type router and no caller's h runs one token
+    at a time through the workspace's h: a workspace too small for that is
+    refused with INVALID_ARGUMENT before any kernel is launched (here, with no
+    GPU, a launch would fail with another status)."""
+    lib = fmx.lib()
+    buf = np.zeros(4096, np.float32)
+    p = buf.ctypes.data + (-buf.ctypes.data) % 256
+    H, E, K = 256, 8, 2
+    layer = fmx.MoELayer(H, 512, E, K, 0, 1e-5, 0.0, wl.Q4_0, p, 0, 1, 0, 6.103515625e-5, 1.0, 2, 2, 2, p, p, p)
+    need = lib.fmx_moe_workspace_bytes(ctypes.byref(layer), 3)
+    assert need > 256
+    rc = lib.fmx_moe_route(ctypes.byref(layer), p, 3, None, p, p, p, p, 256, None)
+    assert rc == 1

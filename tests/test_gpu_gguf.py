@@ -10,6 +10,7 @@ import pytest
 
 from freemoe_amd import gguf
 from freemoe_amd import workloads as wl
+from freemoe_amd.device import DeviceLayer
 from golden import engine_models as em
 from test_gpu_moe import check_layer
 from test_gpu_prefill import check_prefill
