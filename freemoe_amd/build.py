@@ -20,7 +20,7 @@ CSRC = PKG / "csrc"
 LIB = PKG / "libfmx.so"
 
 SOURCES = ["capi.cpp", "quant.hip", "matvec.hip", "gemm.hip", "moe.hip", "down_pair_q4k.hip", "bucket.hip",
-           "prefill.hip"]
+           "prefill.hip", "attention.hip"]
 
 HIP_FLAGS = [
     "--offload-arch=gfx950",

@@ -594,6 +594,17 @@ int fmx_moe_prefill_timed(const fmx_moe_layer *L, const float *x, float *out, ui
     return rc;
 }
 
+int fmx_attention_decode(const float *q, const float *kv, uint64_t row_stride, uint32_t v_offset,
+                         uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t positions,
+                         double scale, float *out, void *workspace, uint64_t workspace_bytes, void *stream) {
+    if (int rc = fault_gate()) return rc;
+    if (!q || !kv || !out || !workspace || workspace_bytes < kStatusBytes) return FMX_ERR_INVALID_ARGUMENT;
+    if (!aligned16(q) || !aligned16(kv) || !aligned16(out) || !aligned16(workspace)) return FMX_ERR_INVALID_ARGUMENT;
+    if (!(scale == scale)) return FMX_ERR_INVALID_ARGUMENT;
+    return attention_decode(q, kv, row_stride, v_offset, heads, kv_heads, head_dim, positions, scale, out,
+                            static_cast<uint32_t *>(workspace), static_cast<hipStream_t>(stream));
+}
+
 int fmx_moe_status(void *workspace, void *stream) {
     if (!workspace) return FMX_ERR_INVALID_ARGUMENT;
     if (int rc = fault_gate()) return rc;

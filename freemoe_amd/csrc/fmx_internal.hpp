@@ -32,6 +32,11 @@ int fault_gate();
 
 int status_of_hip(hipError_t e);
 
+// attention.hip: fmx_attention_decode after its pointer checks.
+int attention_decode(const float *q, const float *kv, uint64_t row_stride, uint32_t v_offset, uint32_t heads,
+                     uint32_t kv_heads, uint32_t head_dim, uint32_t positions, double scale, float *out,
+                     uint32_t *status, hipStream_t s);
+
 // Raises kernel `fn`'s dynamic LDS limit to `bytes` when above the 64 KiB
 // default (gfx950 workgroups may use up to 160 KiB).
 int allow_lds(const void *fn, size_t bytes);

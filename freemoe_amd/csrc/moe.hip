@@ -776,13 +776,18 @@ __device__ inline float swiglu(float gate, float up) {
 // Gate and up rows j of the expert at rank blockIdx.y, RJ rows per thread:
 // the first PF chunks of every row are requested before h is staged.
 // Four wavefronts per SIMD (at most 128 VGPRs): the whole grid of a Mixtral
-// expert pair is then resident at once.
+// expert pair is then resident at once. A wavefront's eight 8-lane groups
+// take seven rows (the eighth group repeats the seventh's row, whose loads
+// the wavefront's coalescing merges, and stores nothing): the 28672 rows of a
+// Mixtral pair are then 4096 wavefronts, four on every SIMD, where eight rows
+// per wavefront left half the SIMDs four and half three.
 template <class T, int RJ, int PF>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4 / RJ), aligned(kHotAlign))) void gate_up_kernel(
     ExpertArgs a, const float *__restrict__ h, const float *__restrict__ logits, uint32_t *__restrict__ ids,
     float *__restrict__ w, float *__restrict__ act, uint32_t *__restrict__ status) {
     extern __shared__ __align__(16) float lds[];
-    const uint32_t tid = threadIdx.x, l = tid & 7, slot = tid >> 3;
+    const uint32_t tid = threadIdx.x, l = tid & 7, g8 = (tid >> 3) & 7;
+    const uint32_t slot = (tid >> 6) * 7 + (g8 < 7 ? g8 : 6);
     const uint32_t rank = blockIdx.y;
     const uint32_t blocks = a.gu.blocks;
     // the logits are requested first, then h's first tile, so that the
@@ -804,7 +809,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4 / RJ
     const uint8_t *gate = static_cast<const uint8_t *>(a.gate[e]);
     const uint8_t *up = static_cast<const uint8_t *>(a.up[e]);
     const uint32_t F = a.ffn;
-    const uint32_t j0 = (blockIdx.x * (kThreads / 8) + slot) * RJ;
+    const uint32_t j0 = (blockIdx.x * (kThreads / 64 * 7) + slot) * RJ;
     typename T::Row rw[2 * RJ];
     float t[2 * RJ];
 #pragma unroll
@@ -830,7 +835,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4 / RJ
     for (int m = 0; m < RJ; ++m) {
         const float g = T::finish(t[2 * m]);
         const float u = T::finish(t[2 * m + 1]);
-        if (l == 0 && j0 + m < F) act[static_cast<uint64_t>(rank) * F + j0 + m] = swiglu(g, u);
+        if (l == 0 && g8 < 7 && j0 + m < F) act[static_cast<uint64_t>(rank) * F + j0 + m] = swiglu(g, u);
     }
 }
 
@@ -1028,7 +1033,7 @@ int launch_gate_up_q(const ExpertArgs &a, const float *h, const float *logits, u
     auto gu = gate_up_kernel<TG, kRJ, kGateUpPF>;
     const size_t lds = gate_up_lds(a);
     if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds)) return rc;
-    return launch_timed(gu, dim3(div_up(a.ffn, (kThreads / 8) * kRJ), a.top_k), lds, s, kev, a, h, logits, ids, w,
+    return launch_timed(gu, dim3(div_up(a.ffn, (kThreads / 64 * 7) * kRJ), a.top_k), lds, s, kev, a, h, logits, ids, w,
                         act, status);
 }
 

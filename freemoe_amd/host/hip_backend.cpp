@@ -67,6 +67,15 @@ struct HipBackend::State {
     void *moe_ws = nullptr, *moe_small = nullptr;
     uint64_t moe_ws_cap = 0, moe_small_cap = 0;
     std::map<std::vector<uintptr_t>, void *> slot_tables; // packed expert pointers -> device table
+    // KV caches seen by attention(): per layer cache (its row 0's host
+    // address), the position count of the last call and a copy of the last
+    // row it uploaded
+    struct KvSync {
+        uint64_t positions = 0;
+        std::vector<float> last_row;
+    };
+    std::map<uintptr_t, KvSync> kv_sync;
+    void *attn_status = nullptr;
 
     ~State() {
         for (auto &f : fences) fmx_fence_release(f.second);
@@ -76,6 +85,7 @@ struct HipBackend::State {
         fmx_free(y_dev);
         fmx_free(moe_ws);
         fmx_free(moe_small);
+        fmx_free(attn_status);
     }
 
     const Twin *find_twin(const void *host, uint64_t *offset) const {
@@ -520,6 +530,50 @@ bool HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, ui
         record_operation({"expert_down" + ex, name(), down_bytes + F * 4ull, H * 4ull});
     }
     record_control("expert_combine.L" + l, K * H * 4ull, H * 4ull, name());
+    return true;
+}
+
+bool HipBackend::attention(const AttentionView &A, const float *q, float *out) {
+    if (fault_ == BackendFault::DeviceLoss) fail(ErrorCode::DEVICE_LOSS, "injected device loss");
+    if (!q || !out || !A.kv || A.positions == 0 || A.heads == 0 || A.head_dim == 0)
+        fail(ErrorCode::INVALID_ARGUMENT, "invalid attention arguments");
+    const uint64_t P = A.positions, D = A.head_dim, H = A.heads;
+    // shapes fmx_attention_decode does not take run the engine's own loop
+    if (P > 8192 || D > 256 || D % 4 || A.kv_heads == 0 || H % A.kv_heads || A.row_stride % 4 || A.v_offset % 4 ||
+        A.v_offset < A.kv_heads * D || A.v_offset + A.kv_heads * D > A.row_stride)
+        return false;
+    std::lock_guard<std::mutex> lock(state_->mutex);
+    State &s = *state_;
+    uint64_t off = 0;
+    const State::Twin *t = s.find_twin(A.kv, &off);
+    const uint64_t row_bytes = A.row_stride * 4;
+    if (!t || off % 16 || off + P * row_bytes > t->bytes) return false;
+    float *kv_dev = reinterpret_cast<float *>(static_cast<uint8_t *>(t->device) + off);
+    // rows written on the host since the last call: the next row when this
+    // call continues the last one (its row P - 2 still as uploaded), every
+    // row otherwise (a new sequence, or rows a batched prefill wrote)
+    State::KvSync &ks = s.kv_sync[reinterpret_cast<uintptr_t>(A.kv)];
+    const float *prev = A.kv + (P >= 2 ? (P - 2) * A.row_stride : 0);
+    const bool next_row = P >= 2 && ks.positions + 1 == P && ks.last_row.size() == A.row_stride &&
+                          std::memcmp(prev, ks.last_row.data(), row_bytes) == 0;
+    const uint64_t from = next_row ? P - 1 : 0;
+    check(fmx_upload(kv_dev + from * A.row_stride, A.kv + from * A.row_stride, (P - from) * row_bytes, s.stream,
+                     nullptr),
+          "attention cache rows");
+    ks.positions = P;
+    ks.last_row.assign(A.kv + (P - 1) * A.row_stride, A.kv + P * A.row_stride);
+    if (!s.attn_status) check(fmx_alloc(256, &s.attn_status), "attention status");
+    const uint64_t qo_bytes = H * D * 4;
+    ensure_scratch(qo_bytes, qo_bytes);
+    check(fmx_upload(s.x_dev, q, qo_bytes, s.stream, nullptr), "attention query");
+    check(fmx_attention_decode(static_cast<const float *>(s.x_dev), kv_dev, A.row_stride, A.v_offset,
+                               static_cast<uint32_t>(H), A.kv_heads, static_cast<uint32_t>(D),
+                               static_cast<uint32_t>(P), A.scale, static_cast<float *>(s.y_dev), s.attn_status, 256,
+                               s.stream),
+          "attention.L" + std::to_string(A.layer));
+    check(fmx_download(out, s.y_dev, qo_bytes, s.stream), "attention output");
+    check(fmx_moe_status(s.attn_status, s.stream), "non-finite attention score in layer " + std::to_string(A.layer));
+    record_operation({"attention.L" + std::to_string(A.layer), name(), P * A.kv_heads * D * 8 + qo_bytes, qo_bytes});
     return true;
 }
 

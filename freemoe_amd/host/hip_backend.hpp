@@ -70,6 +70,16 @@ public:
     // or throws.
     bool moe_layer(const MoeLayerView &layer, const float *x, float *out, uint32_t *ids, float *weights);
 
+    // One token's attention in one layer on the device (fmx_attention_decode):
+    // the engine's full-context loop (engine.cpp:1360-1420) for the cache
+    // rows the view describes. The cache is a buffer of this backend whose
+    // rows the engine writes on the host: the rows written since the last call
+    // go to its HBM twin first (one row when the call continues the previous
+    // one, every row otherwise). Returns false for a shape the kernel does not
+    // take, so the engine runs its own loop. Where FreeMoe's Backend declares
+    // the same virtual (the integration's fourth edit), this overrides it.
+    bool attention(const AttentionView &view, const float *q, float *out);
+
     // gemm_quant (include/fm/kernels.hpp:68) for a matrix (raw rows, any
     // supported type) inside one of this backend's buffers: y[t][o] for
     // tokens t, bit for bit the reference's (fmx_gemm_quant). The batched

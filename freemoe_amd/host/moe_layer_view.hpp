@@ -1,5 +1,6 @@
-// moe_layer_view.hpp — one routed MoE layer as FreeMoe's engine holds it, for
-// a backend that runs the whole block (engine.cpp:1602-1776) on the device.
+// moe_layer_view.hpp — one routed MoE layer, and one token's attention, as
+// FreeMoe's engine holds them, for a backend that runs the whole block
+// (engine.cpp:1602-1776) or the attention loop (1360-1420) on the device.
 //
 // Host pointers as the engine has them: weights inside the backend's buffers
 // (the fixed-weight buffer, the expert slots); the norm gains and the logit
@@ -27,6 +28,20 @@ struct MoeLayerView {
     // residency's slots), all resident: the kernels route on the device.
     std::vector<const void *> expert_payloads;
     uint32_t gate_type = 0, up_type = 0, down_type = 0;
+};
+
+// One token's attention in one layer: the engine's KV cache (a host pointer
+// inside a backend buffer) with `positions` rows written, position t's row at
+// kv + t * row_stride floats (every kv head's key, the values at +
+// v_offset), and the query [heads x head_dim] the call passes.
+struct AttentionView {
+    uint32_t layer = 0;
+    uint32_t heads = 0, kv_heads = 0, head_dim = 0;
+    uint64_t positions = 0;
+    double scale = 1.0;
+    const float *kv = nullptr;
+    uint64_t row_stride = 0;
+    uint32_t v_offset = 0;
 };
 
 } // namespace fm

@@ -260,6 +260,24 @@ int fmx_moe_bucket(const uint32_t *ids, uint32_t tokens, uint32_t top_k, uint32_
                    uint32_t *offsets, uint32_t *token_list, uint32_t *rank_list, void *workspace,
                    uint64_t workspace_bytes, void *stream);
 
+/* Decode attention of one token over its `positions` cached positions, the
+ * full-context multi-head / grouped-query case of the engine's attention loop
+ * (engine.cpp:1360-1420; replaces its per-head host loop behind
+ * fm::HipBackend::attention). kv: the layer's cache on the device, position
+ * t's row at kv + t * row_stride floats holding every kv head's key, the
+ * values at + v_offset; q and out: [heads x head_dim] floats; scale: the
+ * score scale (1 / sqrt(head_dim)). Per head: scores float(double dot * scale)
+ * with the dot summed in index order, the engine's softmax (float maximum,
+ * double exponentials summed in position order), values summed in double in
+ * position order. Only exp is the device's own (within an ulp of the host
+ * libm's). heads % kv_heads == 0, head_dim <= 256 and % 4 == 0, positions
+ * <= 8192, pointers 16-byte aligned. workspace (>= 256 bytes): its first
+ * word receives the error word; a non-finite score (INTERNAL_ERROR in the
+ * engine) is reported by fmx_moe_status on it. */
+int fmx_attention_decode(const float *q, const float *kv, uint64_t row_stride, uint32_t v_offset,
+                         uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t positions,
+                         double scale, float *out, void *workspace, uint64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

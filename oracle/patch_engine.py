@@ -11,9 +11,10 @@ run it on HipBackend next to the unedited CPU engine.
 Edits (each located by a short anchor in the original; the script stops if
 an anchor is missing or not unique):
 
-  backend.hpp  three virtuals on fm::Backend: matvec_quant (block-type
-               matrix times vector), gemm_quant (the batched product) and
-               moe_layer (the whole routed block, default: not taken).
+  backend.hpp  four virtuals on fm::Backend: matvec_quant (block-type
+               matrix times vector), gemm_quant (the batched product),
+               moe_layer (the whole routed block, default: not taken) and
+               attention (one token's attention, default: not taken).
   backend.cpp  their defaults: FreeMoe's own gemv_quant / gemm_quant with
                the engine's kernel settings and the engine's op records
                ("cpu-quant", "cpu-batched"), so every CPU backend behaves as
@@ -23,7 +24,10 @@ an anchor is missing or not unique):
                routed MoE branch (1602) first offers the layer to
                Backend::moe_layer and, when the backend ran it, records the
                routing, keeps residency's selected / executed accounting and
-               takes the layer's output as the new residual stream.
+               takes the layer's output as the new residual stream; the
+               per-token attention loop (1367-1420) is first offered to
+               Backend::attention (a fourth virtual, default: declined) for
+               the full-context multi-head / grouped-query case.
 """
 from __future__ import annotations
 
@@ -60,7 +64,8 @@ def replace_call(text: str, call: str, start_anchor: str, end_anchor: str, new: 
     return text[:s] + indent + new + "\n" + text[line_end(text, e):]
 
 
-BACKEND_HPP_DECL = """struct MoeLayerView; // moe_layer_view.hpp (fmx integration)
+BACKEND_HPP_DECL = """struct MoeLayerView;  // moe_layer_view.hpp (fmx integration)
+struct AttentionView; // moe_layer_view.hpp (fmx integration)
 
 """
 
@@ -75,6 +80,10 @@ BACKEND_HPP_VIRTUALS = """    // fmx integration: block-type products and the ro
     virtual bool moe_layer(const MoeLayerView &layer, const float *x, float *out, uint32_t *ids,
                            float *weights) {
         (void)layer, (void)x, (void)out, (void)ids, (void)weights;
+        return false;
+    }
+    virtual bool attention(const AttentionView &view, const float *q, float *out) {
+        (void)view, (void)q, (void)out;
         return false;
     }
 """
@@ -174,6 +183,30 @@ ENGINE_HOOK = """            // fmx integration: offer the whole routed block to
 """
 
 
+ENGINE_ATTENTION_HOOK = """        // fmx integration: offer the attention loop below to the backend for
+        // the full-context case its kernel computes (no ALiBi, logit soft-cap,
+        // sinks or window; values as wide as keys; not MLA). The cache rows
+        // stay where the engine wrote them.
+        bool attention_on_backend = false;
+        if (alibi_slopes.empty() && !(c.attn_logit_softcap > 0.0) && !c.attn_sinks &&
+            !c.layer_uses_window(layer) && !c.mla && c.head_v_dim() == c.head_dim) {
+            AttentionView av;
+            av.layer = layer;
+            av.heads = c.heads;
+            av.kv_heads = c.kv_heads;
+            av.head_dim = c.head_dim;
+            av.positions = position + 1;
+            av.scale = scale;
+            const uint64_t row0 = c.cache_index(layer, 0, c.context);
+            av.kv = kv_ + row0;
+            av.row_stride = c.cache_index(layer, 1, c.context) - row0;
+            av.v_offset = kv_dim;
+            attention_on_backend = backend_->attention(av, q.data(), attention.data());
+        }
+        if (!attention_on_backend)
+"""
+
+
 def patch(tree: Path, out: Path) -> None:
     hpp = (tree / "include/fm/backend.hpp").read_text()
     at = once(hpp, "class Backend {\n", "backend.hpp")
@@ -203,6 +236,11 @@ def patch(tree: Path, out: Path) -> None:
         raise SystemExit("patch_engine: the routed branch does not start where expected")
     s = line_start(eng, decl)
     eng = eng[:s] + ENGINE_HOOK + eng[s:]
+    att = once(eng, "std::vector<float> attention(attn_out_dim, 0.0f);", "engine.cpp attention")
+    loop = eng.find("        for (uint32_t head = 0; head < c.heads; ++head) {", att)
+    if loop < 0 or loop - att > 400:
+        raise SystemExit("patch_engine: the attention loop does not follow the attention vector")
+    eng = eng[:loop] + ENGINE_ATTENTION_HOOK + eng[loop:]
 
     (out / "include/fm").mkdir(parents=True, exist_ok=True)
     (out / "src").mkdir(parents=True, exist_ok=True)

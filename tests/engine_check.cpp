@@ -44,10 +44,11 @@
 // batched products); "hooked" (projections the renamed direct calls ran on
 // the device); "fallbacks" (renamed calls that ran FreeMoe's CPU kernel, for
 // an engine on another backend kind in the same process); "fused_layers"
-// (MoE blocks HipBackend::moe_layer ran).
+// (MoE blocks HipBackend::moe_layer ran); "device_attention" (token-layer
+// attentions HipBackend::attention ran).
 // Built twice: on FreeMoe's unchanged sources (engine_check) and on the
 // sources with the integration's edits (engine_check_fused, where the engine
-// calls Backend::matvec_quant / gemm_quant / moe_layer itself).
+// calls Backend::matvec_quant / gemm_quant / moe_layer / attention itself).
 // Exits non-zero on an engine error.
 #include "fm/engine.hpp"
 #include "fm/residency.hpp"
@@ -89,7 +90,7 @@ fm::RunConfig config_for(const std::string &model, bool gpu) {
 // the accounting of block-type projections (see the header).
 std::string op_labels(fm::Backend &b) {
     std::map<std::string, uint64_t> by, hooked;
-    uint64_t quant_records = 0, batch_records = 0, fused_layers = 0;
+    uint64_t quant_records = 0, batch_records = 0, fused_layers = 0, device_attention = 0;
     const std::string dev = b.name();
     for (const auto &op : b.operations()) {
         by[op.backend] += 1;
@@ -99,6 +100,7 @@ std::string op_labels(fm::Backend &b) {
             op.name.compare(op.name.size() - 6, 6, ".batch") == 0)
             ++batch_records;
         if (op.backend == dev && op.name.rfind("expert_combine.L", 0) == 0) ++fused_layers;
+        if (op.backend == dev && op.name.rfind("attention.L", 0) == 0) ++device_attention;
     }
     auto obj = [](const std::map<std::string, uint64_t> &m) {
         std::string s = "{";
@@ -114,6 +116,7 @@ std::string op_labels(fm::Backend &b) {
            ",\"quant_records\":" + std::to_string(quant_records) +
            ",\"batch_records\":" + std::to_string(batch_records) +
            ",\"fused_layers\":" + std::to_string(fused_layers) +
+           ",\"device_attention\":" + std::to_string(device_attention) +
            ",\"fallbacks\":" + std::to_string(fmx_engine_hook_fallbacks()) + "}";
 }
 

@@ -131,3 +131,18 @@ def test_route_checks_its_workspace_before_launching():
     assert need > 256
     rc = lib.fmx_moe_route(ctypes.byref(layer), p, 3, None, p, p, p, p, 256, None)
     assert rc == 1
+
+
+def test_attention_decode_refuses_shapes_before_launch():
+    """fmx_attention_decode checks its shape on the host: positions beyond
+    8192, a head width that is not a multiple of 4, heads not a multiple of
+    the kv heads are SHAPE_MISMATCH, a null pointer INVALID_ARGUMENT, all
+    before anything is launched."""
+    lib = fmx.lib()
+    buf = np.zeros(64, np.float32)
+    p = buf.ctypes.data + (-buf.ctypes.data) % 16
+    # positions beyond 8192, head_dim not a multiple of 4, heads not a multiple of kv_heads
+    assert lib.fmx_attention_decode(p, p, 256, 128, 4, 4, 32, 8193, 0.5, p, p, 256, None) == 3
+    assert lib.fmx_attention_decode(p, p, 256, 128, 4, 4, 30, 8, 0.5, p, p, 256, None) == 3
+    assert lib.fmx_attention_decode(p, p, 256, 128, 6, 4, 32, 8, 0.5, p, p, 256, None) == 3
+    assert lib.fmx_attention_decode(None, p, 256, 128, 4, 4, 32, 8, 0.5, p, p, 256, None) == 1

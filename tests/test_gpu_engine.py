@@ -53,7 +53,8 @@ def check_device_accounting(ops, fused=False):
     in a process without a CPU engine (that would also have raised). With
     the integration's edits the engine calls the backend itself: there are
     no cpu-* records at all."""
-    labels = {k for k in ops if k not in ("hooked", "quant_records", "batch_records", "fused_layers", "fallbacks")}
+    labels = {k for k in ops if k not in ("hooked", "quant_records", "batch_records", "fused_layers", "fallbacks",
+                                          "device_attention")}
     assert labels <= DEVICE_LABELS, labels
     assert ops["hooked"].get("gemv_quant", 0) == ops["quant_records"], ops
     assert ops["hooked"].get("gemm_quant", 0) == ops["batch_records"], ops
@@ -214,12 +215,15 @@ def test_eight_layer_decoder_256_256_fused_against_cpu_engine(gpu, decoder_path)
     """The 8-layer decoder at its stated size, 256 random prompt bytes then
     256 greedy tokens, through FreeMoe's engine with the integration's edits
     on HipBackend: every MoE block runs as one fmx_moe_decode
-    (Backend::moe_layer), the F32 attention and head projections as
-    fmx_matvec. Prompt logits bit for bit, every routing record and greedy id
-    equal to what FreeMoe's CPU engine produced for the same checkpoint and
-    prompt (tests/golden/decoder_256_256.fmxg, made by
+    (Backend::moe_layer), every token's attention as one
+    fmx_attention_decode per layer over the cache rows mirrored to HBM
+    (Backend::attention), the F32 attention and head projections as
+    fmx_matvec. Against what FreeMoe's CPU engine produced for the same
+    checkpoint and prompt (tests/golden/decoder_256_256.fmxg, made by
     tests/golden/make_decoder_golden.py; the JSON beside it pins the
-    checkpoint's SHA-256)."""
+    checkpoint's SHA-256): every routing record and greedy id equal, prompt
+    logits within 1e-4 (the attention's exp is the device's, within an ulp of
+    the host libm's, so a last bit may differ; the count is printed)."""
     import hashlib
     import sys
 
@@ -235,13 +239,16 @@ def test_eight_layer_decoder_256_256_fused_against_cpu_engine(gpu, decoder_path)
     print(r)
     assert r["backend"] == "hip-gfx950"
     assert r["prompt_tokens"] == meta["prompt_len"] + 1
-    assert r["logits"] > 0 and r["differing_logits"] == 0 and r["max_abs_diff"] == 0.0
+    print(f"[decoder] logits differing in any bit: {r['differing_logits']} of {r['logits']}, "
+          f"max abs diff {r['max_abs_diff']}", file=sys.__stderr__, flush=True)
+    assert r["logits"] > 0 and r["max_abs_diff"] <= 1e-4
     assert r["routing_identical"] and r["ids_identical"]
     assert r["routing_events"] == (r["prompt_tokens"] + r["generated"] - 1) * 8 or \
         r["routing_events"] == (r["prompt_tokens"] + r["generated"]) * 8
     ops = r["gpu_ops"]
     check_device_accounting(ops, fused=True)
     assert ops["fused_layers"] == r["routing_events"]  # every MoE block ran as one fused layer
+    assert ops["device_attention"] == r["routing_events"]  # and every attention on the device
 
 
 @pytest.mark.gpu
@@ -254,7 +261,7 @@ def test_fused_engine_compare_reference_on_hip_backend(gpu):
     assert r["backend"] == "hip-gfx950"
     check_compare(r, 20)
     check_device_accounting(r["ops"], fused=True)
-    assert r["ops"]["fused_layers"] > 0
+    assert r["ops"]["fused_layers"] > 0 and r["ops"]["device_attention"] == r["ops"]["fused_layers"]
 
 
 @pytest.mark.gpu
@@ -262,18 +269,21 @@ def test_fused_engine_compare_reference_on_hip_backend(gpu):
                                      "quant-expert-fused", "quant-expert-separate"])
 def test_fused_engine_quantised_checkpoints(gpu, variant):
     """FreeMoe's block-type checkpoints through the edited engine: the GPU
-    engine's routed blocks run fused, its other block-type projections
-    through HipBackend::matvec_quant under the engine's own op names; the
-    CPU engine in the same process runs the edit's defaults (FreeMoe's
-    kernels). Prompt logits bit for bit, greedy ids and routing equal."""
+    engine's routed blocks run fused and its attention on the device, its
+    other block-type projections through HipBackend::matvec_quant under the
+    engine's own op names; the CPU engine in the same process runs the
+    edit's defaults (FreeMoe's kernels and loops). Greedy ids and routing
+    equal, prompt logits within 1e-4 (the device attention's exp may move a
+    last bit)."""
     text = "mixed experts" if variant.startswith("quant-expert") else "quantised conformance"
     r = run("prompt", FIXTURES / f"{variant}.gguf", 6, text, binary=FUSED)
     print(r)
     assert r["backends"] == ["cpu", "hip-gfx950"]
-    assert r["logits"] > 0 and r["differing_logits"] == 0 and r["max_abs_diff"] == 0.0
+    assert r["logits"] > 0 and r["max_abs_diff"] <= 1e-4
     assert r["ids_identical"] and r["routing_identical"] and r["generated"] == 6
     check_device_accounting(r["gpu_ops"], fused=True)
     assert r["gpu_ops"]["fused_layers"] == r["routing_events"]
+    assert r["gpu_ops"]["device_attention"] > 0
 
 
 @pytest.mark.gpu
