@@ -76,6 +76,34 @@ struct HipBackend::State {
     };
     std::map<uintptr_t, KvSync> kv_sync;
     void *attn_status = nullptr;
+    // pinned host staging of a call's inputs and outputs (the engine's
+    // vectors are pageable): one copy in and one out per call
+    void *stage_in = nullptr, *stage_out = nullptr;
+    uint64_t stage_in_cap = 0, stage_out_cap = 0;
+
+    uint8_t *pinned(void *&buf, uint64_t &cap, uint64_t bytes) {
+        if (bytes > cap) {
+            fmx_host_free(buf);
+            buf = nullptr;
+            cap = 0;
+            check_status(fmx_host_alloc(bytes, &buf), "pinned staging");
+            cap = bytes;
+        }
+        return static_cast<uint8_t *>(buf);
+    }
+    // bytes of src to device dst through the pinned input staging; the copy
+    // is queued on the stream (a later download's synchronisation covers it)
+    void upload_staged(void *dst, const void *src, uint64_t bytes) {
+        uint8_t *h = pinned(stage_in, stage_in_cap, bytes);
+        std::memcpy(h, src, static_cast<size_t>(bytes));
+        check_status(fmx_upload(dst, h, bytes, stream, nullptr), "staged upload");
+    }
+    // bytes of device src to dst through the pinned output staging (waits)
+    void download_staged(void *dst, const void *src, uint64_t bytes) {
+        uint8_t *h = pinned(stage_out, stage_out_cap, bytes);
+        check_status(fmx_download(h, src, bytes, stream), "staged download");
+        std::memcpy(dst, h, static_cast<size_t>(bytes));
+    }
 
     ~State() {
         for (auto &f : fences) fmx_fence_release(f.second);
@@ -86,6 +114,8 @@ struct HipBackend::State {
         fmx_free(moe_ws);
         fmx_free(moe_small);
         fmx_free(attn_status);
+        fmx_host_free(stage_in);
+        fmx_host_free(stage_out);
     }
 
     const Twin *find_twin(const void *host, uint64_t *offset) const {
@@ -331,11 +361,11 @@ void HipBackend::matvec(const float *weights, const float *x, float *y, uint32_t
     if (!t || off + static_cast<uint64_t>(out_dim) * in_dim * 4 > t->bytes)
         fail(ErrorCode::INVALID_ARGUMENT, "matvec weights are not in a device buffer: " + op_name);
     ensure_scratch(static_cast<uint64_t>(in_dim) * 4, static_cast<uint64_t>(out_dim) * 4);
-    check(fmx_upload(s.x_dev, x, static_cast<uint64_t>(in_dim) * 4, s.stream, nullptr), op_name);
+    s.upload_staged(s.x_dev, x, static_cast<uint64_t>(in_dim) * 4);
     check(fmx_matvec(FMX_TYPE_F32, static_cast<uint8_t *>(t->device) + off, static_cast<const float *>(s.x_dev),
                      static_cast<float *>(s.y_dev), out_dim, in_dim, s.stream),
           op_name);
-    check(fmx_download(y, s.y_dev, static_cast<uint64_t>(out_dim) * 4, s.stream), op_name);
+    s.download_staged(y, s.y_dev, static_cast<uint64_t>(out_dim) * 4);
     record_operation({op_name, name(), (static_cast<uint64_t>(out_dim) * in_dim + in_dim) * sizeof(float),
                       static_cast<uint64_t>(out_dim) * sizeof(float)});
 }
@@ -353,11 +383,11 @@ void HipBackend::matvec_quant(uint32_t type_id, const void *weights, const float
     State &s = *state_;
     void *packed = s.packed_twin(type_id, weights, out_dim, in_dim);
     ensure_scratch(static_cast<uint64_t>(in_dim) * 4, static_cast<uint64_t>(out_dim) * 4);
-    check(fmx_upload(s.x_dev, x, static_cast<uint64_t>(in_dim) * 4, s.stream, nullptr), op_name);
+    s.upload_staged(s.x_dev, x, static_cast<uint64_t>(in_dim) * 4);
     check(fmx_matvec(type_id, packed, static_cast<const float *>(s.x_dev), static_cast<float *>(s.y_dev), out_dim,
                      in_dim, s.stream),
           op_name);
-    check(fmx_download(y, s.y_dev, static_cast<uint64_t>(out_dim) * 4, s.stream), op_name);
+    s.download_staged(y, s.y_dev, static_cast<uint64_t>(out_dim) * 4);
     record_operation({op_name, name(), raw_bytes(type_id, out_dim, in_dim) + in_dim * 4ull,
                       static_cast<uint64_t>(out_dim) * sizeof(float)});
 }
@@ -380,11 +410,11 @@ void HipBackend::gemm_quant(uint32_t type_id, const void *weights, const float *
         fail(ErrorCode::INVALID_ARGUMENT, "batched product weights are not in a device buffer: " + op_name);
     const uint64_t x_bytes = static_cast<uint64_t>(tokens) * in_dim * 4, y_bytes = static_cast<uint64_t>(tokens) * out_dim * 4;
     ensure_scratch(x_bytes, y_bytes);
-    check(fmx_upload(s.x_dev, x, x_bytes, s.stream, nullptr), op_name);
+    s.upload_staged(s.x_dev, x, x_bytes);
     check(fmx_gemm_quant(type_id, static_cast<uint8_t *>(t->device) + off, static_cast<const float *>(s.x_dev),
                          static_cast<float *>(s.y_dev), tokens, out_dim, in_dim, s.stream),
           op_name);
-    check(fmx_download(y, s.y_dev, y_bytes, s.stream), op_name);
+    s.download_staged(y, s.y_dev, y_bytes);
     record_operation({op_name, name(), w_bytes + x_bytes, y_bytes});
 }
 
@@ -461,7 +491,12 @@ bool HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, ui
         s.moe_small_cap = small;
     }
     uint8_t *sm = static_cast<uint8_t *>(s.moe_small);
+    // x, the norm gains (when not resident in a buffer) and the logit bias go
+    // up in one copy of the block [x | norm | bias] as laid out on the device
+    uint8_t *hin = s.pinned(s.stage_in, s.stage_in_cap, o_out);
     const float *norm_dev = nullptr;
+    uint64_t in_bytes = H * 4ull;
+    std::memcpy(hin + o_x, x, H * 4ull);
     if (L.norm_weight) {
         uint64_t off = 0;
         const State::Twin *t = s.find_twin(L.norm_weight, &off);
@@ -469,12 +504,16 @@ bool HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, ui
         if (t && off + H * 4ull <= t->bytes && addr % 16 == 0) {
             norm_dev = reinterpret_cast<const float *>(addr);
         } else {
-            check(fmx_upload(sm + o_norm, L.norm_weight, H * 4ull, s.stream, nullptr), "norm gains");
+            std::memcpy(hin + o_norm, L.norm_weight, H * 4ull);
+            in_bytes = o_norm + H * 4ull;
             norm_dev = reinterpret_cast<const float *>(sm + o_norm);
         }
     }
-    if (L.router_bias) check(fmx_upload(sm + o_bias, L.router_bias, E * 4ull, s.stream, nullptr), "router bias");
-    check(fmx_upload(sm + o_x, x, H * 4ull, s.stream, nullptr), "MoE input");
+    if (L.router_bias) {
+        std::memcpy(hin + o_bias, L.router_bias, E * 4ull);
+        in_bytes = o_bias + E * 4ull;
+    }
+    check(fmx_upload(sm + o_x, hin + o_x, in_bytes, s.stream, nullptr), "MoE inputs");
 
     fmx_moe_layer d;
     std::memset(&d, 0, sizeof(d));
@@ -512,9 +551,14 @@ bool HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, ui
                          reinterpret_cast<uint32_t *>(sm + o_ids), reinterpret_cast<float *>(sm + o_w), s.moe_ws,
                          s.moe_ws_cap, s.stream),
           "moe layer " + l);
-    check(fmx_download(out, sm + o_out, H * 4ull, s.stream), "MoE output");
-    check(fmx_download(ids, sm + o_ids, K * 4ull, s.stream), "MoE routing");
-    check(fmx_download(weights, sm + o_w, K * 4ull, s.stream), "MoE weights");
+    {
+        // out, ids and weights back in one copy of [out | ids | weights]
+        uint8_t *hout = s.pinned(s.stage_out, s.stage_out_cap, small - o_out);
+        check(fmx_download(hout, sm + o_out, o_w + K * 4ull - o_out, s.stream), "MoE outputs");
+        std::memcpy(out, hout, H * 4ull);
+        std::memcpy(ids, hout + (o_ids - o_out), K * 4ull);
+        std::memcpy(weights, hout + (o_w - o_out), K * 4ull);
+    }
     check(fmx_moe_status(s.moe_ws, s.stream), "router scores of layer " + l);
 
     // the reference's operation log for this block (engine.cpp:1603-1776)
@@ -565,13 +609,13 @@ bool HipBackend::attention(const AttentionView &A, const float *q, float *out) {
     if (!s.attn_status) check(fmx_alloc(256, &s.attn_status), "attention status");
     const uint64_t qo_bytes = H * D * 4;
     ensure_scratch(qo_bytes, qo_bytes);
-    check(fmx_upload(s.x_dev, q, qo_bytes, s.stream, nullptr), "attention query");
+    s.upload_staged(s.x_dev, q, qo_bytes);
     check(fmx_attention_decode(static_cast<const float *>(s.x_dev), kv_dev, A.row_stride, A.v_offset,
                                static_cast<uint32_t>(H), A.kv_heads, static_cast<uint32_t>(D),
                                static_cast<uint32_t>(P), A.scale, static_cast<float *>(s.y_dev), s.attn_status, 256,
                                s.stream),
           "attention.L" + std::to_string(A.layer));
-    check(fmx_download(out, s.y_dev, qo_bytes, s.stream), "attention output");
+    s.download_staged(out, s.y_dev, qo_bytes);
     check(fmx_moe_status(s.attn_status, s.stream), "non-finite attention score in layer " + std::to_string(A.layer));
     record_operation({"attention.L" + std::to_string(A.layer), name(), P * A.kv_heads * D * 8 + qo_bytes, qo_bytes});
     return true;
