@@ -188,7 +188,185 @@ __global__ __launch_bounds__(256) void invert_slots_kernel(const uint32_t *__res
     rank_list[pos] = i % K;
 }
 
+// ------------------------------------------------- many-workgroup bucketing --
+// The same lists (and slot_of, tiles, offsets) over many workgroups, for the
+// prefill: the tokens in chunks of kChunkTokens, one workgroup per chunk in
+// two passes. Pass 1 writes each chunk's per-expert counts (integer adds in
+// LDS) and a bad-id word; pass 2 gives each chunk the expert offsets (an
+// exclusive scan of the totals) plus the counts of the chunks before it, and
+// places the chunk's pairs by the popcounts of per-expert token bitmasks, as
+// the single-workgroup pass does per 1024-token chunk. Deterministic: no
+// position comes from an atomic slot grab.
+constexpr uint32_t kChunkTokens = 256;
+constexpr uint32_t kChunkWords = kChunkTokens / 32; // bitmask words per expert
+
+// counts[c][E + 1]: chunk c's per-expert counts, then 1 when one of its ids is
+// >= E. grid: chunks.
+__global__ __launch_bounds__(kChunkTokens) void bucket_count_kernel(const uint32_t *__restrict__ ids,
+                                                                   uint32_t tokens, uint32_t K, uint32_t E,
+                                                                   uint32_t *__restrict__ counts) {
+    __shared__ uint32_t cnt[kBucketMaxExperts];
+    __shared__ uint32_t bad;
+    const uint32_t tid = threadIdx.x, c = blockIdx.x;
+    if (tid == 0) bad = 0;
+    for (uint32_t e = tid; e < E; e += kChunkTokens) cnt[e] = 0;
+    __syncthreads();
+    const uint32_t t0 = c * kChunkTokens, t1 = tokens - t0 < kChunkTokens ? tokens : t0 + kChunkTokens;
+    const uint64_t i1 = static_cast<uint64_t>(t1) * K;
+    for (uint64_t i = static_cast<uint64_t>(t0) * K + tid; i < i1; i += kChunkTokens) {
+        const uint32_t e = ids[i];
+        if (e < E) atomicAdd(&cnt[e], 1u);
+        else atomicOr(&bad, 1u);
+    }
+    __syncthreads();
+    uint32_t *out = counts + static_cast<uint64_t>(c) * (E + 1);
+    for (uint32_t e = tid; e < E; e += kChunkTokens) out[e] = cnt[e];
+    if (tid == 0) out[E] = bad;
+}
+
+// Pass 2. grid: chunks; chunk 0 also writes offsets[E + 1] and the tiles.
+__global__ __launch_bounds__(kChunkTokens) void bucket_place_kernel(
+    const uint32_t *__restrict__ ids, uint32_t tokens, uint32_t K, uint32_t E, uint32_t chunks,
+    const uint32_t *__restrict__ counts, uint32_t *__restrict__ offsets, uint32_t *__restrict__ slot_of,
+    uint32_t *__restrict__ status, uint32_t *__restrict__ tiles, uint32_t tile_rows) {
+    __shared__ uint32_t total[kBucketMaxExperts], base[kBucketMaxExperts], own[kBucketMaxExperts];
+    __shared__ uint32_t mask[kBucketMaxExperts * kChunkWords], below[kBucketMaxExperts * kChunkWords];
+    __shared__ uint32_t bad;
+    const uint32_t tid = threadIdx.x, c = blockIdx.x;
+    const uint32_t t0 = c * kChunkTokens;
+    if (tid == 0) bad = 0;
+    for (uint32_t i = tid; i < E * kChunkWords; i += kChunkTokens) mask[i] = 0;
+    __syncthreads();
+    // per expert: the total over chunks and the count of the chunks before c
+    for (uint32_t e = tid; e < E; e += kChunkTokens) {
+        uint32_t tot = 0, pre = 0;
+        for (uint32_t q = 0; q < chunks; ++q) {
+            const uint32_t v = counts[static_cast<uint64_t>(q) * (E + 1) + e];
+            pre += q < c ? v : 0u;
+            tot += v;
+        }
+        total[e] = tot;
+        base[e] = pre;
+        own[e] = counts[static_cast<uint64_t>(c) * (E + 1) + e];
+    }
+    for (uint32_t q = tid; q < chunks; q += kChunkTokens)
+        if (counts[static_cast<uint64_t>(q) * (E + 1) + E]) atomicOr(&bad, 1u);
+    __syncthreads();
+    if (bad) {
+        if (c == 0 && tid == 0) {
+            atomicOr(status, STATUS_BAD_EXPERT);
+            if (tiles) tiles[0] = 0; // nothing downstream runs on these lists
+        }
+        // every position out of range: the gather and the combine skip them
+        const uint64_t i1 = static_cast<uint64_t>(tokens - t0 < kChunkTokens ? tokens : t0 + kChunkTokens) * K;
+        for (uint64_t i = static_cast<uint64_t>(t0) * K + tid; i < i1; i += kChunkTokens) slot_of[i] = 0xFFFFFFFFu;
+        return;
+    }
+    // exclusive scan of the totals over experts by one wavefront (as the
+    // single-workgroup pass); chunk 0 writes the offsets and the tiles
+    if (tid < 64) {
+        constexpr uint32_t kPerLane = kBucketMaxExperts / 64;
+        uint32_t rows = 0, nts = 0;
+#pragma unroll
+        for (uint32_t j = 0; j < kPerLane; ++j) {
+            const uint32_t e = tid * kPerLane + j;
+            const uint32_t v = e < E ? total[e] : 0;
+            rows += v;
+            if (tiles) nts += (v + tile_rows - 1) / tile_rows;
+        }
+        uint32_t rincl = rows, tincl = nts;
+#pragma unroll
+        for (uint32_t d = 1; d < 64; d <<= 1) {
+            const uint32_t rv = __shfl_up(rincl, d), tv = __shfl_up(tincl, d);
+            if (tid >= d) {
+                rincl += rv;
+                tincl += tv;
+            }
+        }
+        uint32_t run = rincl - rows, nt = tincl - nts;
+        for (uint32_t j = 0; j < kPerLane; ++j) {
+            const uint32_t e = tid * kPerLane + j;
+            if (e >= E) break;
+            const uint32_t v = total[e];
+            base[e] += run;
+            if (c == 0) {
+                offsets[e] = run;
+                if (tiles)
+                    for (uint32_t r = 0; r < v; r += tile_rows, ++nt) {
+                        tiles[1 + 3 * nt] = e;
+                        tiles[2 + 3 * nt] = run + r;
+                        tiles[3 + 3 * nt] = v - r < tile_rows ? v - r : tile_rows;
+                    }
+            }
+            run += v;
+        }
+        if (tid == 63 && c == 0) {
+            offsets[E] = rincl;
+            if (tiles) tiles[0] = tincl;
+        }
+    }
+    // the chunk's tokens into per-expert bitmasks
+    const uint32_t t = t0 + tid;
+    const bool live = t < tokens;
+    const uint32_t *tid_ids = ids + static_cast<uint64_t>(live ? t : 0) * K;
+    uint32_t ev[kIdRegs];
+#pragma unroll
+    for (uint32_t r = 0; r < kIdRegs; ++r) ev[r] = live && r < K ? tid_ids[r] : 0;
+    if (live) {
+#pragma unroll
+        for (uint32_t r = 0; r < kIdRegs; ++r)
+            if (r < K) atomicOr(&mask[ev[r] * kChunkWords + (tid >> 5)], 1u << (tid & 31));
+        for (uint32_t r = kIdRegs; r < K; ++r)
+            atomicOr(&mask[tid_ids[r] * kChunkWords + (tid >> 5)], 1u << (tid & 31));
+    }
+    __syncthreads();
+    // per expert, the exclusive prefix of its words' popcounts (8-lane groups)
+    for (uint32_t i = tid; i < E * kChunkWords; i += kChunkTokens) {
+        const uint32_t pc = __builtin_popcount(mask[i]), q = i & (kChunkWords - 1);
+        uint32_t incl = pc;
+#pragma unroll
+        for (uint32_t d = 1; d < kChunkWords; d <<= 1) {
+            const uint32_t v = __shfl_up(incl, d, kChunkWords);
+            if (q >= d) incl += v;
+        }
+        below[i] = incl - pc;
+        // a token that lists one expert twice sets one bit for two counts
+        if (q == kChunkWords - 1 && incl != own[i / kChunkWords]) atomicOr(status, STATUS_BAD_EXPERT);
+    }
+    __syncthreads();
+    if (live) {
+        const uint32_t w = tid >> 5, lowbits = (1u << (tid & 31)) - 1u;
+        auto place = [&](uint32_t r, uint32_t e) {
+            slot_of[static_cast<uint64_t>(t) * K + r] =
+                base[e] + below[e * kChunkWords + w] + __builtin_popcount(mask[e * kChunkWords + w] & lowbits);
+        };
+#pragma unroll
+        for (uint32_t r = 0; r < kIdRegs; ++r)
+            if (r < K) place(r, ev[r]);
+        for (uint32_t r = kIdRegs; r < K; ++r) place(r, tid_ids[r]);
+    }
+}
+
 } // namespace
+
+uint64_t bucket_chunk_counts_bytes(uint32_t tokens, uint32_t experts) {
+    return static_cast<uint64_t>(div_up(tokens, kChunkTokens)) * (experts + 1) * sizeof(uint32_t);
+}
+
+int launch_bucket_chunked(const uint32_t *ids, uint32_t tokens, uint32_t K, uint32_t E, uint32_t *offsets,
+                          uint32_t *slot_of, uint32_t *status, uint32_t *counts, hipStream_t s, uint32_t *tiles,
+                          uint32_t tile_rows) {
+    if (!slot_of || !counts || E == 0 || E > kBucketMaxExperts || (tiles && tile_rows == 0))
+        return FMX_ERR_INVALID_ARGUMENT;
+    if (tokens == 0) return FMX_OK;
+    const uint32_t chunks = div_up(tokens, kChunkTokens);
+    hipLaunchKernelGGL(bucket_count_kernel, dim3(chunks), dim3(kChunkTokens), 0, s, ids, tokens, K, E, counts);
+    FMX_LAUNCH_CHECK();
+    hipLaunchKernelGGL(bucket_place_kernel, dim3(chunks), dim3(kChunkTokens), 0, s, ids, tokens, K, E, chunks, counts,
+                       offsets, slot_of, status, tiles, tile_rows);
+    FMX_LAUNCH_CHECK();
+    return FMX_OK;
+}
 
 size_t bucket_lds_bytes(uint32_t experts) {
     return (2ull * experts + 2ull * experts * kWords) * sizeof(uint32_t);

@@ -52,7 +52,8 @@ DecodeWorkspace decode_workspace(const fmx_moe_layer *L, uint32_t tokens) {
 //   the decode scratch (act of one token) for shapes the GEMMs do not tile |
 //   logits [tokens x experts] f32
 struct PrefillWorkspace {
-    uint64_t h = 0, offsets = 0, token_list = 0, rank_list = 0, slot_of = 0, tiles = 0, x = 0, act = 0, dn = 0,
+    uint64_t h = 0, offsets = 0, token_list = 0, rank_list = 0, slot_of = 0, tiles = 0, chunk_counts = 0, x = 0,
+             act = 0, dn = 0,
              dec_act = 0, logits = 0, total = 0;
     uint32_t pairs = 0, max_tiles = 0;
 };
@@ -71,6 +72,7 @@ PrefillWorkspace prefill_workspace(const fmx_moe_layer *L, uint32_t tokens) {
     w.rank_list = take(P * 4);
     w.slot_of = take(P * 4);
     w.tiles = take((1 + 3ull * w.max_tiles) * 4);
+    w.chunk_counts = take(bucket_chunk_counts_bytes(tokens, L->experts));
     // the GEMMs read 256 rows from every tile's first row: both activation
     // matrices carry that many rows of padding
     w.x = take((P + kPrefillTileRows) * H * 2);
@@ -547,10 +549,10 @@ int prefill_layer(const fmx_moe_layer *L, const float *x, float *out, uint32_t t
     b.act = reinterpret_cast<__bf16 *>(base + ws.act);
     b.dn = reinterpret_cast<float *>(base + ws.dn);
     b.splits = prefill_down_splits(L->experts, L->ffn);
-    if (int rc = launch_bucket(ids, tokens, L->top_k, L->experts, reinterpret_cast<uint32_t *>(base + ws.offsets),
-                               reinterpret_cast<uint32_t *>(base + ws.token_list),
-                               reinterpret_cast<uint32_t *>(base + ws.rank_list), slot_of, status, s,
-                               reinterpret_cast<uint32_t *>(base + ws.tiles), kPrefillTileRows))
+    if (int rc = launch_bucket_chunked(ids, tokens, L->top_k, L->experts,
+                                       reinterpret_cast<uint32_t *>(base + ws.offsets), slot_of, status,
+                                       reinterpret_cast<uint32_t *>(base + ws.chunk_counts), s,
+                                       reinterpret_cast<uint32_t *>(base + ws.tiles), kPrefillTileRows))
         return rc;
     if (int rc = launch_prefill_experts(ea, b, ws.max_tiles, s, kev)) return rc;
     *tiled = true;
