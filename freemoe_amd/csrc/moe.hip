@@ -242,24 +242,270 @@ __device__ Routing wave_route(const RouteArgs &a, const float *__restrict__ logi
     return wave_route_values(a, v, bad);
 }
 
+// ------------------------------------------------- the in-order double sum --
+// The reference's sum of squares is s = 0; s = fl(s + a_i) for i ascending
+// (a_i = x_i^2, exact in double). ordered_sum reproduces it bit for bit with
+// the whole workgroup instead of one lane, by a property of the sequence:
+// while s stays in one binade [2^e, 2^(e+1)), every s is a multiple of
+// u = 2^(e-52) and fl(s + a) = s + q u with q = a / u rounded to an integer
+// (the nearest one; at an exact half the one that makes (s + q u) / u even).
+// So inside a binade the running sum is an integer prefix sum of s / u whose
+// only dependence on s is the parity of s / u at ties: each term is a map
+// (P, p) -> (P + inc[p], out[p]) on (s / u, its parity), maps compose
+// associatively, and a workgroup scan gives every prefix at once, in 64-bit
+// integer arithmetic on the terms' mantissas. The first term that would
+// leave the binade (s + a >= 2^(e+1)) is added by one lane as an ordinary
+// double add from the exact prefix before it, and the next scan starts there
+// in the new binade. The first kSeqTerms terms (where s changes binade
+// often) are added by one lane; a token whose sum leaves its binade more than
+// kMaxScans times finishes in one lane too.
+constexpr uint32_t kSeqTerms = 256;
+constexpr uint32_t kMaxScans = 48;
+constexpr uint64_t kTwo53 = 1ull << 53;
+
+// A term's map: s / u grows by inc0 or inc1 (parity 0 or 1 before the term)
+// and the parity after it is bit 0 / bit 1 of `out`.
+struct SumMap {
+    uint64_t inc0, inc1;
+    uint32_t out;
+};
+
+__device__ inline SumMap sum_map_identity() { return SumMap{0, 0, 2u}; }
+
+// f, then g
+__device__ inline SumMap sum_map_then(const SumMap &f, const SumMap &g) {
+    const uint32_t f0 = f.out & 1u, f1 = f.out >> 1;
+    SumMap r;
+    r.inc0 = f.inc0 + (f0 ? g.inc1 : g.inc0);
+    r.inc1 = f.inc1 + (f1 ? g.inc1 : g.inc0);
+    r.out = ((g.out >> f0) & 1u) | (((g.out >> f1) & 1u) << 1);
+    return r;
+}
+
+// Term a (a double >= 0) in binade e: its map, n = floor(a / u), and whether
+// it leaves the binade by itself (a >= 2^(e+1), infinities and NaN included:
+// then its map only has to be large). a / u = m 2^(Ea - e) for a = m 2^(Ea - 52),
+// m the 53-bit significand, so n is m shifted right by d = e - Ea and the
+// shifted-out bits decide the rounding: above half up, at half a tie.
+__device__ inline SumMap sum_term(double a, int e, uint64_t &n, bool &big) {
+    const uint64_t b = static_cast<uint64_t>(__double_as_longlong(a));
+    const uint32_t be = static_cast<uint32_t>(b >> 52) & 0x7FFu;
+    const uint64_t m = (b & ((1ull << 52) - 1)) | (be ? 1ull << 52 : 0);
+    const int d = e - (static_cast<int>(be) - 1023);
+    big = d < 0;
+    const uint32_t sh = d < 0 ? 0u : d > 63 ? 63u : static_cast<uint32_t>(d);
+    const uint64_t q = m >> sh, r = m & ((1ull << sh) - 1), half = sh ? 1ull << (sh - 1) : 0;
+    const bool wide = d > 63; // a < u / 2 (or a == 0): rounds to nothing
+    n = wide ? 0 : q;
+    const bool up = !wide && sh != 0 && r > half, tie = !wide && sh != 0 && r == half;
+    SumMap f;
+    const uint64_t base = n + (up ? 1u : 0u);
+    f.inc0 = base + (tie ? (n & 1u) : 0u);
+    f.inc1 = base + (tie ? ((n & 1u) ^ 1u) : 0u);
+    f.out = tie ? 0u : ((f.inc0 & 1u) ? 1u : 2u);
+    if (big) f = SumMap{kTwo53, kTwo53, 2u};
+    return f;
+}
+
+// The map of lane - D within this lane's row of 16 (row_shr:D, DPP), the
+// identity for the row's first D lanes.
+template <int D>
+__device__ inline uint32_t row_shr_u32(uint32_t v, uint32_t fill) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(static_cast<int>(fill), static_cast<int>(v), 0x110 + D, 0xF, 0xF, false));
+}
+template <int D>
+__device__ inline uint64_t row_shr_u64(uint64_t v) {
+    return (static_cast<uint64_t>(row_shr_u32<D>(static_cast<uint32_t>(v >> 32), 0)) << 32) |
+           row_shr_u32<D>(static_cast<uint32_t>(v), 0);
+}
+template <int D>
+__device__ inline SumMap row_shr_map(const SumMap &g) {
+    return SumMap{row_shr_u64<D>(g.inc0), row_shr_u64<D>(g.inc1), row_shr_u32<D>(g.out, 2u)};
+}
+__device__ inline SumMap readlane_map(const SumMap &g, int lane) {
+    auto rd64 = [lane](uint64_t v) {
+        const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(v), lane);
+        const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(v >> 32), lane);
+        return (static_cast<uint64_t>(hi) << 32) | lo;
+    };
+    return SumMap{rd64(g.inc0), rd64(g.inc1), static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(g.out), lane))};
+}
+
+// The composition of the maps of the lanes below this one (exclusive scan
+// over the wavefront) and of all 64 (*total): a scan inside each row of 16
+// lanes by DPP row shifts, then the rows' totals read out and put in front.
+__device__ inline SumMap wave_scan_maps(SumMap g, SumMap *total) {
+    g = sum_map_then(row_shr_map<1>(g), g);
+    g = sum_map_then(row_shr_map<2>(g), g);
+    g = sum_map_then(row_shr_map<4>(g), g);
+    g = sum_map_then(row_shr_map<8>(g), g);
+    const SumMap below_in_row = row_shr_map<1>(g);
+    const SumMap r0 = readlane_map(g, 15), r1 = readlane_map(g, 31), r2 = readlane_map(g, 47), r3 = readlane_map(g, 63);
+    const SumMap p2 = sum_map_then(r0, r1), p3 = sum_map_then(p2, r2);
+    *total = sum_map_then(p3, r3);
+    const uint32_t row = (threadIdx.x & 63) >> 4;
+    const SumMap rows_before = row == 0 ? sum_map_identity() : row == 1 ? r0 : row == 2 ? p2 : p3;
+    return sum_map_then(rows_before, below_in_row);
+}
+
+__device__ inline uint32_t wave_min_u32(uint32_t v) {
+    v = min(v, lane_xor_u32<1>(v));
+    v = min(v, lane_xor_u32<2>(v));
+    v = min(v, lane_xor_u32<4>(v));
+    v = min(v, lane_xor_u32<8>(v));
+    uint32_t a, b;
+    lane_pair_u32<16>(v, a, b);
+    v = min(a, b);
+    lane_pair_u32<32>(v, a, b);
+    return min(a, b);
+}
+
+struct OrderedSumShared {
+    double s;          // the running sum
+    uint32_t next;     // the first term not yet in it
+    SumMap wave_total[16];
+    uint32_t wave_first[16]; // per wavefront: the first term leaving the binade
+};
+
+// sum(a_j, j = 0 .. n-1) in index order, bit for bit, by all NT threads (a
+// in LDS, n <= 16 NT). Every thread calls it and gets the sum; it ends after
+// a barrier. Out of line: inlined, its registers would be allocated around
+// the callers' common path too. Each scan covers a window of the next c NT terms (c per thread,
+// c about 1.5 next / NT: while the terms are alike, s leaves its binade about
+// when the count of terms in it has doubled); a window with no term leaving
+// the binade still ends exact, and the next scan starts after it.
+template <uint32_t NT>
+__device__ __attribute__((noinline)) double ordered_sum(const double *a, uint32_t n, OrderedSumShared &sh) {
+    static_assert(NT % 64 == 0 && NT / 64 <= 16, "one to sixteen wavefronts");
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) {
+        // the first terms in one lane, 8 LDS reads requested ahead of the
+        // adds they feed; then on while the sum is still 0
+        constexpr uint32_t kB = 8;
+        const uint32_t lead = n < kSeqTerms ? n : kSeqTerms, nb = lead / kB;
+        double s = 0.0, buf[2][kB];
+        if (nb > 0) {
+#pragma unroll
+            for (uint32_t q = 0; q < kB; ++q) buf[0][q] = a[q];
+        }
+        for (uint32_t bi = 0; bi < nb; bi += 2) {
+#pragma unroll
+            for (uint32_t half = 0; half < 2; ++half) {
+                const uint32_t b = bi + half;
+                if (b >= nb) break;
+                const uint32_t nx = (b + 1 < nb ? b + 1 : b) * kB;
+#pragma unroll
+                for (uint32_t q = 0; q < kB; ++q) buf[half ^ 1][q] = a[nx + q];
+#pragma unroll
+                for (uint32_t q = 0; q < kB; ++q) s += buf[half][q];
+            }
+        }
+        uint32_t i = nb * kB;
+        while (i < n && (i < lead || s == 0.0)) s += a[i++];
+        sh.s = s;
+        sh.next = i;
+    }
+    __syncthreads();
+    for (uint32_t scan = 0;; ++scan) {
+        const double s = sh.s;
+        const uint32_t next = sh.next;
+        if (next >= n) break;
+        if (!__builtin_isfinite(s) || scan >= kMaxScans) {
+            __syncthreads();
+            if (tid == 0) {
+                double r = s;
+                for (uint32_t i = next; i < n; ++i) r += a[i];
+                sh.s = r;
+            }
+            __syncthreads();
+            break;
+        }
+        // s > 0 and normal: its binade e and s / u = its significand
+        const uint64_t sb = static_cast<uint64_t>(__double_as_longlong(s));
+        const int e = static_cast<int>((sb >> 52) & 0x7FFu) - 1023;
+        const uint64_t P0 = (sb & ((1ull << 52) - 1)) | (1ull << 52);
+        const uint32_t p0 = static_cast<uint32_t>(P0 & 1u);
+        // the window [next, end) and this thread's terms [j0, j1) of it
+        const uint32_t c0 = (next + next / 2 + NT - 1) / NT, c = c0 < 1 ? 1 : c0 > 16 ? 16 : c0;
+        const uint32_t end = n - next < c * NT ? n : next + c * NT;
+        const uint32_t j0 = next + tid * c < end ? next + tid * c : end, j1 = end - j0 < c ? end : j0 + c;
+        SumMap g = sum_map_identity();
+#pragma unroll 4
+        for (uint32_t j = j0; j < j1; ++j) {
+            uint64_t nj;
+            bool big;
+            g = sum_map_then(g, sum_term(a[j], e, nj, big));
+        }
+        SumMap total;
+        const SumMap before = wave_scan_maps(g, &total);
+        if (lane == 0) sh.wave_total[wave] = total;
+        __syncthreads();
+        // this thread's starting (s / u, parity): the earlier wavefronts, then
+        // the earlier lanes of this one
+        uint64_t P = P0;
+        uint32_t p = p0;
+        for (uint32_t w = 0; w < wave; ++w) {
+            const SumMap &t = sh.wave_total[w];
+            P += p ? t.inc1 : t.inc0;
+            p = (t.out >> p) & 1u;
+        }
+        P += p ? before.inc1 : before.inc0;
+        p = (before.out >> p) & 1u;
+        uint32_t mine = n;
+        double s_first = 0.0;
+#pragma unroll 4
+        for (uint32_t j = j0; j < j1; ++j) {
+            const double aj = a[j];
+            uint64_t nj;
+            bool big;
+            const SumMap m = sum_term(aj, e, nj, big);
+            if (big || P + nj >= kTwo53) {
+                mine = j;
+                // the reference's add, from the exact prefix (P < 2^53)
+                s_first = ldexp(static_cast<double>(P), e - 52) + aj;
+                break;
+            }
+            P += p ? m.inc1 : m.inc0;
+            p = (m.out >> p) & 1u;
+        }
+        const uint32_t first = wave_min_u32(mine);
+        if (lane == 0) sh.wave_first[wave] = first;
+        __syncthreads();
+        uint32_t f = sh.wave_first[0];
+        for (uint32_t w = 1; w < NT / 64; ++w) f = min(f, sh.wave_first[w]);
+        if (f == n) {
+            // no term of the window leaves the binade: the thread holding the
+            // window's last term has its sum (P <= 2^53, exact in double)
+            if (j1 == end && j0 < j1) {
+                sh.s = ldexp(static_cast<double>(P), e - 52);
+                sh.next = end;
+            }
+        } else if (mine == f) {
+            sh.s = s_first;
+            sh.next = f + 1;
+        }
+        __syncthreads();
+    }
+    return sh.s;
+}
+
 // RMSNorm (engine.cpp:723-740) of one token held P float4 per thread
 // (element 4 (tid + i NT) + j in xv[i], its gain in gv[i]) into hv[4 i + j].
 // The reference's sum of squares is a sequential double sum; here it is a
 // parallel sum plus a certificate: every normalised value is checked to lie
 // farther from a float rounding boundary than the worst-case difference
-// between the two sums can move it; only when one is that close does one lane
-// redo the sum in the reference's order, from a copy of x in `scratch` (LDS,
-// at least hidden floats, 16-byte aligned), or with kSquares from the squares
-// (exact in double) written there (at least 2 hidden floats), the one lane
-// then running nothing but the chain of adds. Either way hv is the
-// reference's h bit for bit. Every thread of the workgroup calls it; it ends
-// after a barrier.
-template <uint32_t NT, uint32_t P, bool kSquares = false>
+// between the two sums can move it; only when one is that close does the
+// workgroup redo the sum in the reference's order (ordered_sum) from the
+// squares (exact in double) written to `scratch` (LDS, at least 2 hidden
+// floats, 16-byte aligned). Either way hv is the reference's h bit for bit.
+// Every thread of the workgroup calls it; it ends after a barrier.
+template <uint32_t NT, uint32_t P>
 __device__ __forceinline__ void token_rmsnorm(const RouteArgs &a, const float4 (&xv)[P], const float4 (&gv)[P],
                                               bool has_gain, float (&hv)[4 * P], float *scratch) {
     __shared__ double wave_part[NT / 64];
-    __shared__ double ss_s;
     __shared__ int unsafe_s;
+    __shared__ OrderedSumShared osum;
     const uint32_t H = a.hidden, tid = threadIdx.x, H4 = H / 4;
     double part = 0.0;
 #pragma unroll
@@ -301,76 +547,20 @@ __device__ __forceinline__ void token_rmsnorm(const RouteArgs &a, const float4 (
         if (__any(unsafe) && (tid & 63) == 0) unsafe_s = 1;
         __syncthreads();
         if (!unsafe_s) break;
-        if (kSquares) {
-            // every thread writes its squares into LDS, then one lane adds
-            // them in order, its operands requested one batch (16 adds) ahead
-            double2 *tl = reinterpret_cast<double2 *>(scratch);
+        // the squares into LDS, then the sum in the reference's order
+        double2 *tl = reinterpret_cast<double2 *>(scratch);
 #pragma unroll
-            for (uint32_t i = 0; i < P; ++i) {
-                const uint32_t q = tid + i * NT;
-                if (q < H4) {
-                    tl[2 * q] = make_double2(static_cast<double>(xv[i].x) * static_cast<double>(xv[i].x),
-                                             static_cast<double>(xv[i].y) * static_cast<double>(xv[i].y));
-                    tl[2 * q + 1] = make_double2(static_cast<double>(xv[i].z) * static_cast<double>(xv[i].z),
-                                                 static_cast<double>(xv[i].w) * static_cast<double>(xv[i].w));
-                }
+        for (uint32_t i = 0; i < P; ++i) {
+            const uint32_t q = tid + i * NT;
+            if (q < H4) {
+                tl[2 * q] = make_double2(static_cast<double>(xv[i].x) * static_cast<double>(xv[i].x),
+                                         static_cast<double>(xv[i].y) * static_cast<double>(xv[i].y));
+                tl[2 * q + 1] = make_double2(static_cast<double>(xv[i].z) * static_cast<double>(xv[i].z),
+                                             static_cast<double>(xv[i].w) * static_cast<double>(xv[i].w));
             }
-            __syncthreads();
-            if (tid == 0) {
-                constexpr uint32_t kB = 8; // double2 per batch
-                const uint32_t n2 = 2 * H4, nb = n2 / kB;
-                double2 buf[2][kB];
-                double s = 0.0;
-                if (nb > 0) {
-#pragma unroll
-                    for (uint32_t q = 0; q < kB; ++q) buf[0][q] = tl[q];
-                }
-                for (uint32_t bi = 0; bi < nb; bi += 2) {
-#pragma unroll
-                    for (uint32_t half = 0; half < 2; ++half) {
-                        const uint32_t b = bi + half;
-                        if (b >= nb) break;
-                        const uint32_t nx = (b + 1 < nb ? b + 1 : b) * kB;
-#pragma unroll
-                        for (uint32_t q = 0; q < kB; ++q) buf[half ^ 1][q] = tl[nx + q];
-#pragma unroll
-                        for (uint32_t q = 0; q < kB; ++q) {
-                            s += buf[half][q].x;
-                            s += buf[half][q].y;
-                        }
-                    }
-                }
-                for (uint32_t q = nb * kB; q < n2; ++q) {
-                    const double2 v = tl[q];
-                    s += v.x;
-                    s += v.y;
-                }
-                ss_s = s;
-            }
-            __syncthreads();
-            ss = ss_s;
-            continue;
-        }
-        // the reference's order: x into LDS, one lane sums it
-        float4 *xl = reinterpret_cast<float4 *>(scratch);
-#pragma unroll
-        for (uint32_t i = 0; i < P; ++i)
-            if (tid + i * NT < H4) xl[tid + i * NT] = xv[i];
-        __syncthreads();
-        if (tid == 0) {
-            double s = 0.0;
-#pragma unroll 8
-            for (uint32_t q = 0; q < H4; ++q) {
-                const float4 v = xl[q];
-                s += static_cast<double>(v.x) * static_cast<double>(v.x);
-                s += static_cast<double>(v.y) * static_cast<double>(v.y);
-                s += static_cast<double>(v.z) * static_cast<double>(v.z);
-                s += static_cast<double>(v.w) * static_cast<double>(v.w);
-            }
-            ss_s = s;
         }
         __syncthreads();
-        ss = ss_s;
+        ss = ordered_sum<NT>(reinterpret_cast<const double *>(scratch), H, osum);
     }
 }
 
@@ -483,7 +673,7 @@ __global__ __launch_bounds__(NT) __attribute__((aligned(kHotAlign))) void route_
         gv[i] = g4[qc];
     }
     float hv[4 * P];
-    token_rmsnorm<NT, P>(a, xv, gv, has_gain, hv, rs);
+    token_rmsnorm<NT, P>(a, xv, gv, has_gain, hv, lds); // hs and rs: see route_lds_bytes
     // h and the router row into the chain layout
 #pragma unroll
     for (uint32_t i = 0; i < P; ++i) {
@@ -509,7 +699,8 @@ __global__ __launch_bounds__(NT) __attribute__((aligned(kHotAlign))) void route_
 }
 
 // RMSNorm of token blockIdx.x into h (batched routing). NT threads, 4 float4
-// per thread (hidden <= 16 NT); LDS: 2 hidden floats for the in-order fallback.
+// per thread (hidden <= 16 NT); LDS: 2 hidden floats (the squares, for the
+// in-order sum when the certificate fails).
 template <uint32_t NT>
 __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *__restrict__ x,
                                                      float *__restrict__ h) {
@@ -528,7 +719,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *_
         gv[i] = g4[qc];
     }
     float hv[4 * P];
-    token_rmsnorm<NT, P, true>(a, xv, gv, has_gain, hv, lds);
+    token_rmsnorm<NT, P>(a, xv, gv, has_gain, hv, lds);
     float4 *h4 = reinterpret_cast<float4 *>(h + static_cast<uint64_t>(t) * H);
 #pragma unroll
     for (uint32_t i = 0; i < P; ++i) {
@@ -1112,6 +1303,8 @@ int allow_lds(const void *fn, size_t bytes) {
     return FMX_OK;
 }
 
+// route_rows_kernel's LDS: h and the router row in chain layout (32 cs >= 2
+// hidden floats, which first hold the squares of an in-order sum of squares).
 size_t route_lds_bytes(uint32_t hidden) { return 2ull * 16 * route_chain_stride(hidden) * sizeof(float); }
 
 // RMSNorm of `tokens` rows of x into h: one workgroup per token.

@@ -182,6 +182,71 @@ def test_rmsnorm_in_order_sum_across_inputs(gpu, kind):
     assert check_layer(gpu, lw, x) == 0
 
 
+def replay_inputs(kind, T, H, rng):
+    """T tokens of hidden H whose squares' in-order sum exercises the
+    workgroup replay: plain normals, values with three fraction bits and with
+    random trailing zero bits (their squares' sums meet exact rounding ties),
+    values spread over 2^-40 .. 2^40 (the sum changes binade often) and a
+    first half of zeros (the sum stays 0 for a while)."""
+    v = rng.standard_normal((T, H)).astype(np.float32)
+    if kind == "three_fraction_bits":
+        v = np.round(v * 8) / np.float32(8)
+    elif kind == "trailing_zeros":
+        b = v.view(np.uint32) & ~((np.uint32(1) << rng.integers(0, 24, (T, H)).astype(np.uint32)) - np.uint32(1))
+        v = b.view(np.float32)
+    elif kind == "wide":
+        v = (v * np.exp2(rng.uniform(-40, 40, (T, H)))).astype(np.float32)
+    elif kind == "leading_zeros":
+        v[:, : H // 2] = 0.0
+    return np.ascontiguousarray(v, dtype=np.float32)
+
+
+def near_midpoint_tokens(x, lw):
+    """Tokens with an element whose in-order x*scale*gain lies within the
+    device certificate's tolerance of a float midpoint: the device cannot
+    settle those by its parallel sum, so they take the in-order replay."""
+    import near_ties as nt
+    H = x.shape[1]
+    rel = 0.6e-16 * (H + 32) + 2e-15
+    near = []
+    for t in range(x.shape[0]):
+        yd = nt.in_order_rmsnorm_double(x[t], lw.norm_weight, lw.rms_eps)
+        if (nt.midpoint_distance(yd) <= rel).any():
+            near.append(t)
+    return near
+
+
+@pytest.mark.parametrize("kind", ["normal", "three_fraction_bits", "trailing_zeros", "wide", "leading_zeros"])
+@pytest.mark.parametrize("H", [2048, 4096, 8192])
+def test_rmsnorm_in_order_replay_many_tokens(gpu, kind, H):
+    """The in-order sum of squares, replayed by the whole workgroup (binade by
+    binade) where the parallel sum cannot be certified: h bit for bit against
+    the oracle's RMSNorm for every token of a 1024-token batch (the batched
+    RMSNorm kernel, 0.4-10% of whose tokens lie near a float midpoint) and
+    for single-token routes (the decode routing kernel) of up to 48 of the
+    near tokens and 8 others."""
+    import torch
+    lw = wl.make_layer(H, 256, 8, 2, wl.Q4_0, 51)
+    rng = np.random.default_rng(H + len(kind))
+    x = replay_inputs(kind, 1024, H, rng)
+    near = near_midpoint_tokens(x, lw)
+    dl = DeviceLayer(lw, gpu)
+    h, _, _, _ = dl.route(torch.from_numpy(x).to(gpu))
+    torch.cuda.synchronize()
+    assert dl.status() == 0
+    got = bits(to_np(h))
+    for t in range(x.shape[0]):
+        want = fo.rmsnorm(x[t], lw.norm_weight, lw.rms_eps)
+        assert np.array_equal(got[t], bits(want)), f"batched h token {t}"
+    for t in near[:48] + list(range(8)):
+        h1, _, _, _ = dl.route(torch.from_numpy(x[t:t + 1]).to(gpu))
+        torch.cuda.synchronize()
+        want = fo.rmsnorm(x[t], lw.norm_weight, lw.rms_eps)
+        assert np.array_equal(bits(to_np(h1[0])), bits(want)), f"single-token h token {t}"
+    print(f"{kind} hidden {H}: {len(near)} of 1024 tokens near a midpoint")
+    assert len(near) >= 3
+
+
 def large_value_layer(gain_log2, gate_scale_bits):
     """A Q4_0 layer whose h (or act) holds values of 2^70 .. 2^106: element 5
     of h is about 2^gain_log2 (its RMSNorm gain; x[:, 5] = 1 and the router
