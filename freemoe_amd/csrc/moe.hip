@@ -145,7 +145,8 @@ struct Routing {
 // Routing of one token from its E <= 256 router logits, by one wavefront
 // (every lane calls it; lane r < top_k receives rank r):
 //   softmax (engine.cpp:378-393): float max, double exp(v - max) summed in
-//   index order, float quotients;
+//   index order (or, kCertified, a certified wavefront sum where that gives
+//   the same quotients), float quotients;
 //   stable top-k (engine.cpp:395-411): the highest probability first, ties to
 //   the lower index; picked as the wave maximum of (probability bits, ~index),
 //   which orders non-negative floats and breaks ties the same way;
@@ -166,8 +167,9 @@ __device__ __forceinline__ void route_logits_load(const RouteArgs &a, const floa
     }
 }
 
-// wave_route from logits already loaded by route_logits_load.
-template <int kSlots = 4>
+// wave_route from logits already loaded by route_logits_load. kCertified:
+// the softmax sum as a certified wavefront sum (worth it for many experts).
+template <int kSlots = 4, bool kCertified = false>
 __device__ Routing wave_route_values(const RouteArgs &a, const float (&v)[kSlots], bool *bad) {
     const uint32_t E = a.experts, K = a.top_k, lane = threadIdx.x & 63;
     bool nonfinite = false;
@@ -193,12 +195,34 @@ __device__ Routing wave_route_values(const RouteArgs &a, const float (&v)[kSlots
 #pragma unroll
     for (int j = 0; j < kSlots; ++j)
         ex[j] = lane + 64 * j < E ? exp(static_cast<double>(v[j]) - static_cast<double>(m)) : 0.0;
+    // The reference's sum is sequential in index order (readlane by
+    // readlane here). kCertified: a wavefront sum first, with a certificate
+    // as for RMSNorm: the two sums of E terms in (0, 1] differ by at most
+    // (E + kSlots + 5) 2^-53 of the sum, which moves each quotient by that
+    // much plus its own rounding; only when a quotient lies that close to a
+    // float rounding boundary is the sum taken in order.
     double sum = 0.0;
+    bool in_order = true;
+    if constexpr (kCertified) {
+        double part = 0.0;
 #pragma unroll
-    for (int j = 0; j < kSlots; ++j) {
-        if (64u * j >= E) break;
-        const uint32_t n = E - 64 * j < 64 ? E - 64 * j : 64;
-        for (uint32_t i = 0; i < n; ++i) sum += readlane_double(ex[j], i);
+        for (int j = 0; j < kSlots; ++j) part += ex[j];
+        sum = wave_sum_double(part);
+        const double rel_tol = 1.2e-16 * static_cast<double>(E + 2 * kSlots + 10);
+        const uint32_t tol0 = static_cast<uint32_t>(ceil(rel_tol * 4503599627370496.0)); // rel_tol * 2^52
+        bool unsafe = false;
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j) unsafe |= (lane + 64 * j < E) & rounding_unsafe(ex[j] / sum, tol0);
+        in_order = __any(unsafe);
+    }
+    if (in_order) {
+        sum = 0.0;
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j) {
+            if (64u * j >= E) break;
+            const uint32_t n = E - 64 * j < 64 ? E - 64 * j : 64;
+            for (uint32_t i = 0; i < n; ++i) sum += readlane_double(ex[j], i);
+        }
     }
     uint64_t key[kSlots];
 #pragma unroll
@@ -235,11 +259,11 @@ __device__ Routing wave_route_values(const RouteArgs &a, const float (&v)[kSlots
     return r;
 }
 
-template <int kSlots = 4>
+template <int kSlots = 4, bool kCertified = false>
 __device__ Routing wave_route(const RouteArgs &a, const float *__restrict__ logits, bool *bad) {
     float v[kSlots];
     route_logits_load(a, logits, v);
-    return wave_route_values(a, v, bad);
+    return wave_route_values<kSlots, kCertified>(a, v, bad);
 }
 
 // ------------------------------------------------- the in-order double sum --
@@ -739,15 +763,17 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *_
 // take small tiles (2 tokens x 8 or 16 rows) so that the grid still covers
 // the device; many take 16 x 32 (4 x 8 pairs per lane). grid:
 // (ceil(tokens / TT), ceil(experts / TR)).
-constexpr uint32_t kRtPad = 20; // floats per (token or row, chain) in LDS: 16 steps + 4
+constexpr uint32_t kRtPad = 20;                   // floats per (token or row, chain) in LDS: 16 steps + 4
+constexpr uint32_t kRtRowExtra = 0;               // floats after each token's or row's 16 chains
+constexpr uint32_t kRtRow = 16 * kRtPad + kRtRowExtra; // floats per token or row
 template <uint32_t PT, uint32_t PR, uint32_t GT>
 __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const float *__restrict__ h,
                                                           uint32_t tokens, float *__restrict__ logits,
                                                           uint32_t *__restrict__ ids, float *__restrict__ weights,
                                                           uint32_t *__restrict__ status) {
     constexpr uint32_t GR = 16 / GT, TT = GT * PT, TR = GR * PR;
-    __shared__ __align__(16) float hl[TT][16][kRtPad];
-    __shared__ __align__(16) float wl[TR][16][kRtPad];
+    __shared__ __align__(16) float hl[TT * kRtRow];
+    __shared__ __align__(16) float wl[TR * kRtRow];
     __shared__ float lg[TT][TR];
     const uint32_t H = a.hidden, E = a.experts, tid = threadIdx.x;
     const uint32_t c = tid & 15, g = tid >> 4;
@@ -781,11 +807,11 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
             const uint32_t q = tid + 256 * i;
             if (kItems % 256 != 0 && q >= kItems) break;
             const uint32_t row = q / 64, f = q % 64, s0 = f >> 2, c0 = 4 * (f & 3);
-            float(*dst)[kRtPad] = row < TT ? hl[row] : wl[row - TT];
-            dst[c0][s0] = sv[i].x;
-            dst[c0 + 1][s0] = sv[i].y;
-            dst[c0 + 2][s0] = sv[i].z;
-            dst[c0 + 3][s0] = sv[i].w;
+            float *dst = (row < TT ? hl + row * kRtRow : wl + (row - TT) * kRtRow) + c0 * kRtPad + s0;
+            dst[0] = sv[i].x;
+            dst[kRtPad] = sv[i].y;
+            dst[2 * kRtPad] = sv[i].z;
+            dst[3 * kRtPad] = sv[i].w;
         }
     };
     float acc[PT][PR];
@@ -802,9 +828,9 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
         for (uint32_t s4 = 0; s4 < steps; s4 += 4) {
             float4 hq[PT], wq[PR];
 #pragma unroll
-            for (uint32_t i = 0; i < PT; ++i) hq[i] = *reinterpret_cast<const float4 *>(&hl[tg + i][c][s4]);
+            for (uint32_t i = 0; i < PT; ++i) hq[i] = *reinterpret_cast<const float4 *>(&hl[(tg + i) * kRtRow + c * kRtPad + s4]);
 #pragma unroll
-            for (uint32_t j = 0; j < PR; ++j) wq[j] = *reinterpret_cast<const float4 *>(&wl[rg + j][c][s4]);
+            for (uint32_t j = 0; j < PR; ++j) wq[j] = *reinterpret_cast<const float4 *>(&wl[(rg + j) * kRtRow + c * kRtPad + s4]);
             const uint32_t ns = steps - s4 < 4 ? steps - s4 : 4;
 #pragma unroll
             for (uint32_t u = 0; u < 4; ++u) {
@@ -867,7 +893,7 @@ __global__ __launch_bounds__(64) void route_finish_kernel(RouteArgs a, const flo
                                                           uint32_t *__restrict__ status) {
     const uint32_t t = blockIdx.x, lane = threadIdx.x;
     bool bad;
-    const Routing r = wave_route(a, logits + static_cast<uint64_t>(t) * a.experts, &bad);
+    const Routing r = wave_route<4, true>(a, logits + static_cast<uint64_t>(t) * a.experts, &bad);
     if (lane < a.top_k) {
         ids[static_cast<uint64_t>(t) * a.top_k + lane] = r.id;
         weights[static_cast<uint64_t>(t) * a.top_k + lane] = r.weight;

@@ -247,6 +247,79 @@ def test_rmsnorm_in_order_replay_many_tokens(gpu, kind, H):
     assert len(near) >= 3
 
 
+def one_hot_router_layer(H, E, K, seed, logits):
+    """A layer whose router row e holds one nonzero weight, at element e, so
+    that expert e's logit is float(h[e] * c_e) exactly on every path; c_e is
+    chosen from the oracle's h of token `x` to give about `logits`."""
+    lw = wl.make_layer(H, 128, E, K, wl.Q8_0, seed)
+    x = wl.inputs(H, 4, seed + 1)
+    h = host_layer(lw).route(x[0])[0]
+    lw.router = np.zeros((E, H), np.float32)
+    lw.router[np.arange(E), np.arange(E)] = (logits / h[:E]).astype(np.float32)
+    return lw, x, h
+
+
+def softmax_quotients(v):
+    """The reference's softmax quotients e_t / sum in double (before the
+    float rounding): float max, exp in double, the sum in index order."""
+    import math
+    m = float(np.max(v))
+    ex = np.array([math.exp(float(t) - m) for t in v])
+    return ex / np.cumsum(ex)[-1]
+
+
+def test_route_softmax_sum_certificate_and_in_order_sum(gpu):
+    """128 experts: the softmax sum of the many-expert routing kernel is a
+    certified wavefront sum. A token crafted so that one quotient lies within
+    1e-14 of a float midpoint (the certificate must send it to the in-order
+    sum), one whose quotients include a subnormal float (always in order), and
+    plain tokens: logits, ids and weights bit for bit against the oracle on
+    the batched route."""
+    import torch
+    import near_ties as nt
+    H, E, K = 256, 128, 8
+    rng = np.random.default_rng(71)
+    base = rng.standard_normal(E).astype(np.float32)
+    # search the last expert's logit for a quotient next to a midpoint
+    lw, x, h = one_hot_router_layer(H, E, K, 73, base)
+    base = (np.diag(lw.router)[:E] * h[:E]).astype(np.float32)  # the logits the kernels compute
+    found = None
+    for start in range(0, 400_000, 2048):
+        cand = (base[-1] * (1.0 + (np.arange(start, start + 2048) * 2.0 ** -22))).astype(np.float32)
+        c = (cand / h[E - 1]).astype(np.float32)
+        last = (c * np.float32(h[E - 1])).astype(np.float32)  # the logit float(c * h) the kernels compute
+        V = np.repeat(base[None, :], len(cand), 0)
+        V[:, -1] = last
+        m = V.max(axis=1, keepdims=True).astype(np.float64)
+        ex = np.exp(V.astype(np.float64) - m)
+        q = ex / np.cumsum(ex, axis=1)[:, -1:]
+        d = nt.midpoint_distance(q.ravel()).reshape(q.shape).min(axis=1)
+        i = int(np.argmin(d))
+        if d[i] < 5e-15:
+            found = c[i]
+            break
+    assert found is not None, "no near-midpoint quotient found"
+    lw.router[E - 1, E - 1] = found
+    logits0 = host_layer(lw).route(x[0])[1]
+    dist = nt.midpoint_distance(softmax_quotients(logits0)).min()
+    assert dist < 1e-14, dist
+    # a second layer: one expert's logit 95 below the largest, a subnormal quotient
+    sub = base.copy()
+    sub[5] = base.max() - np.float32(95.0)
+    lw2, x2, _ = one_hot_router_layer(H, E, K, 75, sub)
+    for layer, xs in ((lw, x), (lw2, x2)):
+        dl = DeviceLayer(layer, gpu)
+        hd, lg, ids, w = dl.route(torch.from_numpy(xs).to(gpu))
+        torch.cuda.synchronize()
+        assert dl.status() == 0
+        hl = host_layer(layer)
+        for t in range(len(xs)):
+            hh, ll, _, ii, ww = hl.route(xs[t])
+            assert np.array_equal(bits(to_np(lg[t])), bits(ll)), f"logits token {t}"
+            assert np.array_equal(to_np(ids[t]).astype(np.uint32), ii), f"ids token {t}"
+            assert np.array_equal(bits(to_np(w[t])), bits(ww)), f"weights token {t}"
+
+
 def large_value_layer(gain_log2, gate_scale_bits):
     """A Q4_0 layer whose h (or act) holds values of 2^70 .. 2^106: element 5
     of h is about 2^gain_log2 (its RMSNorm gain; x[:, 5] = 1 and the router
