@@ -228,7 +228,8 @@ __global__ __launch_bounds__(kChunkTokens) void bucket_count_kernel(const uint32
 __global__ __launch_bounds__(kChunkTokens) void bucket_place_kernel(
     const uint32_t *__restrict__ ids, uint32_t tokens, uint32_t K, uint32_t E, uint32_t chunks,
     const uint32_t *__restrict__ counts, uint32_t *__restrict__ offsets, uint32_t *__restrict__ slot_of,
-    uint32_t *__restrict__ status, uint32_t *__restrict__ tiles, uint32_t tile_rows) {
+    uint32_t *__restrict__ token_list, uint32_t *__restrict__ status, uint32_t *__restrict__ tiles,
+    uint32_t tile_rows) {
     __shared__ uint32_t total[kBucketMaxExperts], base[kBucketMaxExperts], own[kBucketMaxExperts];
     __shared__ uint32_t mask[kBucketMaxExperts * kChunkWords], below[kBucketMaxExperts * kChunkWords];
     __shared__ uint32_t bad;
@@ -337,8 +338,10 @@ __global__ __launch_bounds__(kChunkTokens) void bucket_place_kernel(
     if (live) {
         const uint32_t w = tid >> 5, lowbits = (1u << (tid & 31)) - 1u;
         auto place = [&](uint32_t r, uint32_t e) {
-            slot_of[static_cast<uint64_t>(t) * K + r] =
+            const uint32_t pos =
                 base[e] + below[e * kChunkWords + w] + __builtin_popcount(mask[e * kChunkWords + w] & lowbits);
+            slot_of[static_cast<uint64_t>(t) * K + r] = pos;
+            if (token_list) token_list[pos] = t;
         };
 #pragma unroll
         for (uint32_t r = 0; r < kIdRegs; ++r)
@@ -354,8 +357,8 @@ uint64_t bucket_chunk_counts_bytes(uint32_t tokens, uint32_t experts) {
 }
 
 int launch_bucket_chunked(const uint32_t *ids, uint32_t tokens, uint32_t K, uint32_t E, uint32_t *offsets,
-                          uint32_t *slot_of, uint32_t *status, uint32_t *counts, hipStream_t s, uint32_t *tiles,
-                          uint32_t tile_rows) {
+                          uint32_t *slot_of, uint32_t *token_list, uint32_t *status, uint32_t *counts, hipStream_t s,
+                          uint32_t *tiles, uint32_t tile_rows) {
     if (!slot_of || !counts || E == 0 || E > kBucketMaxExperts || (tiles && tile_rows == 0))
         return FMX_ERR_INVALID_ARGUMENT;
     if (tokens == 0) return FMX_OK;
@@ -363,7 +366,7 @@ int launch_bucket_chunked(const uint32_t *ids, uint32_t tokens, uint32_t K, uint
     hipLaunchKernelGGL(bucket_count_kernel, dim3(chunks), dim3(kChunkTokens), 0, s, ids, tokens, K, E, counts);
     FMX_LAUNCH_CHECK();
     hipLaunchKernelGGL(bucket_place_kernel, dim3(chunks), dim3(kChunkTokens), 0, s, ids, tokens, K, E, chunks, counts,
-                       offsets, slot_of, status, tiles, tile_rows);
+                       offsets, slot_of, token_list, status, tiles, tile_rows);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }

@@ -48,7 +48,8 @@ DecodeWorkspace decode_workspace(const fmx_moe_layer *L, uint32_t tokens) {
 // Prefill workspace (all offsets 256-byte aligned), pairs = tokens * top_k:
 //   [0, 256) error word | h [tokens x hidden] f32 | offsets [experts + 1] |
 //   token_list, rank_list, slot_of [pairs] | row tiles [1 + 3 * max_tiles] |
-//   x [pairs x hidden] bf16 | act [pairs x ffn] bf16 | dn [splits x pairs x hidden] f32 |
+//   chunk counts | x [tokens x hidden] bf16 | act [pairs + 192 rows x ffn] bf16 |
+//   dn [splits x pairs x hidden] f32 |
 //   the decode scratch (act of one token) for shapes the GEMMs do not tile |
 //   logits [tokens x experts] f32
 struct PrefillWorkspace {
@@ -73,9 +74,10 @@ PrefillWorkspace prefill_workspace(const fmx_moe_layer *L, uint32_t tokens) {
     w.slot_of = take(P * 4);
     w.tiles = take((1 + 3ull * w.max_tiles) * 4);
     w.chunk_counts = take(bucket_chunk_counts_bytes(tokens, L->experts));
-    // the GEMMs read 256 rows from every tile's first row: both activation
-    // matrices carry that many rows of padding
-    w.x = take((P + kPrefillTileRows) * H * 2);
+    // h in bf16 (the gate/up GEMM's rows, through token_list); the GEMMs read
+    // a whole 192-row tile from every tile's first row of act, which carries
+    // that many rows of padding
+    w.x = take(static_cast<uint64_t>(tokens) * H * 2);
     w.act = take((P + kPrefillTileRows) * F * 2);
     w.dn = take(prefill_down_splits(L->experts, L->ffn) * P * H * 4);
     w.dec_act = take(static_cast<uint64_t>(L->top_k) * F * 4);
@@ -550,7 +552,8 @@ int prefill_layer(const fmx_moe_layer *L, const float *x, float *out, uint32_t t
     b.dn = reinterpret_cast<float *>(base + ws.dn);
     b.splits = prefill_down_splits(L->experts, L->ffn);
     if (int rc = launch_bucket_chunked(ids, tokens, L->top_k, L->experts,
-                                       reinterpret_cast<uint32_t *>(base + ws.offsets), slot_of, status,
+                                       reinterpret_cast<uint32_t *>(base + ws.offsets), slot_of,
+                                       reinterpret_cast<uint32_t *>(base + ws.token_list), status,
                                        reinterpret_cast<uint32_t *>(base + ws.chunk_counts), s,
                                        reinterpret_cast<uint32_t *>(base + ws.tiles), kPrefillTileRows))
         return rc;

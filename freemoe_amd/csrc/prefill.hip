@@ -4,11 +4,11 @@
 // prompt token (engine.cpp:1870, 2395-2399). Here the batch is
 //   route (bit-identical to the per-token routing, moe.hip)
 //   -> bucket (per-expert token lists and row tiles, bucket.hip)
-//   -> gather: h rows of each (token, expert) pair into an expert-contiguous
-//      bf16 matrix X [pairs x hidden]
-//   -> gate/up grouped GEMM on bf16 MFMA, weights dequantised from their
-//      packed blocks in registers, SwiGLU in the epilogue -> act [pairs x ffn]
-//      bf16
+//   -> h into bf16 rows in the packed K order, one per token
+//   -> gate/up grouped GEMM on bf16 MFMA over each expert's pairs (their
+//      tokens' rows read through the bucketing's token list), weights
+//      dequantised from their packed blocks in registers, SwiGLU in the
+//      epilogue -> act [pairs x ffn] bf16
 //   -> down grouped GEMM (K split in two for few experts) -> D f32 partials
 //   -> combine per token in rank order plus the residual.
 //
@@ -388,9 +388,10 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // LDS, 16 bytes per lane in lane order, so thread t (wavefront w, lane l)
 // fills slot l % 16 of tile row sr = 4 w + l / 16 (+ 32 i for row block i)
 // and loads the granule the swizzle puts there, granule (l % 16) ^ (sr % 16).
-// The activation matrix has at least 192 readable rows past every tile's
-// first row (the workspace pads it), and rows past the tile (up to 32 NMB)
-// only feed output rows that are never written.
+// Every staging row has a readable source (gate/up: the token of the pair,
+// or of the last pair for rows past them; down: the workspace pads act by a
+// tile), and rows past the tile (up to 32 NMB) only feed output rows that
+// are never written.
 //
 // Requests: step st requests the activations of step st + 1 (into the LDS
 // buffer that step st - 1 read) and the weights of step st + 2, and at its
@@ -405,12 +406,15 @@ struct GemmWave {
     typename T::WStep w[3];
     f32x16 acc[NMB];
 
+    // xrow[i]: this thread's granule of staging row sr + 32 i at K position 0
+    // (see run).
+    const __bf16 *xrow[NMB];
+
     // This thread's granules of step k0's activations into LDS buffer `dst`
     // (the wavefront's 1 KiB of row block 0 of the buffer: wave-uniform).
-    __device__ __forceinline__ void load_x(char *dst, const __bf16 *src, uint64_t ld, uint32_t k0) {
+    __device__ __forceinline__ void load_x(char *dst, uint32_t k0) {
 #pragma unroll
-        for (uint32_t i = 0; i < NMB; ++i)
-            load_lds16(src + static_cast<uint64_t>(32 * i) * ld + k0, dst + i * 32 * kGRowBytes);
+        for (uint32_t i = 0; i < NMB; ++i) load_lds16(xrow[i] + k0, dst + i * 32 * kGRowBytes);
     }
 
     // The MFMAs of one K step from ring slot `slot`; a_kk[kk]: byte address of
@@ -446,10 +450,9 @@ struct GemmWave {
     // buffer and the weights of step `nw` into `slot_next`, multiply step
     // (ring slot `slot`, LDS buffer `buf`), wait for the activations, barrier.
     __device__ __forceinline__ void step(int slot, int slot_next, uint32_t buf, uint32_t nw, uint32_t nx,
-                                         const uint8_t *m0, uint32_t r0, const PackedGeometry &g,
-                                         const __bf16 *xsrc, uint64_t ldx, char *lds, uint32_t wbase, uint32_t aoff0,
-                                         uint32_t h) {
-        load_x(lds + (buf ^ 1) * kGBufBytes + wbase, xsrc, ldx, nx * kGStepK);
+                                         const uint8_t *m0, uint32_t r0, const PackedGeometry &g, char *lds,
+                                         uint32_t wbase, uint32_t aoff0, uint32_t h) {
+        load_x(lds + (buf ^ 1) * kGBufBytes + wbase, nx * kGStepK);
         T::load_step(w[slot_next], m0, g, r0, nw, h);
         __builtin_amdgcn_sched_barrier(0);
         const char *a_kk[8];
@@ -461,9 +464,12 @@ struct GemmWave {
         lds_barrier();
     }
 
-    // K steps [s0, s0 + steps) against weight row (m0, r0).
-    __device__ __forceinline__ void run(const uint8_t *m0, uint32_t r0, const PackedGeometry &g,
-                                        const __bf16 *xsrc, uint64_t ldx, uint32_t s0, uint32_t steps, char *lds) {
+    // K steps [s0, s0 + steps) against weight row (m0, r0). Staging row r of
+    // the tile (r < 32 NMB) is the activation row row_of(r) (a pointer to
+    // its K position 0).
+    template <class RowOf>
+    __device__ __forceinline__ void run(const uint8_t *m0, uint32_t r0, const PackedGeometry &g, RowOf row_of,
+                                        uint32_t s0, uint32_t steps, char *lds) {
         const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5;
         const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
         const uint32_t last = s0 + steps - 1;
@@ -473,7 +479,8 @@ struct GemmWave {
         const uint32_t aoff0 = ar * kGRowBytes + (((8 * h) ^ xswz(ar)) << 4);
         // staging: row sr = 4 w + l / 16 (= tid / 16), slot l % 16
         const uint32_t sr = tid >> 4;
-        xsrc += static_cast<uint64_t>(sr) * ldx + 8 * ((lane & 15) ^ xswz(sr));
+#pragma unroll
+        for (uint32_t i = 0; i < NMB; ++i) xrow[i] = row_of(sr + 32 * i) + 8 * ((lane & 15) ^ xswz(sr));
         const uint32_t wbase = 1024 * wave;
 #pragma unroll
         for (uint32_t mb = 0; mb < NMB; ++mb)
@@ -481,7 +488,7 @@ struct GemmWave {
             for (int i = 0; i < 16; ++i) acc[mb][i] = 0.0f;
         // prologue: activations of s0 into LDS buffer 0, weights of s0 and
         // s0 + 1
-        load_x(lds + wbase, xsrc, ldx, s0 * kGStepK);
+        load_x(lds + wbase, s0 * kGStepK);
 #pragma unroll
         for (int p = 0; p < 2; ++p) T::load_step(w[p], m0, g, r0, clampk(s0 + p), h);
         wait_vm_lgkm0<0>();
@@ -492,8 +499,7 @@ struct GemmWave {
 #pragma unroll
             for (uint32_t u = 0; u < kPass; ++u) {
                 const uint32_t st = s0 + s + u;
-                step(u % 3, (u + 2) % 3, u & 1, clampk(st + 2), clampk(st + 1), m0, r0, g, xsrc, ldx, lds, wbase,
-                     aoff0, h);
+                step(u % 3, (u + 2) % 3, u & 1, clampk(st + 2), clampk(st + 1), m0, r0, g, lds, wbase, aoff0, h);
             }
         }
         // the remaining steps (fewer than kPass)
@@ -501,28 +507,25 @@ struct GemmWave {
         for (uint32_t u = 0; u < kPass; ++u) {
             if (s + u >= steps) break;
             const uint32_t st = s0 + s + u;
-            step(u % 3, (u + 2) % 3, u & 1, clampk(st + 2), clampk(st + 1), m0, r0, g, xsrc, ldx, lds, wbase, aoff0,
-                 h);
+            step(u % 3, (u + 2) % 3, u & 1, clampk(st + 2), clampk(st + 1), m0, r0, g, lds, wbase, aoff0, h);
         }
     }
 };
 
 // ------------------------------------------------------------------ kernels --
 
-// X[slot_of[t K + r]][p] = bf16(h[t][element at packed position p]) for
-// every rank r of token t: one workgroup per (2048-element segment, token),
-// so each h row is read once (16-byte loads into LDS) and its packed bf16
-// segment written to the token's K pair rows; 8 positions per thread.
-// Positions at or past `pairs` (a routing table the bucketing rejected) are
-// skipped. grid: (ceil(hidden / 2048), tokens).
-constexpr uint32_t kGatherSeg = 2048;
+// hb[t][p] = bf16(h[t][element at packed position p]): one workgroup per
+// (2048-element segment, token), the h segment staged in LDS by 16-byte
+// loads, 8 positions (one 16-byte store) per thread. The gate/up GEMM reads
+// each pair's row of hb through token_list. grid: (ceil(hidden / 2048),
+// tokens).
+constexpr uint32_t kPackSeg = 2048;
 template <class T>
-__global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ h, uint32_t hidden, uint32_t K,
-                                                     const uint32_t *__restrict__ slot_of, uint32_t pairs,
-                                                     __bf16 *__restrict__ x) {
-    __shared__ __align__(16) float seg[kGatherSeg];
-    const uint32_t t = blockIdx.y, e0 = blockIdx.x * kGatherSeg, tid = threadIdx.x;
-    const uint32_t n = hidden - e0 < kGatherSeg ? hidden - e0 : kGatherSeg;
+__global__ __launch_bounds__(256) void pack_h_kernel(const float *__restrict__ h, uint32_t hidden,
+                                                     __bf16 *__restrict__ hb) {
+    __shared__ __align__(16) float seg[kPackSeg];
+    const uint32_t t = blockIdx.y, e0 = blockIdx.x * kPackSeg, tid = threadIdx.x;
+    const uint32_t n = hidden - e0 < kPackSeg ? hidden - e0 : kPackSeg;
     const float4 *src = reinterpret_cast<const float4 *>(h + static_cast<uint64_t>(t) * hidden + e0);
     for (uint32_t q = tid; q < n / 4; q += 256) reinterpret_cast<float4 *>(seg)[q] = src[q];
     __syncthreads();
@@ -532,11 +535,7 @@ __global__ __launch_bounds__(256) void gather_kernel(const float *__restrict__ h
     uint32_t v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = pack_bf16x2(seg[cb + T::elem(pc + 2 * i)], seg[cb + T::elem(pc + 2 * i + 1)]);
-    const uint4 packed = make_uint4(v[0], v[1], v[2], v[3]);
-    for (uint32_t r = 0; r < K; ++r) {
-        const uint32_t pos = slot_of[static_cast<uint64_t>(t) * K + r];
-        if (pos < pairs) *reinterpret_cast<uint4 *>(x + static_cast<uint64_t>(pos) * hidden + e0 + p) = packed;
-    }
+    *reinterpret_cast<uint4 *>(hb + static_cast<uint64_t>(t) * hidden + e0 + p) = make_uint4(v[0], v[1], v[2], v[3]);
 }
 
 // Column of activation element f (an ffn index) in the down projection's
@@ -560,13 +559,21 @@ __device__ __forceinline__ uint32_t down_k_position(uint32_t down_type, uint32_t
 // columns, which apply SwiGLU.
 template <class T, uint32_t NMB>
 __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, uint32_t row0, uint32_t rows,
-                             const __bf16 *__restrict__ x, __bf16 *__restrict__ act, char *lds) {
+                                             uint32_t pairs, uint32_t tokens, const __bf16 *__restrict__ hb,
+                                             const uint32_t *__restrict__ token_list, __bf16 *__restrict__ act,
+                                             char *lds) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t f = blockIdx.x * 128 + 32 * (wave & 3) + (lane & 31);
     const bool is_up = wave >= 4;
     GemmWave<T, NMB> gw;
-    gw.run(static_cast<const uint8_t *>(is_up ? a.up[e] : a.gate[e]), f, a.gu,
-           x + static_cast<uint64_t>(row0) * a.hidden, a.hidden, 0, a.hidden / kGStepK, lds);
+    const uint32_t H = a.hidden;
+    // rows past the pairs read the last pair's token; a token index out of
+    // range (a list the bucketing reported as broken) reads token 0
+    auto row_of = [=](uint32_t r) {
+        const uint32_t pr = row0 + r < pairs ? row0 + r : pairs - 1, t = token_list[pr];
+        return hb + static_cast<uint64_t>(t < tokens ? t : 0u) * H;
+    };
+    gw.run(static_cast<const uint8_t *>(is_up ? a.up[e] : a.gate[e]), f, a.gu, row_of, 0, H / kGStepK, lds);
     // the K loop ended with a barrier after every wavefront's last LDS read
     float *xc = reinterpret_cast<float *>(lds) + (wave & 3) * NMB * 16 * 64 + lane;
     if (!is_up) {
@@ -595,18 +602,18 @@ __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, ui
 // (their workgroups return at once) come last in dispatch order.
 template <class T>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gate_up_gemm_kernel(
-    ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, const __bf16 *__restrict__ x,
-    __bf16 *__restrict__ act) {
+    ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, uint32_t tokens, const __bf16 *__restrict__ hb,
+    const uint32_t *__restrict__ token_list, __bf16 *__restrict__ act) {
     extern __shared__ __align__(16) char xlds[];
     uint32_t e, row0, rows;
     if (!row_tile(tiles, blockIdx.y, a.experts, pairs, e, row0, rows)) return;
     switch ((rows + 31) / 32) {
-    case 1: gate_up_tile<T, 1>(a, e, row0, rows, x, act, xlds); break;
-    case 2: gate_up_tile<T, 2>(a, e, row0, rows, x, act, xlds); break;
-    case 3: gate_up_tile<T, 3>(a, e, row0, rows, x, act, xlds); break;
-    case 4: gate_up_tile<T, 4>(a, e, row0, rows, x, act, xlds); break;
-    case 5: gate_up_tile<T, 5>(a, e, row0, rows, x, act, xlds); break;
-    default: gate_up_tile<T, 6>(a, e, row0, rows, x, act, xlds); break;
+    case 1: gate_up_tile<T, 1>(a, e, row0, rows, pairs, tokens, hb, token_list, act, xlds); break;
+    case 2: gate_up_tile<T, 2>(a, e, row0, rows, pairs, tokens, hb, token_list, act, xlds); break;
+    case 3: gate_up_tile<T, 3>(a, e, row0, rows, pairs, tokens, hb, token_list, act, xlds); break;
+    case 4: gate_up_tile<T, 4>(a, e, row0, rows, pairs, tokens, hb, token_list, act, xlds); break;
+    case 5: gate_up_tile<T, 5>(a, e, row0, rows, pairs, tokens, hb, token_list, act, xlds); break;
+    default: gate_up_tile<T, 6>(a, e, row0, rows, pairs, tokens, hb, token_list, act, xlds); break;
     }
 }
 
@@ -620,7 +627,9 @@ __device__ __forceinline__ void down_tile(const ExpertArgs &a, uint32_t e, uint3
     const uint32_t n = blockIdx.x * 256 + 32 * wave + (lane & 31);
     const uint8_t *wd = static_cast<const uint8_t *>(a.down[e]);
     GemmWave<T, NMB> gw;
-    gw.run(wd, n, a.dn, act + static_cast<uint64_t>(row0) * a.ffn, a.ffn, blockIdx.y * steps, steps, lds);
+    const uint32_t F = a.ffn;
+    auto row_of = [=](uint32_t r) { return act + static_cast<uint64_t>(row0 + r) * F; };
+    gw.run(wd, n, a.dn, row_of, blockIdx.y * steps, steps, lds);
     const uint32_t H = a.hidden;
     float *dst = dn + static_cast<uint64_t>(blockIdx.y) * pairs * H;
 #pragma unroll
@@ -684,11 +693,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float *__restrict__ 
 // ---------------------------------------------------------------- launchers --
 
 template <class T>
-int launch_gather(const float *h, uint32_t hidden, uint32_t tokens, uint32_t K, const uint32_t *slot_of,
-                  uint32_t pairs, __bf16 *x, hipStream_t s) {
+int launch_pack_h(const float *h, uint32_t hidden, uint32_t tokens, __bf16 *hb, hipStream_t s) {
     if (tokens == 0) return FMX_OK;
-    hipLaunchKernelGGL(gather_kernel<T>, dim3(div_up(hidden, kGatherSeg), tokens), dim3(256), 0, s, h, hidden, K,
-                       slot_of, pairs, x);
+    hipLaunchKernelGGL(pack_h_kernel<T>, dim3(div_up(hidden, kPackSeg), tokens), dim3(256), 0, s, h, hidden, hb);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
@@ -701,20 +708,21 @@ int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tile
     if (int rc = allow_lds(reinterpret_cast<const void *>(gu), lds)) return rc;
     if (int rc = allow_lds(reinterpret_cast<const void *>(dn), lds)) return rc;
     if (b.pairs == 0) return FMX_OK;
-    if (int rc = launch_gather<T>(b.h, a.hidden, b.tokens, b.top_k, b.slot_of, b.pairs, b.x, s)) return rc;
+    if (int rc = launch_pack_h<T>(b.h, a.hidden, b.tokens, b.x, s)) return rc;
     const dim3 gu_grid(a.ffn / 128, max_tiles), dn_grid(a.hidden / 256, b.splits, max_tiles);
     const uint32_t steps = a.ffn / kGStepK / b.splits;
     if (kev) {
         // the launches record kev[0..1] / kev[2..3] at kernel start and end
-        hipExtLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, kev[0], kev[1], 0, a, b.tiles, b.pairs, b.x,
-                              b.act);
+        hipExtLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, kev[0], kev[1], 0, a, b.tiles, b.pairs,
+                              b.tokens, b.x, b.token_list, b.act);
         FMX_LAUNCH_CHECK();
         hipExtLaunchKernelGGL(dn, dn_grid, dim3(kGThreads), lds, s, kev[2], kev[3], 0, a, b.tiles, b.pairs, b.act,
                               steps, b.dn);
         FMX_LAUNCH_CHECK();
         return FMX_OK;
     }
-    hipLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.x, b.act);
+    hipLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.tokens, b.x, b.token_list,
+                       b.act);
     FMX_LAUNCH_CHECK();
     hipLaunchKernelGGL(dn, dn_grid, dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.act, steps, b.dn);
     FMX_LAUNCH_CHECK();

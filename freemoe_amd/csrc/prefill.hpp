@@ -14,7 +14,7 @@ struct PrefillBuffers {
     const uint32_t *tiles;       // row tiles of the bucketing (count, then expert / first row / rows)
     uint32_t tokens;
     uint32_t pairs;              // tokens * top_k
-    __bf16 *x;                   // [pairs x hidden] gathered h in the gate/up packed K order
+    __bf16 *x;                   // [tokens x hidden] h in bf16, in the gate/up packed K order
     __bf16 *act;                 // [pairs x ffn] SwiGLU output in the down packed K order
     float *dn;                   // [splits x pairs x hidden] down projections (partial over K splits)
     uint32_t splits;             // K splits of the down projection (prefill_down_splits)
@@ -30,7 +30,8 @@ bool prefill_gemm_supported(const ExpertArgs &a);
 // K splits of the down projection (its partial products are summed by the
 // combine).
 uint32_t prefill_down_splits(uint32_t experts, uint32_t ffn);
-// gather -> gate/up GEMM + SwiGLU -> down GEMM, over `max_tiles` row tiles.
+// h to bf16 -> gate/up GEMM (rows through token_list) + SwiGLU -> down GEMM,
+// over `max_tiles` row tiles.
 // kev (optional): events the gate/up launch records at its start and end
 // (kev[0], kev[1]) and the down launch likewise (kev[2], kev[3]).
 int launch_prefill_experts(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tiles, hipStream_t s,
