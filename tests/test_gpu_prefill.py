@@ -90,15 +90,14 @@ def test_prefill_mixtral_q8_0_512_tokens(gpu):
     print(f"mixtral q8_0 512 tokens: norm ratio {norm_ratio:.3e}, max ratio {max_ratio:.3e}")
 
 
-def test_prefill_finegrained_q4_k_1100_tokens(gpu):
-    """The fine-grained layer's shape (hidden 2048, ffn 768, 128 experts, top-8,
-    Q4_K, Zipf(1.2) router bias) at 1100 tokens: the single-split down GEMM,
-    bucketing over two 1024-token chunks, and experts with no pair, one pair
-    and more than one 192-pair row tile."""
-    lw = wl.make_layer(2048, 768, 128, 8, wl.Q4_K, 41, zipf_s=1.2)
-    x = wl.inputs(2048, 1100, 42)
+def test_prefill_finegrained_q4_k_2048_tokens(gpu):
+    """The fine-grained prefill workload itself (hidden 2048, ffn 768, 128
+    experts, top-8, Q4_K, Zipf(1.2) router bias, 2048 tokens): the
+    single-split down GEMM, bucketing over eight 256-token chunks, and experts
+    with no pair, one pair and more than one 192-pair row tile."""
+    lw, x = wl.workload("finegrained")
     norm_ratio, max_ratio = check_prefill(gpu, lw, x)
-    print(f"finegrained q4_k 1100 tokens: norm ratio {norm_ratio:.3e}, max ratio {max_ratio:.3e}")
+    print(f"finegrained q4_k 2048 tokens: norm ratio {norm_ratio:.3e}, max ratio {max_ratio:.3e}")
 
 
 def test_prefill_mixed_block_types(gpu):
