@@ -229,7 +229,7 @@ __global__ __launch_bounds__(kChunkTokens) void bucket_place_kernel(
     const uint32_t *__restrict__ ids, uint32_t tokens, uint32_t K, uint32_t E, uint32_t chunks,
     const uint32_t *__restrict__ counts, uint32_t *__restrict__ offsets, uint32_t *__restrict__ slot_of,
     uint32_t *__restrict__ token_list, uint32_t *__restrict__ status, uint32_t *__restrict__ tiles,
-    uint32_t tile_rows) {
+    uint32_t *__restrict__ order, uint32_t tile_rows) {
     __shared__ uint32_t total[kBucketMaxExperts], base[kBucketMaxExperts], own[kBucketMaxExperts];
     __shared__ uint32_t mask[kBucketMaxExperts * kChunkWords], below[kBucketMaxExperts * kChunkWords];
     __shared__ uint32_t bad;
@@ -264,27 +264,55 @@ __global__ __launch_bounds__(kChunkTokens) void bucket_place_kernel(
         return;
     }
     // exclusive scan of the totals over experts by one wavefront (as the
-    // single-workgroup pass); chunk 0 writes the offsets and the tiles
+    // single-workgroup pass); chunk 0 writes the offsets and the tiles in
+    // expert order, and with `order` the same tiles largest first (order[i]:
+    // the i-th tile to run), so that a GEMM's last rounds of workgroups hold
+    // the short ones: every expert's full tiles (expert order), then the
+    // partial tiles by row blocks, most first (expert order within a class).
+    // The partial tiles' counts per class (9 bits each, at most 256 experts)
+    // are scanned packed in one 64-bit word.
     if (tid < 64) {
         constexpr uint32_t kPerLane = kBucketMaxExperts / 64;
-        uint32_t rows = 0, nts = 0;
+        const uint32_t nb = tile_rows / 32; // row-block classes of a partial tile (<= 7)
+        auto cls = [tile_rows](uint32_t v) { return (v % tile_rows + 31) / 32; }; // 0: no partial tile
+        uint32_t rows = 0, nts = 0, full = 0;
+        uint64_t part = 0;
 #pragma unroll
         for (uint32_t j = 0; j < kPerLane; ++j) {
             const uint32_t e = tid * kPerLane + j;
             const uint32_t v = e < E ? total[e] : 0;
             rows += v;
-            if (tiles) nts += (v + tile_rows - 1) / tile_rows;
+            if (tiles) {
+                nts += (v + tile_rows - 1) / tile_rows;
+                full += v / tile_rows;
+                if (cls(v)) part += 1ull << (9 * (cls(v) - 1));
+            }
         }
-        uint32_t rincl = rows, tincl = nts;
+        uint32_t rincl = rows, tincl = nts, fincl = full;
+        uint64_t pincl = part;
 #pragma unroll
         for (uint32_t d = 1; d < 64; d <<= 1) {
-            const uint32_t rv = __shfl_up(rincl, d), tv = __shfl_up(tincl, d);
+            const uint32_t rv = __shfl_up(rincl, d), tv = __shfl_up(tincl, d), fv = __shfl_up(fincl, d);
+            const uint64_t pv = __shfl_up(pincl, d);
             if (tid >= d) {
                 rincl += rv;
                 tincl += tv;
+                fincl += fv;
+                pincl += pv;
             }
         }
-        uint32_t run = rincl - rows, nt = tincl - nts;
+        uint32_t run = rincl - rows, nt = tincl - nts, nf = fincl - full;
+        // where this lane's next partial tile of each class goes in `order`
+        uint32_t np[7] = {};
+        if (order) {
+            const uint32_t ftotal = __shfl(fincl, 63);
+            const uint64_t ptotal = __shfl(pincl, 63), pexcl = pincl - part;
+            uint32_t at = ftotal;
+            for (uint32_t k = nb; k >= 1; --k) {
+                np[k - 1] = at + static_cast<uint32_t>((pexcl >> (9 * (k - 1))) & 511u);
+                at += static_cast<uint32_t>((ptotal >> (9 * (k - 1))) & 511u);
+            }
+        }
         for (uint32_t j = 0; j < kPerLane; ++j) {
             const uint32_t e = tid * kPerLane + j;
             if (e >= E) break;
@@ -294,9 +322,11 @@ __global__ __launch_bounds__(kChunkTokens) void bucket_place_kernel(
                 offsets[e] = run;
                 if (tiles)
                     for (uint32_t r = 0; r < v; r += tile_rows, ++nt) {
+                        const uint32_t n = v - r < tile_rows ? v - r : tile_rows;
                         tiles[1 + 3 * nt] = e;
                         tiles[2 + 3 * nt] = run + r;
-                        tiles[3 + 3 * nt] = v - r < tile_rows ? v - r : tile_rows;
+                        tiles[3 + 3 * nt] = n;
+                        if (order) order[n == tile_rows ? nf++ : np[cls(v) - 1]++] = nt;
                     }
             }
             run += v;
@@ -358,15 +388,18 @@ uint64_t bucket_chunk_counts_bytes(uint32_t tokens, uint32_t experts) {
 
 int launch_bucket_chunked(const uint32_t *ids, uint32_t tokens, uint32_t K, uint32_t E, uint32_t *offsets,
                           uint32_t *slot_of, uint32_t *token_list, uint32_t *status, uint32_t *counts, hipStream_t s,
-                          uint32_t *tiles, uint32_t tile_rows) {
-    if (!slot_of || !counts || E == 0 || E > kBucketMaxExperts || (tiles && tile_rows == 0))
+                          uint32_t *tiles, uint32_t *order, uint32_t tile_rows) {
+    // order (with tiles): tile_rows a multiple of 32, at most 7 row blocks
+    // (the classes of the partial tiles' packed counts)
+    if (!slot_of || !counts || E == 0 || E > kBucketMaxExperts || (tiles && tile_rows == 0) || (order && !tiles) ||
+        (order && (tile_rows % 32 || tile_rows > 224)))
         return FMX_ERR_INVALID_ARGUMENT;
     if (tokens == 0) return FMX_OK;
     const uint32_t chunks = div_up(tokens, kChunkTokens);
     hipLaunchKernelGGL(bucket_count_kernel, dim3(chunks), dim3(kChunkTokens), 0, s, ids, tokens, K, E, counts);
     FMX_LAUNCH_CHECK();
     hipLaunchKernelGGL(bucket_place_kernel, dim3(chunks), dim3(kChunkTokens), 0, s, ids, tokens, K, E, chunks, counts,
-                       offsets, slot_of, token_list, status, tiles, tile_rows);
+                       offsets, slot_of, token_list, status, tiles, order, tile_rows);
     FMX_LAUNCH_CHECK();
     return FMX_OK;
 }

@@ -48,13 +48,13 @@ DecodeWorkspace decode_workspace(const fmx_moe_layer *L, uint32_t tokens) {
 // Prefill workspace (all offsets 256-byte aligned), pairs = tokens * top_k:
 //   [0, 256) error word | h [tokens x hidden] f32 | offsets [experts + 1] |
 //   token_list, rank_list, slot_of [pairs] | row tiles [1 + 3 * max_tiles] |
-//   chunk counts | x [tokens x hidden] bf16 | act [pairs + 192 rows x ffn] bf16 |
+//   tile order [max_tiles] | chunk counts | x [tokens x hidden] bf16 | act [pairs + 192 rows x ffn] bf16 |
 //   dn [splits x pairs x hidden] f32 |
 //   the decode scratch (act of one token) for shapes the GEMMs do not tile |
 //   logits [tokens x experts] f32
 struct PrefillWorkspace {
-    uint64_t h = 0, offsets = 0, token_list = 0, rank_list = 0, slot_of = 0, tiles = 0, chunk_counts = 0, x = 0,
-             act = 0, dn = 0,
+    uint64_t h = 0, offsets = 0, token_list = 0, rank_list = 0, slot_of = 0, tiles = 0, tile_order = 0,
+             chunk_counts = 0, x = 0, act = 0, dn = 0,
              dec_act = 0, logits = 0, total = 0;
     uint32_t pairs = 0, max_tiles = 0;
 };
@@ -73,6 +73,7 @@ PrefillWorkspace prefill_workspace(const fmx_moe_layer *L, uint32_t tokens) {
     w.rank_list = take(P * 4);
     w.slot_of = take(P * 4);
     w.tiles = take((1 + 3ull * w.max_tiles) * 4);
+    w.tile_order = take(static_cast<uint64_t>(w.max_tiles) * 4);
     w.chunk_counts = take(bucket_chunk_counts_bytes(tokens, L->experts));
     // h in bf16 (the gate/up GEMM's rows, through token_list); the GEMMs read
     // a whole 192-row tile from every tile's first row of act, which carries
@@ -545,6 +546,7 @@ int prefill_layer(const fmx_moe_layer *L, const float *x, float *out, uint32_t t
     b.slot_of = slot_of;
     b.top_k = L->top_k;
     b.tiles = reinterpret_cast<uint32_t *>(base + ws.tiles);
+    b.tile_order = reinterpret_cast<uint32_t *>(base + ws.tile_order);
     b.tokens = tokens;
     b.pairs = ws.pairs;
     b.x = reinterpret_cast<__bf16 *>(base + ws.x);
@@ -555,7 +557,8 @@ int prefill_layer(const fmx_moe_layer *L, const float *x, float *out, uint32_t t
                                        reinterpret_cast<uint32_t *>(base + ws.offsets), slot_of,
                                        reinterpret_cast<uint32_t *>(base + ws.token_list), status,
                                        reinterpret_cast<uint32_t *>(base + ws.chunk_counts), s,
-                                       reinterpret_cast<uint32_t *>(base + ws.tiles), kPrefillTileRows))
+                                       reinterpret_cast<uint32_t *>(base + ws.tiles),
+                                       reinterpret_cast<uint32_t *>(base + ws.tile_order), kPrefillTileRows))
         return rc;
     if (int rc = launch_prefill_experts(ea, b, ws.max_tiles, s, kev)) return rc;
     *tiled = true;

@@ -598,15 +598,16 @@ __device__ __forceinline__ void gate_up_tile(const ExpertArgs &a, uint32_t e, ui
     }
 }
 
-// grid: (ffn / 128, max row tiles): the row tiles past the bucketing's count
-// (their workgroups return at once) come last in dispatch order.
+// grid: (ffn / 128, max row tiles): tile order[blockIdx.y] (largest first);
+// the row tiles past the bucketing's count (their workgroups return at once)
+// come last in dispatch order.
 template <class T>
 __global__ __launch_bounds__(kGThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gate_up_gemm_kernel(
-    ExpertArgs a, const uint32_t *__restrict__ tiles, uint32_t pairs, uint32_t tokens, const __bf16 *__restrict__ hb,
-    const uint32_t *__restrict__ token_list, __bf16 *__restrict__ act) {
+    ExpertArgs a, const uint32_t *__restrict__ tiles, const uint32_t *__restrict__ order, uint32_t pairs,
+    uint32_t tokens, const __bf16 *__restrict__ hb, const uint32_t *__restrict__ token_list, __bf16 *__restrict__ act) {
     extern __shared__ __align__(16) char xlds[];
     uint32_t e, row0, rows;
-    if (!row_tile(tiles, blockIdx.y, a.experts, pairs, e, row0, rows)) return;
+    if (blockIdx.y >= tiles[0] || !row_tile(tiles, order[blockIdx.y], a.experts, pairs, e, row0, rows)) return;
     switch ((rows + 31) / 32) {
     case 1: gate_up_tile<T, 1>(a, e, row0, rows, pairs, tokens, hb, token_list, act, xlds); break;
     case 2: gate_up_tile<T, 2>(a, e, row0, rows, pairs, tokens, hb, token_list, act, xlds); break;
@@ -713,16 +714,16 @@ int launch_gemms(const ExpertArgs &a, const PrefillBuffers &b, uint32_t max_tile
     const uint32_t steps = a.ffn / kGStepK / b.splits;
     if (kev) {
         // the launches record kev[0..1] / kev[2..3] at kernel start and end
-        hipExtLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, kev[0], kev[1], 0, a, b.tiles, b.pairs,
-                              b.tokens, b.x, b.token_list, b.act);
+        hipExtLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, kev[0], kev[1], 0, a, b.tiles, b.tile_order,
+                              b.pairs, b.tokens, b.x, b.token_list, b.act);
         FMX_LAUNCH_CHECK();
         hipExtLaunchKernelGGL(dn, dn_grid, dim3(kGThreads), lds, s, kev[2], kev[3], 0, a, b.tiles, b.pairs, b.act,
                               steps, b.dn);
         FMX_LAUNCH_CHECK();
         return FMX_OK;
     }
-    hipLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.tokens, b.x, b.token_list,
-                       b.act);
+    hipLaunchKernelGGL(gu, gu_grid, dim3(kGThreads), lds, s, a, b.tiles, b.tile_order, b.pairs, b.tokens, b.x,
+                       b.token_list, b.act);
     FMX_LAUNCH_CHECK();
     hipLaunchKernelGGL(dn, dn_grid, dim3(kGThreads), lds, s, a, b.tiles, b.pairs, b.act, steps, b.dn);
     FMX_LAUNCH_CHECK();

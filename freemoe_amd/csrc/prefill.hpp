@@ -12,6 +12,7 @@ struct PrefillBuffers {
     const uint32_t *slot_of;     // [tokens x top_k] pair row of each (token, rank)
     uint32_t top_k;
     const uint32_t *tiles;       // row tiles of the bucketing (count, then expert / first row / rows)
+    const uint32_t *tile_order;  // the tiles' indices largest first (the gate/up GEMM's dispatch order)
     uint32_t tokens;
     uint32_t pairs;              // tokens * top_k
     __bf16 *x;                   // [tokens x hidden] h in bf16, in the gate/up packed K order
