@@ -323,6 +323,18 @@ def kernels_leg(dev, reps=10, cpu=True):
     return res
 
 
+def calibration_copy(dev, nbytes):
+    """One plain device-to-device copy of nbytes: a kernel of known traffic,
+    against which a profiler's byte counters are scaled."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -361,6 +373,8 @@ def main() -> int:
     if args.kernels_only:
         print(json.dumps({"kernels": kernels_leg(dev, reps=args.steps, cpu=not args.no_cpu_baseline)}))
         return 0
+    if args.copy_bytes and (args.prefill_only or args.ragged_only):
+        calibration_copy(dev, args.copy_bytes)
     if args.prefill_only:
         res = prefill_leg(dev, reps=args.steps, cpu=not args.no_cpu_baseline)
         print(json.dumps({"prefill": res}))
@@ -387,12 +401,7 @@ def main() -> int:
     torch.cuda.synchronize()
 
     if args.copy_bytes:
-        src = torch.ones(args.copy_bytes // 4, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+        calibration_copy(dev, args.copy_bytes)
     for _ in range(args.warmup):
         dl.decode(xd, out, ids, wts)
     torch.cuda.synchronize()
