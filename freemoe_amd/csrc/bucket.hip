@@ -239,12 +239,19 @@ __global__ __launch_bounds__(kChunkTokens) void bucket_place_kernel(
     for (uint32_t i = tid; i < E * kChunkWords; i += kChunkTokens) mask[i] = 0;
     __syncthreads();
     // per expert: the total over chunks and the count of the chunks before c
+    // (the chunks' counts requested 8 at a time, so their latencies overlap)
     for (uint32_t e = tid; e < E; e += kChunkTokens) {
         uint32_t tot = 0, pre = 0;
-        for (uint32_t q = 0; q < chunks; ++q) {
-            const uint32_t v = counts[static_cast<uint64_t>(q) * (E + 1) + e];
-            pre += q < c ? v : 0u;
-            tot += v;
+        for (uint32_t q0 = 0; q0 < chunks; q0 += 8) {
+            uint32_t v[8];
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j)
+                v[j] = q0 + j < chunks ? counts[static_cast<uint64_t>(q0 + j) * (E + 1) + e] : 0u;
+#pragma unroll
+            for (uint32_t j = 0; j < 8; ++j) {
+                pre += q0 + j < c ? v[j] : 0u;
+                tot += v[j];
+            }
         }
         total[e] = tot;
         base[e] = pre;

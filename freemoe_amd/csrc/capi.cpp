@@ -522,10 +522,9 @@ int prefill_layer(const fmx_moe_layer *L, const float *x, float *out, uint32_t t
     uint8_t *base = static_cast<uint8_t *>(workspace);
     uint32_t *status = reinterpret_cast<uint32_t *>(base);
     float *h = reinterpret_cast<float *>(base + ws.h);
-    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, status);
-    FMX_LAUNCH_CHECK();
+    // the routing's first kernel zeroes the error word
     if (int rc = launch_route(ra, x, tokens, h, reinterpret_cast<float *>(base + ws.logits), ids, weights, status,
-                              s))
+                              s, true))
         return rc;
     const uint64_t H = L->hidden, K = L->top_k;
     if (!prefill_gemm_supported(ea)) {

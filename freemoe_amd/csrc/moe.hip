@@ -727,8 +727,11 @@ __global__ __launch_bounds__(NT) __attribute__((aligned(kHotAlign))) void route_
 // in-order sum when the certificate fails).
 template <uint32_t NT>
 __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *__restrict__ x,
-                                                     float *__restrict__ h) {
+                                                     float *__restrict__ h, uint32_t *__restrict__ clear) {
     constexpr uint32_t P = 4;
+    // the call's error word, zeroed by the first kernel of the call (no later
+    // kernel of the call runs before this one ends, and this one sets no bit)
+    if (clear && blockIdx.x == 0 && threadIdx.x == 0) *clear = 0;
     extern __shared__ __align__(16) float lds[];
     const uint32_t H = a.hidden, H4 = H / 4, tid = threadIdx.x, t = blockIdx.x;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + static_cast<uint64_t>(t) * H);
@@ -1334,16 +1337,17 @@ int allow_lds(const void *fn, size_t bytes) {
 size_t route_lds_bytes(uint32_t hidden) { return 2ull * 16 * route_chain_stride(hidden) * sizeof(float); }
 
 // RMSNorm of `tokens` rows of x into h: one workgroup per token.
-int launch_rmsnorm(const RouteArgs &a, const float *x, uint32_t tokens, float *h, hipStream_t s) {
+int launch_rmsnorm(const RouteArgs &a, const float *x, uint32_t tokens, float *h, hipStream_t s,
+                   uint32_t *clear = nullptr) {
     const size_t lds = 2ull * a.hidden * sizeof(float);
     if (a.hidden <= 16 * 256) {
         auto k = rmsnorm_kernel<256>;
         if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
-        hipLaunchKernelGGL(k, dim3(tokens), dim3(256), lds, s, a, x, h);
+        hipLaunchKernelGGL(k, dim3(tokens), dim3(256), lds, s, a, x, h, clear);
     } else {
         auto k = rmsnorm_kernel<1024>;
         if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
-        hipLaunchKernelGGL(k, dim3(tokens), dim3(1024), lds, s, a, x, h);
+        hipLaunchKernelGGL(k, dim3(tokens), dim3(1024), lds, s, a, x, h, clear);
     }
     FMX_LAUNCH_CHECK();
     return FMX_OK;
@@ -1409,10 +1413,10 @@ int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, flo
 // it did.
 int launch_route_batched(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                          hipStream_t s, uint32_t *ids = nullptr, float *weights = nullptr,
-                         uint32_t *status = nullptr, bool *routed = nullptr) {
+                         uint32_t *status = nullptr, bool *routed = nullptr, uint32_t *clear = nullptr) {
     if (routed) *routed = false;
     if (a.hidden > kMaxHidden || a.hidden % 4 || a.experts == 0) return FMX_ERR_SHAPE_MISMATCH;
-    if (int rc = launch_rmsnorm(a, x, tokens, h, s)) return rc;
+    if (int rc = launch_rmsnorm(a, x, tokens, h, s, clear)) return rc;
     if (a.router_type != FMX_TYPE_F32) return launch_router_quant(a, h, tokens, logits, s);
     const bool fuse = ids && weights && status && routed && a.experts <= 32;
     uint32_t *fi = fuse ? ids : nullptr;
@@ -1430,11 +1434,19 @@ int launch_route_batched(const RouteArgs &a, const float *x, uint32_t tokens, fl
     return FMX_OK;
 }
 
+__global__ void route_clear_kernel(uint32_t *word) { *word = 0; }
+
 int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
-                 uint32_t *ids, float *weights, uint32_t *status, hipStream_t s) {
+                 uint32_t *ids, float *weights, uint32_t *status, hipStream_t s, bool clear_status) {
     bool routed = false;
-    if (int rc = h && tokens > 1 ? launch_route_batched(a, x, tokens, h, logits, s, ids, weights, status, &routed)
-                                 : launch_route_logits(a, x, tokens, h, logits, s))
+    const bool batched = h && tokens > 1;
+    if (clear_status && !batched) {
+        hipLaunchKernelGGL(route_clear_kernel, dim3(1), dim3(1), 0, s, status);
+        FMX_LAUNCH_CHECK();
+    }
+    if (int rc = batched ? launch_route_batched(a, x, tokens, h, logits, s, ids, weights, status, &routed,
+                                                clear_status ? status : nullptr)
+                         : launch_route_logits(a, x, tokens, h, logits, s))
         return rc;
     if (routed) return FMX_OK;
     hipLaunchKernelGGL(route_finish_kernel, dim3(tokens), dim3(64), 0, s, a, logits, ids, weights, status);

@@ -45,8 +45,10 @@ struct DecodeScratch {
 int launch_route_logits(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
                         hipStream_t s);
 // launch_route_logits, then ids / weights ([tokens x top_k]) from the logits.
+// clear_status: zero *status first (by the first routing kernel where that
+// is the batched RMSNorm, else by a kernel of its own).
 int launch_route(const RouteArgs &a, const float *x, uint32_t tokens, float *h, float *logits,
-                 uint32_t *ids, float *weights, uint32_t *status, hipStream_t s);
+                 uint32_t *ids, float *weights, uint32_t *status, hipStream_t s, bool clear_status = false);
 int prepare_expert_args(const fmx_moe_layer *L, const RouteArgs &route, ExpertArgs *a);
 // Routing arguments of a layer (geometry and LDS tile of a block-type router).
 int prepare_route_args(const fmx_moe_layer *L, RouteArgs *a);
