@@ -58,7 +58,7 @@ def test_decode_graph_replays_match_eager(gpu, type_id, down_type):
 
 
 def test_prefill_graph_replays_match_eager(gpu):
-    """The batched layer (routing, bucketing, gather, grouped GEMMs, combine)
+    """The batched layer (routing, bucketing, bf16 rows, grouped GEMMs, combine)
     captured likewise: the GEMMs accumulate in a fixed order and the
     bucketing places pairs by rank, so replays equal the eager pass bit for
     bit."""
