@@ -100,6 +100,20 @@ def test_prefill_finegrained_q4_k_2048_tokens(gpu):
     print(f"finegrained q4_k 2048 tokens: norm ratio {norm_ratio:.3e}, max ratio {max_ratio:.3e}")
 
 
+@pytest.mark.parametrize("tokens", [1, 255, 256, 257, 1500])
+def test_prefill_every_token_on_the_same_experts(gpu, tokens):
+    """A router bias that sends every token to experts 0 and 1: two experts
+    with all the pairs (up to 8 full 192-row tiles and a partial one each),
+    six with none, token counts on both sides of the bucketing's 256-token
+    chunks. Routing bit for bit, the FFN within the prefill tolerance."""
+    lw = wl.make_layer(256, 256, 8, 2, wl.Q8_0, 81)
+    bias = np.zeros(8, np.float32)
+    bias[:2] = 40.0
+    lw.router_bias = bias
+    x = wl.inputs(256, tokens, 82)
+    check_prefill(gpu, lw, x)
+
+
 def test_prefill_mixed_block_types(gpu):
     """Gate/up and down in different block types (Q4_K gate/up with Q8_0 down,
     Q8_0 gate/up with Q4_0 down, Q4_K gate/up with Q6_K down as in FreeMoe's
