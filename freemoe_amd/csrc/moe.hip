@@ -761,14 +761,16 @@ __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *_
 // 16 s + c, s = 0, 1, ...), lane c of a 16-lane group owning chain c of a
 // PT x PR block of pairs (PT PR independent chains per lane). h and the
 // router rows pass through LDS 256 elements (16 steps of every chain) at a
-// time, the next tile requested during this one's FMAs; then the lane tree,
-// the sequential tail and the logit bias, as in f32_row_chains. Few experts
-// take small tiles (2 tokens x 8 or 16 rows) so that the grid still covers
-// the device; many take 16 x 32 (4 x 8 pairs per lane). grid:
+// time, the next tile requested during this one's FMAs and, within a tile,
+// the next four steps' operands read from LDS during this four's; then the
+// lane tree, the sequential tail and the logit bias, as in f32_row_chains.
+// Few experts take small tiles (2 tokens x 8 or 16 rows) so that the grid
+// still covers the device; many take 16 x 32 (4 x 8 pairs per lane). grid:
 // (ceil(tokens / TT), ceil(experts / TR)).
-constexpr uint32_t kRtPad = 20;                   // floats per (token or row, chain) in LDS: 16 steps + 4
-constexpr uint32_t kRtRowExtra = 0;               // floats after each token's or row's 16 chains
-constexpr uint32_t kRtRow = 16 * kRtPad + kRtRowExtra; // floats per token or row
+constexpr uint32_t kRtSteps = 16;              // steps of every chain per LDS tile (16 kRtSteps elements)
+constexpr uint32_t kRtF4 = 4 * kRtSteps;       // float4 per token or row per tile
+constexpr uint32_t kRtPad = kRtSteps + 4;      // floats per (token or row, chain) in LDS
+constexpr uint32_t kRtRow = 16 * kRtPad;       // floats per token or row
 template <uint32_t PT, uint32_t PR, uint32_t GT>
 __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const float *__restrict__ h,
                                                           uint32_t tokens, float *__restrict__ logits,
@@ -782,14 +784,14 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
     const uint32_t c = tid & 15, g = tid >> 4;
     const uint32_t tg = (g % GT) * PT, rg = (g / GT) * PR;
     const uint32_t t0 = blockIdx.x * TT, r0 = blockIdx.y * TR;
-    const uint32_t S = H / 16, n16 = S * 16, ntiles = (S + 15) / 16;
-    // staging: the tile's TT + TR rows of 64 float4 each, item q = tid + 256 i
-    // -> row q / 64, float4 q % 64 of the row's 256 elements
-    constexpr uint32_t kItems = (TT + TR) * 64, kPer = (kItems + 255) / 256;
+    const uint32_t S = H / 16, n16 = S * 16, ntiles = (S + kRtSteps - 1) / kRtSteps;
+    // staging: the tile's TT + TR rows of kRtF4 float4 each, item q = tid +
+    // 256 i -> row q / kRtF4, float4 q % kRtF4 of the row's 16 kRtSteps elements
+    constexpr uint32_t kItems = (TT + TR) * kRtF4, kPer = (kItems + 255) / 256;
     const float *src[kPer];
 #pragma unroll
     for (uint32_t i = 0; i < kPer; ++i) {
-        const uint32_t q = tid + 256 * i, row = q / 64 < TT + TR ? q / 64 : 0;
+        const uint32_t q = tid + 256 * i, row = q / kRtF4 < TT + TR ? q / kRtF4 : 0;
         src[i] = row < TT ? h + static_cast<uint64_t>(t0 + row < tokens ? t0 + row : tokens - 1) * H
                           : a.router + static_cast<uint64_t>(r0 + row - TT < E ? r0 + row - TT : E - 1) * H;
     }
@@ -799,7 +801,7 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
         for (uint32_t i = 0; i < kPer; ++i) {
             const uint32_t q = tid + 256 * i;
             if (kItems % 256 != 0 && q >= kItems) break;
-            const uint32_t e = 256 * k + 4 * (q % 64);
+            const uint32_t e = 16 * kRtSteps * k + 4 * (q % kRtF4);
             const uint32_t ec = e + 4 <= n16 ? e : 0; // past the chains' elements: unused
             sv[i] = *reinterpret_cast<const float4 *>(src[i] + ec);
         }
@@ -809,7 +811,7 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
         for (uint32_t i = 0; i < kPer; ++i) {
             const uint32_t q = tid + 256 * i;
             if (kItems % 256 != 0 && q >= kItems) break;
-            const uint32_t row = q / 64, f = q % 64, s0 = f >> 2, c0 = 4 * (f & 3);
+            const uint32_t row = q / kRtF4, f = q % kRtF4, s0 = f >> 2, c0 = 4 * (f & 3);
             float *dst = (row < TT ? hl + row * kRtRow : wl + (row - TT) * kRtRow) + c0 * kRtPad + s0;
             dst[0] = sv[i].x;
             dst[kRtPad] = sv[i].y;
@@ -827,14 +829,15 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
         store_tile();
         __syncthreads();
         if (k + 1 < ntiles) load_tile(k + 1);
-        const uint32_t steps = S - 16 * k < 16 ? S - 16 * k : 16;
-        for (uint32_t s4 = 0; s4 < steps; s4 += 4) {
-            float4 hq[PT], wq[PR];
+        const uint32_t steps = S - kRtSteps * k < kRtSteps ? S - kRtSteps * k : kRtSteps;
+        // operands of steps s4 .. s4 + 3 from LDS, and their FMAs (ns of them)
+        auto read_ops = [&](float4 (&hq)[PT], float4 (&wq)[PR], uint32_t s4) {
 #pragma unroll
             for (uint32_t i = 0; i < PT; ++i) hq[i] = *reinterpret_cast<const float4 *>(&hl[(tg + i) * kRtRow + c * kRtPad + s4]);
 #pragma unroll
             for (uint32_t j = 0; j < PR; ++j) wq[j] = *reinterpret_cast<const float4 *>(&wl[(rg + j) * kRtRow + c * kRtPad + s4]);
-            const uint32_t ns = steps - s4 < 4 ? steps - s4 : 4;
+        };
+        auto fmas = [&](const float4 (&hq)[PT], const float4 (&wq)[PR], uint32_t ns) {
 #pragma unroll
             for (uint32_t u = 0; u < 4; ++u) {
                 if (u >= ns) break;
@@ -847,6 +850,24 @@ __global__ __launch_bounds__(256) void router_tile_kernel(RouteArgs a, const flo
                         acc[i][j] = fma_rn(wu, hu, acc[i][j]);
                     }
                 }
+            }
+        };
+        if (steps == kRtSteps) {
+            // a whole tile: the next four steps' operands requested before
+            // this four's FMAs
+            float4 hq[2][PT], wq[2][PR];
+            read_ops(hq[0], wq[0], 0);
+#pragma unroll
+            for (uint32_t s4 = 0; s4 < kRtSteps; s4 += 4) {
+                const uint32_t b = (s4 / 4) & 1;
+                if (s4 + 4 < kRtSteps) read_ops(hq[b ^ 1], wq[b ^ 1], s4 + 4);
+                fmas(hq[b], wq[b], 4);
+            }
+        } else {
+            for (uint32_t s4 = 0; s4 < steps; s4 += 4) {
+                float4 hq[PT], wq[PR];
+                read_ops(hq, wq, s4);
+                fmas(hq, wq, steps - s4 < 4 ? steps - s4 : 4);
             }
         }
         __syncthreads();
