@@ -722,13 +722,13 @@ __global__ __launch_bounds__(NT) __attribute__((aligned(kHotAlign))) void route_
     }
 }
 
-// RMSNorm of token blockIdx.x into h (batched routing). NT threads, 4 float4
-// per thread (hidden <= 16 NT); LDS: 2 hidden floats (the squares, for the
+// RMSNorm of token blockIdx.x into h (batched routing). NT threads, P float4
+// per thread (hidden <= 4 P NT; P = 2 up to hidden 2048 keeps the registers
+// of the unused half free); LDS: 2 hidden floats (the squares, for the
 // in-order sum when the certificate fails).
-template <uint32_t NT>
+template <uint32_t NT, uint32_t P = 4>
 __global__ __launch_bounds__(NT) void rmsnorm_kernel(RouteArgs a, const float *__restrict__ x,
                                                      float *__restrict__ h, uint32_t *__restrict__ clear) {
-    constexpr uint32_t P = 4;
     // the call's error word, zeroed by the first kernel of the call (no later
     // kernel of the call runs before this one ends, and this one sets no bit)
     if (clear && blockIdx.x == 0 && threadIdx.x == 0) *clear = 0;
@@ -1361,7 +1361,11 @@ size_t route_lds_bytes(uint32_t hidden) { return 2ull * 16 * route_chain_stride(
 int launch_rmsnorm(const RouteArgs &a, const float *x, uint32_t tokens, float *h, hipStream_t s,
                    uint32_t *clear = nullptr) {
     const size_t lds = 2ull * a.hidden * sizeof(float);
-    if (a.hidden <= 16 * 256) {
+    if (a.hidden <= 8 * 256) {
+        auto k = rmsnorm_kernel<256, 2>;
+        if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+        hipLaunchKernelGGL(k, dim3(tokens), dim3(256), lds, s, a, x, h, clear);
+    } else if (a.hidden <= 16 * 256) {
         auto k = rmsnorm_kernel<256>;
         if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
         hipLaunchKernelGGL(k, dim3(tokens), dim3(256), lds, s, a, x, h, clear);
