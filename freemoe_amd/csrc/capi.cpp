@@ -47,13 +47,13 @@ DecodeWorkspace decode_workspace(const fmx_moe_layer *L, uint32_t tokens) {
 
 // Prefill workspace (all offsets 256-byte aligned), pairs = tokens * top_k:
 //   [0, 256) error word | h [tokens x hidden] f32 | offsets [experts + 1] |
-//   token_list, rank_list, slot_of [pairs] | row tiles [1 + 3 * max_tiles] |
+//   token_list, slot_of [pairs] | row tiles [1 + 3 * max_tiles] |
 //   tile order [max_tiles] | chunk counts | x [tokens x hidden] bf16 | act [pairs + 192 rows x ffn] bf16 |
 //   dn [splits x pairs x hidden] f32 |
 //   the decode scratch (act of one token) for shapes the GEMMs do not tile |
 //   logits [tokens x experts] f32
 struct PrefillWorkspace {
-    uint64_t h = 0, offsets = 0, token_list = 0, rank_list = 0, slot_of = 0, tiles = 0, tile_order = 0,
+    uint64_t h = 0, offsets = 0, token_list = 0, slot_of = 0, tiles = 0, tile_order = 0,
              chunk_counts = 0, x = 0, act = 0, dn = 0,
              dec_act = 0, logits = 0, total = 0;
     uint32_t pairs = 0, max_tiles = 0;
@@ -70,7 +70,6 @@ PrefillWorkspace prefill_workspace(const fmx_moe_layer *L, uint32_t tokens) {
     w.h = take(static_cast<uint64_t>(tokens) * H * 4);
     w.offsets = take((E + 1) * 4);
     w.token_list = take(P * 4);
-    w.rank_list = take(P * 4);
     w.slot_of = take(P * 4);
     w.tiles = take((1 + 3ull * w.max_tiles) * 4);
     w.tile_order = take(static_cast<uint64_t>(w.max_tiles) * 4);
