@@ -23,6 +23,9 @@ ROUTE_CASES = {
     "sixteen_experts_odd_tokens": (256, 64, 16, 4, wl.F32, 37, None),
     "twelve_experts": (128, 64, 12, 3, wl.F32, 21, None),
     "forty_experts_partial_tiles": (260, 64, 40, 6, wl.F32, 45, 1.2),
+    # 16 x 32 tiles over a chain length (328 / 16 = 20 steps) that leaves a
+    # partial LDS tile of 4 steps after a whole one, and an 8-element tail
+    "twenty_experts_partial_steps": (328, 64, 20, 4, wl.F32, 37, None),
     # 256 experts, top-8, hidden 7168 (a DeepSeek-V3-sized router): hidden
     # beyond 4096 takes the 1024-thread RMSNorm and routing kernels
     "256_experts_hidden_7168": (7168, 32, 256, 8, wl.Q4_0, 24, 1.2),
