@@ -18,6 +18,7 @@ namespace {
 
 constexpr uint32_t kThreads = 256;              // 4 wavefronts
 constexpr uint32_t kLdsBudgetFloats = 8 * 1024; // 32 KiB of x per tile
+constexpr size_t kMatvecMaxLds = 128 * 1024;     // the Q6_K split kernel's x and dots
 
 template <class T, int NR>
 __global__ __launch_bounds__(kThreads) void matvec_kernel(
@@ -82,19 +83,38 @@ __global__ __launch_bounds__(kThreads) void matvec_q6_k_kernel(const uint8_t *__
 // Q6_K with few rows: G lane groups per row, group g taking blocks
 // g, g + G, ... (each block's dot is independent); the block dots meet in LDS
 // and one lane adds them in block order from 0, as q6_k_row_chains does.
-// LDS: (16 / G) rows x blocks floats.
-template <uint32_t G>
+// kXs: x staged in LDS first (block b at xs + b * kQ6XStride), so each input
+// is read from memory once per workgroup instead of once per row (worth its
+// LDS at 8 rows per workgroup).
+// LDS: (16 / G) rows x blocks dots, then x.
+__host__ __device__ inline uint32_t q6_split_dots_floats(uint32_t rows, uint32_t blocks) {
+    return (rows * blocks + 3u) & ~3u;
+}
+template <uint32_t G, bool kXs>
 __global__ __launch_bounds__(kThreads) void matvec_q6_k_split_kernel(const uint8_t *__restrict__ w,
                                                                      const float *__restrict__ x,
                                                                      float *__restrict__ y, uint32_t rows,
                                                                      uint32_t blocks) {
-    extern __shared__ float dots[];
+    extern __shared__ __align__(16) float q6_lds[];
     constexpr uint32_t kRows = kThreads / 16 / G;
+    float *dots = q6_lds;
     const uint32_t tid = threadIdx.x, c = tid & 15, grp = tid >> 4;
+    const float *xr = x;
+    uint32_t xstride = 256;
+    if constexpr (kXs) {
+        float *xs = q6_lds + q6_split_dots_floats(kRows, blocks);
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        for (uint32_t q = tid; q < blocks * 64; q += kThreads)
+            reinterpret_cast<float4 *>(xs + (q >> 6) * kQ6XStride)[q & 63] = x4[q];
+        __syncthreads();
+        xr = xs;
+        xstride = kQ6XStride;
+    }
     const uint32_t lr = grp / G, part = grp % G;
     const uint32_t r = blockIdx.x * kRows + lr;
     const uint32_t rr = r < rows ? r : rows - 1;
-    q6_k_block_dots(w + static_cast<uint64_t>(rr) * blocks * 210, x, blocks, part, G, c, dots + lr * blocks);
+    q6_k_block_dots(w + static_cast<uint64_t>(rr) * blocks * 210, xr, blocks, part, G, c, dots + lr * blocks,
+                    xstride);
     __syncthreads();
     if (tid < kRows && blockIdx.x * kRows + tid < rows) {
         const float *d = dots + tid * blocks;
@@ -150,14 +170,16 @@ extern "C" int fmx_matvec(uint32_t type_id, const void *packed, const float *x, 
         // or 2 groups
         const bool four = out_dim < 8192;
         const uint32_t rows_per_wg = four ? kThreads / 64 : kThreads / 32;
-        const size_t lds = static_cast<size_t>(rows_per_wg) * g.blocks * sizeof(float);
-        if (out_dim < 32768 && g.blocks >= 8 && lds <= 64 * 1024) {
-            if (four)
-                hipLaunchKernelGGL(matvec_q6_k_split_kernel<4>, dim3(div_up(out_dim, rows_per_wg)), dim3(kThreads),
-                                   lds, s, static_cast<const uint8_t *>(packed), x, y, out_dim, g.blocks);
-            else
-                hipLaunchKernelGGL(matvec_q6_k_split_kernel<2>, dim3(div_up(out_dim, rows_per_wg)), dim3(kThreads),
-                                   lds, s, static_cast<const uint8_t *>(packed), x, y, out_dim, g.blocks);
+        const size_t dots = q6_split_dots_floats(rows_per_wg, g.blocks) * sizeof(float);
+        const size_t with_x = dots + static_cast<size_t>(g.blocks) * kQ6XStride * sizeof(float);
+        if (out_dim < 32768 && g.blocks >= 8 && dots <= 64 * 1024) {
+            auto k = four ? matvec_q6_k_split_kernel<4, false>
+                          : with_x <= kMatvecMaxLds ? matvec_q6_k_split_kernel<2, true>
+                                                    : matvec_q6_k_split_kernel<2, false>;
+            const size_t lds = !four && with_x <= kMatvecMaxLds ? with_x : dots;
+            if (int rc = allow_lds(reinterpret_cast<const void *>(k), lds)) return rc;
+            hipLaunchKernelGGL(k, dim3(div_up(out_dim, rows_per_wg)), dim3(kThreads), lds, s,
+                               static_cast<const uint8_t *>(packed), x, y, out_dim, g.blocks);
             FMX_LAUNCH_CHECK();
             return FMX_OK;
         }

@@ -108,14 +108,22 @@ __device__ inline float q6_k_row_chains(const uint8_t *__restrict__ row, const f
     return total;
 }
 
+// Floats per Q6_K block of inputs staged in LDS: the 16 floats between
+// blocks put 16-lane groups of one wavefront that work on different blocks
+// on different banks.
+constexpr uint32_t kQ6XStride = 272;
+
 // Dots of blocks b0, b0 + stride, ... (< blocks) of one Q6_K row on 16
 // consecutive lanes, each as in q6_k_row_chains (chain c over elements
 // 16 m + c, the lanes' chains joined), the next block's share requested
-// before a block's chain runs; lane 0 writes block b's dot to out[b].
-__device__ inline void q6_k_block_dots(const uint8_t *__restrict__ row, const float *x, uint32_t blocks,
-                                       uint32_t b0, uint32_t stride, uint32_t c, float *out) {
+// before a block's chain runs; lane 0 writes block b's dot to out[b]. Block
+// b's 256 inputs start at x + b * xstride (256 in memory; more where x is
+// staged in LDS with padding between blocks).
+__device__ __forceinline__ void q6_k_block_dots(const uint8_t *__restrict__ row, const float *x, uint32_t blocks,
+                                                uint32_t b0, uint32_t stride, uint32_t c, float *out,
+                                                uint32_t xstride = 256) {
     Q6Lane q[2];
-    if (b0 < blocks) q[0].load(row + static_cast<uint64_t>(b0) * 210, x + static_cast<uint64_t>(b0) * 256, c);
+    if (b0 < blocks) q[0].load(row + static_cast<uint64_t>(b0) * 210, x + static_cast<uint64_t>(b0) * xstride, c);
     for (uint32_t b = b0; b < blocks; b += 2 * stride) {
 #pragma unroll
         for (uint32_t u = 0; u < 2; ++u) {
@@ -123,7 +131,7 @@ __device__ inline void q6_k_block_dots(const uint8_t *__restrict__ row, const fl
             if (bu >= blocks) break;
             const uint32_t nb = bu + stride;
             if (nb < blocks)
-                q[u ^ 1].load(row + static_cast<uint64_t>(nb) * 210, x + static_cast<uint64_t>(nb) * 256, c);
+                q[u ^ 1].load(row + static_cast<uint64_t>(nb) * 210, x + static_cast<uint64_t>(nb) * xstride, c);
             const float acc = q[u].chain();
             const float t = acc + lane_xor<8>(acc);
             const float dot = hsum8_lanes(t);

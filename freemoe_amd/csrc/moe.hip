@@ -1173,13 +1173,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1),
 }
 
 // F32 and Q6_K experts: 16 lanes per row (RowDot16: F32 in gemv_avx2_row's
-// order, Q6_K in row_dot_fused_scalar's), x read through the cache.
+// order, Q6_K in row_dot_fused_scalar's), h staged in LDS first (every row
+// of the workgroup reads all of it; the groups of a wavefront read the same
+// elements at once). LDS: hidden floats.
 template <uint32_t kT>
 __global__ __launch_bounds__(kThreads) void gate_up_rows16_kernel(ExpertArgs a, const float *__restrict__ h,
                                                                   const float *__restrict__ logits,
                                                                   uint32_t *__restrict__ ids, float *__restrict__ w,
                                                                   float *__restrict__ act,
                                                                   uint32_t *__restrict__ status) {
+    extern __shared__ __align__(16) float hl16[];
     const uint32_t tid = threadIdx.x, c = tid & 15;
     const uint32_t rank = blockIdx.y;
     const uint32_t e = expert_of_rank(a.route, logits, ids, rank, blockIdx.x == 0 && rank == 0, ids, w, status);
@@ -1188,13 +1191,19 @@ __global__ __launch_bounds__(kThreads) void gate_up_rows16_kernel(ExpertArgs a, 
         return;
     }
     const uint32_t F = a.ffn, H = a.hidden;
+    const float4 *h4 = reinterpret_cast<const float4 *>(h);
+    for (uint32_t q = tid; q < H / 4; q += kThreads) reinterpret_cast<float4 *>(hl16)[q] = h4[q];
+    __syncthreads();
     const uint32_t j = blockIdx.x * (kThreads / 16) + (tid >> 4);
     const uint32_t jr = j < F ? j : F - 1;
-    const float g = RowDot16<kT>::dot(a.gate[e], jr, h, H, c);
-    const float u = RowDot16<kT>::dot(a.up[e], jr, h, H, c);
+    const float g = RowDot16<kT>::dot(a.gate[e], jr, hl16, H, c);
+    const float u = RowDot16<kT>::dot(a.up[e], jr, hl16, H, c);
     if (c == 0 && j < F) act[static_cast<uint64_t>(rank) * F + j] = swiglu(g, u);
 }
 
+// F32 and Q6_K down rows on 16 lanes each (RowDot16), then the combine in
+// rank order and the residual, as down_kernel; 16 slots, 16 / top_k rows of
+// every rank per workgroup.
 template <uint32_t kT>
 __global__ __launch_bounds__(kThreads) void down_rows16_kernel(ExpertArgs a, const float *__restrict__ x,
                                                                const float *__restrict__ act,
@@ -1218,6 +1227,56 @@ __global__ __launch_bounds__(kThreads) void down_rows16_kernel(ExpertArgs a, con
     }
     const float v = RowDot16<kT>::dot(a.down[e], jr, act + static_cast<uint64_t>(rank) * F, F, c);
     if (c == 0 && slot < K * jpw) dres[slot] = bad ? 0.0f : v;
+    __syncthreads();
+    if (tid < jpw) {
+        const uint32_t jo = blockIdx.x * jpw + tid;
+        if (jo < H) {
+            float ffn = 0.0f;
+            for (uint32_t r = 0; r < K; ++r) ffn = ffn + w[r] * dres[r * jpw + tid];
+            out[jo] = x[jo] + ffn;
+        }
+    }
+}
+
+// Q6_K down rows with G 16-lane groups per row: group g takes blocks g,
+// g + G, ... (each block's dot is independent), the block dots meet in LDS
+// and one lane per row adds them in block order from 0 (as q6_k_row_chains
+// does), then the combine in rank order and the residual. 16 / G slots,
+// 16 / G / top_k rows of every rank per workgroup. LDS: 16 / G slots x
+// blocks floats.
+template <uint32_t G>
+__global__ __launch_bounds__(kThreads) void down_q6_k_split_kernel(ExpertArgs a, const float *__restrict__ x,
+                                                                   const float *__restrict__ act,
+                                                                   const uint32_t *__restrict__ ids,
+                                                                   const float *__restrict__ w,
+                                                                   float *__restrict__ out,
+                                                                   uint32_t *__restrict__ status) {
+    extern __shared__ float dots[];
+    constexpr uint32_t kSlots = kThreads / 16 / G;
+    __shared__ float dres[kSlots];
+    const uint32_t tid = threadIdx.x, c = tid & 15, grp = tid >> 4;
+    const uint32_t slot = grp / G, part = grp % G;
+    const uint32_t K = a.top_k, H = a.hidden, F = a.ffn, blocks = F / 256;
+    const uint32_t jpw = kSlots / K;
+    const uint32_t rank = slot / jpw < K ? slot / jpw : K - 1;
+    const uint32_t j = blockIdx.x * jpw + slot % jpw;
+    const uint32_t jr = j < H ? j : H - 1;
+    uint32_t e = ids[rank];
+    const bool bad = e >= a.experts;
+    if (bad) {
+        if (c == 0 && part == 0) atomicOr(status, STATUS_BAD_EXPERT);
+        e = 0;
+    }
+    q6_k_block_dots(static_cast<const uint8_t *>(a.down[e]) + static_cast<uint64_t>(jr) * blocks * 210,
+                    act + static_cast<uint64_t>(rank) * F, blocks, part, G, c, dots + slot * blocks);
+    __syncthreads();
+    if (tid < K * jpw) {
+        // slot tid: rank tid / jpw
+        const float *d = dots + tid * blocks;
+        float v = 0.0f;
+        for (uint32_t b = 0; b < blocks; ++b) v = v + d[b];
+        dres[tid] = ids[tid / jpw] >= a.experts ? 0.0f : v;
+    }
     __syncthreads();
     if (tid < jpw) {
         const uint32_t jo = blockIdx.x * jpw + tid;
@@ -1294,15 +1353,27 @@ int launch_gate_up(const ExpertArgs &a, const float *h, const float *logits, uin
     const dim3 grid16(div_up(a.ffn, kThreads / 16), a.top_k);
     switch (a.type_gu) {
     case FMX_TYPE_F32:
-        return launch_timed(gate_up_rows16_kernel<FMX_TYPE_F32>, grid16, 0, s, kev, a, h, logits, ids, w, act, status);
+        return launch_timed(gate_up_rows16_kernel<FMX_TYPE_F32>, grid16, a.hidden * sizeof(float), s, kev, a, h, logits,
+                            ids, w, act, status);
     case FMX_TYPE_Q6_K:
-        return launch_timed(gate_up_rows16_kernel<FMX_TYPE_Q6_K>, grid16, 0, s, kev, a, h, logits, ids, w, act,
-                            status);
+        return launch_timed(gate_up_rows16_kernel<FMX_TYPE_Q6_K>, grid16, a.hidden * sizeof(float), s, kev, a, h, logits,
+                            ids, w, act, status);
     case FMX_TYPE_Q4_0: return launch_gate_up_q<Q40>(a, h, logits, ids, w, act, status, s, kev);
     case FMX_TYPE_Q8_0: return launch_gate_up_q<Q80>(a, h, logits, ids, w, act, status, s, kev);
     case FMX_TYPE_Q4_K: return launch_gate_up_q<Q4K>(a, h, logits, ids, w, act, status, s, kev);
     }
     return FMX_ERR_UNSUPPORTED_QUANTISATION;
+}
+
+// down_q6_k_split_kernel<G>: 16 / G row slots over the ranks per workgroup.
+template <uint32_t G>
+int launch_down_q6_k_split(const ExpertArgs &a, const float *x, const float *act, const uint32_t *ids,
+                           const float *w, float *out, uint32_t *status, hipStream_t s, const hipEvent_t *kev) {
+    constexpr uint32_t kSlots = kThreads / 16 / G;
+    const size_t lds = static_cast<size_t>(kSlots) * (a.ffn / 256) * sizeof(float);
+    if (int rc = allow_lds(reinterpret_cast<const void *>(down_q6_k_split_kernel<G>), lds)) return rc;
+    return launch_timed(down_q6_k_split_kernel<G>, dim3(div_up(a.hidden, kSlots / a.top_k)), lds, s, kev, a, x, act,
+                        ids, w, out, status);
 }
 
 int launch_down(const ExpertArgs &a, const float *x, const float *act, const uint32_t *ids, const float *w,
@@ -1314,6 +1385,12 @@ int launch_down(const ExpertArgs &a, const float *x, const float *act, const uin
     case FMX_TYPE_F32:
         return launch_timed(down_rows16_kernel<FMX_TYPE_F32>, grid16(), 0, s, kev, a, x, act, ids, w, out, status);
     case FMX_TYPE_Q6_K:
+        // Q6_K rows of many blocks split over four (or two) lane groups
+        // each, while every rank keeps a row slot
+        if (a.top_k <= kThreads / 64 && a.ffn / 256 >= 8)
+            return launch_down_q6_k_split<4>(a, x, act, ids, w, out, status, s, kev);
+        if (a.top_k <= kThreads / 32 && a.ffn / 256 >= 8)
+            return launch_down_q6_k_split<2>(a, x, act, ids, w, out, status, s, kev);
         return launch_timed(down_rows16_kernel<FMX_TYPE_Q6_K>, grid16(), 0, s, kev, a, x, act, ids, w, out,
                             status);
     case FMX_TYPE_Q4_0:

@@ -475,6 +475,18 @@ def test_block_type_router(gpu, name):
     tp.check_prefill(gpu, lw, x)
 
 
+@pytest.mark.parametrize("top_k", [2, 3, 6])
+def test_decode_q6_k_rows_split_over_lane_groups(gpu, top_k):
+    """Q6_K down rows of at least 8 blocks run on four 16-lane groups each
+    (two past top-4; every fourth or second block, the block dots added in
+    block order from LDS), the gate/up rows against h staged in LDS; top-3
+    and top-6 leave row slots past the last rank unused: the layer stays bit
+    for bit."""
+    lw = wl.make_layer(2048, 2560, 8, top_k, wl.Q6_K, 97)
+    x = wl.inputs(2048, 4, 98)
+    assert check_layer(gpu, lw, x) == 0
+
+
 @pytest.mark.parametrize("gate_type,down_type", [(wl.Q4_K, wl.Q8_0), (wl.Q8_0, wl.Q4_0), (wl.Q4_0, wl.Q4_K),
                                                  (wl.Q4_K, wl.Q6_K), (wl.Q6_K, wl.Q8_0), (wl.Q6_K, wl.Q6_K),
                                                  (wl.F32, wl.Q4_0)])
