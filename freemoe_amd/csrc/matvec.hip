@@ -55,16 +55,32 @@ __global__ __launch_bounds__(kThreads) void matvec_kernel(
 }
 
 // F32: 16 lanes per row (4 row slots per wavefront, 16 per workgroup).
+// kXs: x staged in LDS first (n floats), so each input is read from memory
+// once per workgroup instead of once per row; the groups of a wavefront read
+// the same elements at once.
+template <bool kXs>
 __global__ __launch_bounds__(kThreads) void matvec_f32_kernel(const float *__restrict__ w,
                                                               const float *__restrict__ x,
                                                               float *__restrict__ y,
                                                               uint32_t rows, uint32_t n) {
+    extern __shared__ __align__(16) float xs_f32[];
     const uint32_t tid = threadIdx.x;
     const uint32_t c = tid & 15;
+    const float *xr = x;
+    if constexpr (kXs) {
+        if ((reinterpret_cast<uintptr_t>(x) & 15u) == 0 && n % 4 == 0) {
+            const float4 *x4 = reinterpret_cast<const float4 *>(x);
+            for (uint32_t q = tid; q < n / 4; q += kThreads) reinterpret_cast<float4 *>(xs_f32)[q] = x4[q];
+        } else {
+            for (uint32_t q = tid; q < n; q += kThreads) xs_f32[q] = x[q];
+        }
+        __syncthreads();
+        xr = xs_f32;
+    }
     const uint32_t r = blockIdx.x * (kThreads / 16) + (tid >> 4);
     const uint32_t rr = r < rows ? r : rows - 1;
     const float *row = w + static_cast<uint64_t>(rr) * n;
-    const float total = f32_row_chains(row, x, n, c);
+    const float total = f32_row_chains(row, xr, n, c);
     if (c == 0 && r < rows) y[r] = total;
 }
 
@@ -157,8 +173,13 @@ extern "C" int fmx_matvec(uint32_t type_id, const void *packed, const float *x, 
     hipStream_t s = static_cast<hipStream_t>(stream);
     switch (type_id) {
     case FMX_TYPE_F32:
-        hipLaunchKernelGGL(matvec_f32_kernel, dim3(div_up(out_dim, kThreads / 16)), dim3(kThreads), 0,
-                           s, static_cast<const float *>(packed), x, y, out_dim, in_dim);
+        if (in_dim <= 16384)
+            hipLaunchKernelGGL(matvec_f32_kernel<true>, dim3(div_up(out_dim, kThreads / 16)), dim3(kThreads),
+                               static_cast<size_t>(in_dim) * sizeof(float), s, static_cast<const float *>(packed), x, y,
+                               out_dim, in_dim);
+        else
+            hipLaunchKernelGGL(matvec_f32_kernel<false>, dim3(div_up(out_dim, kThreads / 16)), dim3(kThreads), 0, s,
+                               static_cast<const float *>(packed), x, y, out_dim, in_dim);
         FMX_LAUNCH_CHECK();
         return FMX_OK;
     case FMX_TYPE_Q4_0: return launch_matvec<Q40, 2>(g, packed, x, y, s);

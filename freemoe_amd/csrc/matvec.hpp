@@ -15,8 +15,29 @@ __device__ inline float f32_row_chains(const float *__restrict__ row, const floa
                                        uint32_t c) {
     float acc = 0.0f;
     const uint32_t n16 = n / 16 * 16;
+    // the chain is a dependent FMA sequence: the row's elements are requested
+    // kB steps at a time, the next batch before this one's FMAs
+    constexpr uint32_t kB = 16;
+    const uint32_t nb = n16 / (16 * kB);
+    float wb[2][kB];
+    if (nb > 0) {
+#pragma unroll
+        for (uint32_t u = 0; u < kB; ++u) wb[0][u] = row[16 * u + c];
+    }
+    for (uint32_t bi = 0; bi < nb; bi += 2) {
+#pragma unroll
+        for (uint32_t half = 0; half < 2; ++half) {
+            const uint32_t b = bi + half;
+            if (b >= nb) break;
+            const uint32_t k0 = 16 * kB * b, kn = 16 * kB * (b + 1 < nb ? b + 1 : b);
+#pragma unroll
+            for (uint32_t u = 0; u < kB; ++u) wb[half ^ 1][u] = row[kn + 16 * u + c];
+#pragma unroll
+            for (uint32_t u = 0; u < kB; ++u) acc = fma_rn(wb[half][u], x[k0 + 16 * u + c], acc);
+        }
+    }
 #pragma unroll 8
-    for (uint32_t k = 0; k < n16; k += 16) acc = fma_rn(row[k + c], x[k + c], acc);
+    for (uint32_t k = 16 * kB * nb; k < n16; k += 16) acc = fma_rn(row[k + c], x[k + c], acc);
     const bool tail8 = n - n16 >= 8;
     if (tail8 && c < 8) acc = fma_rn(row[n16 + c], x[n16 + c], acc);
     const float t = acc + lane_xor<8>(acc);
