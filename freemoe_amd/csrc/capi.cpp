@@ -611,6 +611,12 @@ int fmx_attention_decode(const float *q, const float *kv, uint64_t row_stride, u
                             static_cast<uint32_t *>(workspace), static_cast<hipStream_t>(stream));
 }
 
+int fmx_moe_status_of(uint32_t word) {
+    if (word & STATUS_BAD_EXPERT) return FMX_ERR_INVALID_ARGUMENT;
+    if (word & STATUS_NONFINITE_SCORE) return FMX_ERR_INTERNAL;
+    return FMX_OK;
+}
+
 int fmx_moe_status(void *workspace, void *stream) {
     if (!workspace) return FMX_ERR_INVALID_ARGUMENT;
     if (int rc = fault_gate()) return rc;
@@ -620,8 +626,16 @@ int fmx_moe_status(void *workspace, void *stream) {
     FMX_HIP_TRY(hipStreamSynchronize(s));
     hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, static_cast<uint32_t *>(workspace));
     FMX_LAUNCH_CHECK();
-    if (word & STATUS_BAD_EXPERT) return FMX_ERR_INVALID_ARGUMENT;
-    if (word & STATUS_NONFINITE_SCORE) return FMX_ERR_INTERNAL;
+    return fmx_moe_status_of(word);
+}
+
+int fmx_moe_status_copy(void *workspace, uint32_t *host_word, void *stream) {
+    if (!workspace || !host_word) return FMX_ERR_INVALID_ARGUMENT;
+    if (int rc = fault_gate()) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    FMX_HIP_TRY(hipMemcpyAsync(host_word, workspace, 4, hipMemcpyDeviceToHost, s));
+    hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(1), 0, s, static_cast<uint32_t *>(workspace));
+    FMX_LAUNCH_CHECK();
     return FMX_OK;
 }
 

@@ -85,6 +85,8 @@ _SIGNATURES = {
     "fmx_moe_prefill_timed": (c_int, [POINTER(MoELayer), c_void_p, c_void_p, c_uint32, c_void_p, c_void_p,
                                       c_void_p, c_uint64, c_void_p, POINTER(c_double)]),
     "fmx_moe_status": (c_int, [c_void_p, c_void_p]),
+    "fmx_moe_status_copy": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "fmx_moe_status_of": (c_int, [c_uint32]),
     "fmx_attention_decode": (c_int, [c_void_p, c_void_p, c_uint64, c_uint32, c_uint32, c_uint32, c_uint32, c_uint32,
                                      c_double, c_void_p, c_void_p, c_uint64, c_void_p]),
     "fmx_moe_bucket": (c_int, [c_void_p, c_uint32, c_uint32, c_uint32, c_void_p, c_void_p, c_void_p, c_void_p,

@@ -80,6 +80,10 @@ struct HipBackend::State {
     // vectors are pageable): one copy in and one out per call
     void *stage_in = nullptr, *stage_out = nullptr;
     uint64_t stage_in_cap = 0, stage_out_cap = 0;
+    // pinned host word receiving a fused call's device error word, read in
+    // the same synchronisation as the call's outputs
+    void *status_word = nullptr;
+    uint64_t status_word_cap = 0;
 
     uint8_t *pinned(void *&buf, uint64_t &cap, uint64_t bytes) {
         if (bytes > cap) {
@@ -116,6 +120,7 @@ struct HipBackend::State {
         fmx_free(attn_status);
         fmx_host_free(stage_in);
         fmx_host_free(stage_out);
+        fmx_host_free(status_word);
     }
 
     const Twin *find_twin(const void *host, uint64_t *offset) const {
@@ -551,6 +556,9 @@ bool HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, ui
                          reinterpret_cast<uint32_t *>(sm + o_ids), reinterpret_cast<float *>(sm + o_w), s.moe_ws,
                          s.moe_ws_cap, s.stream),
           "moe layer " + l);
+    // the error word comes back with the outputs (one synchronisation)
+    uint32_t *word = reinterpret_cast<uint32_t *>(s.pinned(s.status_word, s.status_word_cap, 4));
+    check(fmx_moe_status_copy(s.moe_ws, word, s.stream), "router scores of layer " + l);
     {
         // out, ids and weights back in one copy of [out | ids | weights]
         uint8_t *hout = s.pinned(s.stage_out, s.stage_out_cap, small - o_out);
@@ -559,7 +567,7 @@ bool HipBackend::moe_layer(const MoeLayerView &L, const float *x, float *out, ui
         std::memcpy(ids, hout + (o_ids - o_out), K * 4ull);
         std::memcpy(weights, hout + (o_w - o_out), K * 4ull);
     }
-    check(fmx_moe_status(s.moe_ws, s.stream), "router scores of layer " + l);
+    check(fmx_moe_status_of(*word), "router scores of layer " + l);
 
     // the reference's operation log for this block (engine.cpp:1603-1776)
     record_operation({"router.L" + l, name(), router_bytes + H * 4ull, E * 4ull});
@@ -615,8 +623,10 @@ bool HipBackend::attention(const AttentionView &A, const float *q, float *out) {
                                static_cast<uint32_t>(P), A.scale, static_cast<float *>(s.y_dev), s.attn_status, 256,
                                s.stream),
           "attention.L" + std::to_string(A.layer));
+    uint32_t *word = reinterpret_cast<uint32_t *>(s.pinned(s.status_word, s.status_word_cap, 4));
+    check(fmx_moe_status_copy(s.attn_status, word, s.stream), "attention status");
     s.download_staged(out, s.y_dev, qo_bytes);
-    check(fmx_moe_status(s.attn_status, s.stream), "non-finite attention score in layer " + std::to_string(A.layer));
+    check(fmx_moe_status_of(*word), "non-finite attention score in layer " + std::to_string(A.layer));
     record_operation({"attention.L" + std::to_string(A.layer), name(), P * A.kv_heads * D * 8 + qo_bytes, qo_bytes});
     return true;
 }

@@ -248,6 +248,16 @@ int fmx_moe_prefill_timed(const fmx_moe_layer *layer, const float *x, float *out
  * expert id out of range): reads and clears it, blocking on `stream`. */
 int fmx_moe_status(void *workspace, void *stream);
 
+/* The error word of `workspace` queued for copy into *host_word and cleared,
+ * in stream order, without waiting: *host_word holds it once the stream has
+ * been synchronised (host_word from fmx_host_alloc, so the copy runs
+ * asynchronously), and fmx_moe_status_of turns it into the status
+ * fmx_moe_status returns. Lets a caller that synchronises for its outputs
+ * anyway read the word in the same wait. No counterpart in the reference,
+ * whose kernels raise on the host. */
+int fmx_moe_status_copy(void *workspace, uint32_t *host_word, void *stream);
+int fmx_moe_status_of(uint32_t word);
+
 /* Per-expert token lists from a routing table ids[tokens x top_k] (device):
  * offsets[experts+1], token_list/rank_list[tokens*top_k] as the reference's
  * routing record (engine.cpp:1707) inverted: tokens ascending within each
