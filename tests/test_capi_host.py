@@ -40,6 +40,18 @@ def test_abi_version_and_status_names():
     assert lib.fmx_status_name(8) == b"DEVICE_LOSS"
 
 
+def test_status_word_mapping():
+    """fmx_moe_status_of maps a device error word as fmx_moe_status does: an
+    expert id out of range wins (INVALID_ARGUMENT), else a non-finite score
+    (INTERNAL_ERROR)."""
+    lib = fmx.lib()
+    assert lib.fmx_moe_status_of(0) == 0
+    assert lib.fmx_moe_status_of(1) == 4
+    assert lib.fmx_moe_status_of(2) == 1
+    assert lib.fmx_moe_status_of(3) == 1
+    assert lib.fmx_moe_status_copy(None, None, None) == 1
+
+
 def test_geometry_matches_reference_table():
     lib = fmx.lib()
     for t, (bs, bb) in {0: (1, 4), 2: (32, 18), 8: (32, 34), 12: (256, 144)}.items():

@@ -370,6 +370,15 @@ def test_decode_reports_nonfinite_scores(gpu):
     assert dl.status() == 4  # INTERNAL_ERROR, as the reference's softmax raises
     assert (to_np(ids) < 4).all()
     assert dl.status() == 0  # read-and-clear
+    # the asynchronous read: queued with the stream, read after its
+    # synchronisation, the word cleared behind it
+    dl.decode(torch.from_numpy(x).to(gpu))
+    word = torch.full((1,), 7, dtype=torch.int32).pin_memory()
+    ws = dl.workspace
+    assert fmx.lib().fmx_moe_status_copy(ws.data_ptr(), word.data_ptr(), fmx.stream_handle()) == 0
+    torch.cuda.synchronize()
+    assert fmx.lib().fmx_moe_status_of(int(word[0])) == 4
+    assert dl.status() == 0
 
 
 def test_bucket_exact_vs_oracle(gpu):
