@@ -219,6 +219,7 @@ def prefill_leg(dev, workload=PREFILL_WORKLOAD, seed=1234, reps=10, cpu=True, cp
                      "flops": flops, "hbm_achieved_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                      "hbm_bytes": wbytes + act_bytes, "ragged_bound_ms": round(ragged_s * 1e3, 4),
                      "ragged_frac": round(ragged_s * 1e3 / ms, 4)}}
+    res["library_bf16_gemm"] = library_gemm_reference(dev, counts, H, F, reps)
     if cpu:
         sys.path.insert(0, str(ROOT / "oracle"))
         import fmoracle as fo
@@ -242,6 +243,53 @@ def prefill_leg(dev, workload=PREFILL_WORKLOAD, seed=1234, reps=10, cpu=True, cp
         want_ids = hl.forward_batch(x[:n])[1]
         res["parity"]["ids_equal"] = bool(np.array_equal(ids[:n].cpu().numpy().astype(np.uint32), want_ids))
     del dl
+    torch.cuda.empty_cache()
+    return res
+
+
+def library_gemm_reference(dev, counts, H, F, reps):
+    """The vendor library's plain bf16 GEMMs (torch.mm, hipBLASLt) of the same
+    ragged shapes, for scale: per expert with n pairs, [n x H] x [H x 2F]
+    (gate and up) and [n x F] x [F x H] (down), over bf16 weights (2 bytes
+    per weight against the block types' 0.56-1.06, and no dequantisation),
+    timed with HIP events over all experts."""
+    import torch
+    live = [int(n) for n in counts if n > 0]
+    nmax = max(live)
+    g = torch.Generator(device=dev).manual_seed(7)
+    a = torch.randn(nmax, H, dtype=torch.bfloat16, device=dev, generator=g)
+    act = torch.randn(nmax, F, dtype=torch.bfloat16, device=dev, generator=g)
+    wgu = [torch.randn(H, 2 * F, dtype=torch.bfloat16, device=dev, generator=g) for _ in live]
+    wdn = [torch.randn(F, H, dtype=torch.bfloat16, device=dev, generator=g) for _ in live]
+    ogu = torch.empty(nmax, 2 * F, dtype=torch.bfloat16, device=dev)
+    odn = torch.empty(nmax, H, dtype=torch.bfloat16, device=dev)
+
+    def gate_up():
+        for i, n in enumerate(live):
+            torch.mm(a[:n], wgu[i], out=ogu[:n])
+
+    def down():
+        for i, n in enumerate(live):
+            torch.mm(act[:n], wdn[i], out=odn[:n])
+
+    res = {}
+    pairs = sum(live)
+    for name, fn, fl in (("gate_up", gate_up, 4.0 * pairs * H * F), ("down", down, 2.0 * pairs * H * F)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        stop.record()
+        torch.cuda.synchronize()
+        us = start.elapsed_time(stop) / reps * 1e3
+        res[name] = {"mean_us": round(us, 3), "achieved_TFLOPs": round(fl / us / 1e6, 1),
+                     "frac": round(fl / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4)}
+    res["note"] = ("torch.mm (hipBLASLt) bf16 x bf16 over the same per-expert row counts, one call per expert and "
+                   "projection, bf16 weights")
+    del a, act, wgu, wdn, ogu, odn
     torch.cuda.empty_cache()
     return res
 

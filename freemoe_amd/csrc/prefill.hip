@@ -141,33 +141,38 @@ struct GQ40 {
         w.q[1] = ld16(q + 16);
         w.d = ld16(packed + static_cast<uint64_t>(r) * g.blocks_padded * 2 + static_cast<uint64_t>(c) * 16);
     }
-    // The chunk's block scales d and -8 d as floats, once per step.
+    // The chunk's block scales as 2^9 d and -8 d, once per step.
     struct Dec {
-        float d[8], nd[8];
+        float d9[8], nd[8];
     };
     __device__ static void decode(const WStep &w, Dec &c) {
         const uint32_t dw[4] = {w.d.x, w.d.y, w.d.z, w.d.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            c.d[j] = half_bits_to_float((j & 1) ? dw[j >> 1] >> 16 : dw[j >> 1] & 0xFFFFu);
-            c.nd[j] = -8.0f * c.d[j];
+            const float d = half_bits_to_float((j & 1) ? dw[j >> 1] >> 16 : dw[j >> 1] & 0xFFFFu);
+            c.d9[j] = d * 0x1p9f;
+            c.nd[j] = -8.0f * d;
         }
     }
     // Positions 64 h + 8 kk .. +8 of the step: dword kk % 4 of the lane's slice
     // kk / 4; its bytes are blocks 2 (kk % 4) (bytes 0, 1) and 2 (kk % 4) + 1
-    // (bytes 2, 3), low nibble first. d (q - 8) = fma(d, q, -8 d) exactly (both
-    // products are exact in f32).
+    // (bytes 2, 3), low nibble first. The nibbles, one per byte, become floats
+    // two at a time read as fp8 (q 2^-9, exact), and d (q - 8) =
+    // fma(2^9 d, q 2^-9, -8 d) exactly (the product is d q, exact in f32; d
+    // comes from an f16, so 2^9 d is exact too).
     __device__ static bf16x8 dequant_kk(const WStep &w, const Dec &c, int kk) {
         const uint4 q = w.q[kk >> 2];
         const int i = kk & 3;
         const uint32_t qw = i == 0 ? q.x : i == 1 ? q.y : i == 2 ? q.z : q.w;
         const uint32_t lo = qw & 0x0F0F0F0Fu, hi = (qw >> 4) & 0x0F0F0F0Fu;
+        const float2 l01 = fp8_pair<false>(lo), l23 = fp8_pair<true>(lo);
+        const float2 h01 = fp8_pair<false>(hi), h23 = fp8_pair<true>(hi);
+        const float lq[4] = {l01.x, l01.y, l23.x, l23.y}, hq[4] = {h01.x, h01.y, h23.x, h23.y};
         uint32_t v[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-            const float d = c.d[2 * i + (b >> 1)], nd = c.nd[2 * i + (b >> 1)];
-            v[b] = pack_bf16x2(__builtin_fmaf(d, static_cast<float>((lo >> (8 * b)) & 0xFFu), nd),
-                               __builtin_fmaf(d, static_cast<float>((hi >> (8 * b)) & 0xFFu), nd));
+            const float d = c.d9[2 * i + (b >> 1)], nd = c.nd[2 * i + (b >> 1)];
+            v[b] = pack_bf16x2(__builtin_fmaf(d, lq[b], nd), __builtin_fmaf(d, hq[b], nd));
         }
         return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
     }
@@ -197,8 +202,9 @@ struct GQ4K {
         w.q[1] = ld16(q + 16);
         w.hd = ld16(packed + (static_cast<uint64_t>(r) * g.chunks + c) * 16);
     }
-    // The super-block's sub-block scales d sc_j and negated mins -dmin m_j
-    // (j < 8) as floats, once per step; both products are exact in f32.
+    // The super-block's sub-block scales 2^9 d sc_j and negated mins
+    // -dmin m_j (j < 8) as floats, once per step; the products are exact in
+    // f32 (an f16 times a 6-bit integer, times a power of two).
     struct Dec {
         float d[8], nm[8];
     };
@@ -211,24 +217,27 @@ struct GQ4K {
         for (int j = 0; j < 8; ++j) {
             uint32_t sc, m;
             k4_scale_min(j, hdr + 4, sc, m);
-            c.d[j] = d * static_cast<float>(sc);
+            c.d[j] = d * static_cast<float>(sc) * 0x1p9f;
             c.nm[j] = -(dmin * static_cast<float>(m));
         }
     }
     // Positions 64 h + 8 kk .. +8 of the step: dword g = kk % 4 of the lane's
-    // slice kk / 4, group g: low nibbles sub-block 2 g, high 2 g + 1.
-    // d sc q - dmin m = fma(d sc, q, -dmin m) exactly (d sc q is exact).
+    // slice kk / 4, group g: low nibbles sub-block 2 g, high 2 g + 1. The
+    // nibbles become floats two at a time read as fp8 (q 2^-9, exact), and
+    // d sc q - dmin m = fma(2^9 d sc, q 2^-9, -dmin m) exactly (d sc q is exact).
     __device__ static bf16x8 dequant_kk(const WStep &w, const Dec &c, int kk) {
         const uint4 q = w.q[kk >> 2];
         const int gi = kk & 3;
         const uint32_t qw = gi == 0 ? q.x : gi == 1 ? q.y : gi == 2 ? q.z : q.w;
         const uint32_t lo = qw & 0x0F0F0F0Fu, hi = (qw >> 4) & 0x0F0F0F0Fu;
         const float d1 = c.d[2 * gi], m1 = c.nm[2 * gi], d2 = c.d[2 * gi + 1], m2 = c.nm[2 * gi + 1];
+        const float2 l01 = fp8_pair<false>(lo), l23 = fp8_pair<true>(lo);
+        const float2 h01 = fp8_pair<false>(hi), h23 = fp8_pair<true>(hi);
+        const float lq[4] = {l01.x, l01.y, l23.x, l23.y}, hq[4] = {h01.x, h01.y, h23.x, h23.y};
         uint32_t v[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k)
-            v[k] = pack_bf16x2(__builtin_fmaf(d1, static_cast<float>((lo >> (8 * k)) & 0xFFu), m1),
-                               __builtin_fmaf(d2, static_cast<float>((hi >> (8 * k)) & 0xFFu), m2));
+            v[k] = pack_bf16x2(__builtin_fmaf(d1, lq[k], m1), __builtin_fmaf(d2, hq[k], m2));
         return __builtin_bit_cast(bf16x8, make_uint4(v[0], v[1], v[2], v[3]));
     }
 };
