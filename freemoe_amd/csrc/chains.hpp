@@ -138,7 +138,7 @@ struct Q40 {
     };
     __device__ static Chunk load(const Row &w, uint32_t c) {
         Chunk k;
-        k.q = ld16(w.quants + static_cast<uint64_t>(c) * 128);
+        k.q = ld16nt(w.quants + static_cast<uint64_t>(c) * 128);
         k.s = ld16(w.scales + static_cast<uint64_t>(c) * 16);
         return k;
     }
@@ -292,7 +292,7 @@ struct Q80 {
     };
     __device__ static Chunk load(const Row &w, uint32_t c) {
         Chunk k;
-        k.q = ld16(w.quants + static_cast<uint64_t>(c) * 128);
+        k.q = ld16nt(w.quants + static_cast<uint64_t>(c) * 128);
         k.s = ld8(w.scales + static_cast<uint64_t>(c) * 8);
         return k;
     }
@@ -390,7 +390,7 @@ struct Q4K {
     };
     __device__ static Chunk load(const Row &w, uint32_t c) {
         Chunk k;
-        k.q = ld16(w.quants + static_cast<uint64_t>(c) * 128);
+        k.q = ld16nt(w.quants + static_cast<uint64_t>(c) * 128);
         k.h = ld16(w.header + static_cast<uint64_t>(c) * 16);
         return k;
     }

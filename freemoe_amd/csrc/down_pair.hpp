@@ -191,7 +191,7 @@ __device__ __forceinline__ float pair_stream(const uint8_t *qp, const uint8_t *s
 #pragma unroll
         for (uint32_t p = 0; p < kSlots; ++p) {
             PairChunk &nx = buf[(p + PF) % kSlots];
-            nx.q = ld8(qp + (p + PF) * 128);
+            nx.q = ld8nt(qp + (p + PF) * 128);
             nx.s = ld16(sp + (p + PF) * 16);
             __builtin_amdgcn_sched_barrier(0);
             float cv[P::kNV];
@@ -207,7 +207,7 @@ __device__ __forceinline__ float pair_stream(const uint8_t *qp, const uint8_t *s
         if (c + p >= c_end) break;
         if (c + p + PF < c_end) {
             PairChunk &nx = buf[(p + PF) % kSlots];
-            nx.q = ld8(qp + (p + PF) * 128);
+            nx.q = ld8nt(qp + (p + PF) * 128);
             nx.s = ld16(sp + (p + PF) * 16);
         }
         float cv[P::kNV];
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(kPairThreads) __attribute__((amdgpu_waves_per_eu(2,
 #pragma unroll
     for (int p = 0; p < PF; ++p) {
         const uint32_t c = static_cast<uint32_t>(p) < c_end ? p : c_end - 1;
-        buf[p].q = ld8(qp + c * 128);
+        buf[p].q = ld8nt(qp + c * 128);
         buf[p].s = ld16(sp + c * 16);
     }
     bool scaled = false;

@@ -197,6 +197,23 @@ __device__ __forceinline__ uint2 ld8(const void *p) {
     return make_uint2(v.x, v.y);
 }
 
+// The same loads marked non-temporal (the nt cache policy: streamed data,
+// read once), for the decode kernels' weight quants, so the expert stream
+// does not evict what the token's kernels read again (the block scales that
+// consecutive chunks share, the activations, h). Mixtral-shaped decode per
+// 1000 tokens: Q4_0 53.9 -> 52.2 ms, Q8_0 88.4 -> 83.0 ms, Q4_K unchanged.
+// The prefill GEMMs keep plain loads (nt: 0.74 -> 0.85 ms for 512 Q8_0
+// tokens).
+__device__ __forceinline__ uint4 ld16nt(const void *p) {
+    const fmx_u32x4 v = __builtin_nontemporal_load((fmx_global_u32x4 *)(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint2 ld8nt(const void *p) {
+    const fmx_u32x2 v = __builtin_nontemporal_load((fmx_global_u32x2 *)(p));
+    return make_uint2(v.x, v.y);
+}
+
 // 6-bit scale/min pair j of a Q4_K super-block (quant.cpp:63-71).
 __device__ __forceinline__ void k4_scale_min(int j, const uint8_t *q, uint32_t &sc, uint32_t &m) {
     if (j < 4) {
