@@ -214,6 +214,10 @@ __device__ __forceinline__ uint2 ld8nt(const void *p) {
     return make_uint2(v.x, v.y);
 }
 
+__device__ __forceinline__ float ldf_nt(const float *p) {
+    return __builtin_nontemporal_load((const __attribute__((address_space(1))) float *)(p));
+}
+
 // 6-bit scale/min pair j of a Q4_K super-block (quant.cpp:63-71).
 __device__ __forceinline__ void k4_scale_min(int j, const uint8_t *q, uint32_t &sc, uint32_t &m) {
     if (j < 4) {

@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void matvec_f32_kernel(const float *__res
     const uint32_t r = blockIdx.x * (kThreads / 16) + (tid >> 4);
     const uint32_t rr = r < rows ? r : rows - 1;
     const float *row = w + static_cast<uint64_t>(rr) * n;
-    const float total = f32_row_chains(row, xr, n, c);
+    const float total = f32_row_chains<true>(row, xr, n, c);
     if (c == 0 && r < rows) y[r] = total;
 }
 

@@ -11,8 +11,19 @@ namespace fmx {
 // FMA, chains 0..7 take the 8-element tail, lanes c and c+8 add (acc0 + acc1),
 // the 8-lane tree sum follows, then an FMA tail over the last n mod 8 elements.
 // Every lane of the group returns the row's value. `x` may point to LDS.
+// kNT: the row's batches read with non-temporal loads. The matrix-vector
+// product uses them: from a cold cache [4096 x 4096] 27.9 -> 20.3 µs and
+// [14336 x 4096] 80.5 -> 53.3 µs, the 8-layer decoder's 256 tokens through
+// the engine 797 -> 775 ms; only a matrix that fits the memory-side cache
+// and is read again at once loses ([14336 x 4096] back to back 43.9 -> 51.1
+// µs). The decode's F32 expert rows keep plain loads (5% faster there).
+template <bool kNT = false>
 __device__ inline float f32_row_chains(const float *__restrict__ row, const float *x, uint32_t n,
                                        uint32_t c) {
+    auto ld = [](const float *p) {
+        if constexpr (kNT) return ldf_nt(p);
+        else return *p;
+    };
     float acc = 0.0f;
     const uint32_t n16 = n / 16 * 16;
     // the chain is a dependent FMA sequence: the row's elements are requested
@@ -22,7 +33,7 @@ __device__ inline float f32_row_chains(const float *__restrict__ row, const floa
     float wb[2][kB];
     if (nb > 0) {
 #pragma unroll
-        for (uint32_t u = 0; u < kB; ++u) wb[0][u] = row[16 * u + c];
+        for (uint32_t u = 0; u < kB; ++u) wb[0][u] = ld(row + 16 * u + c);
     }
     for (uint32_t bi = 0; bi < nb; bi += 2) {
 #pragma unroll
@@ -31,7 +42,7 @@ __device__ inline float f32_row_chains(const float *__restrict__ row, const floa
             if (b >= nb) break;
             const uint32_t k0 = 16 * kB * b, kn = 16 * kB * (b + 1 < nb ? b + 1 : b);
 #pragma unroll
-            for (uint32_t u = 0; u < kB; ++u) wb[half ^ 1][u] = row[kn + 16 * u + c];
+            for (uint32_t u = 0; u < kB; ++u) wb[half ^ 1][u] = ld(row + kn + 16 * u + c);
 #pragma unroll
             for (uint32_t u = 0; u < kB; ++u) acc = fma_rn(wb[half][u], x[k0 + 16 * u + c], acc);
         }
