@@ -93,32 +93,6 @@ struct Q40 {
         });
     }
 
-    // Scaled staging (for compute_half<..., true>): the same layout with every
-    // x value multiplied by 2^9, the sums of the unscaled values. A nibble q
-    // in the low bits of a byte, read as an OCP E4M3 fp8 value, is q * 2^-9
-    // exactly (exponent field 0 or 1), so v_cvt_pk_f32_fp8 turns two nibbles
-    // into two floats q * 2^-9 and (q * 2^-9) * (x * 2^9) rounds the real
-    // product q * x: the arithmetic is the plain one bit for bit, with half
-    // the conversions. x * 2^9 is exact unless it overflows (|x| >= 2^118,
-    // finite): the return value is true when this thread staged such a value,
-    // and then the caller stages the tile again with stage() and runs the
-    // plain arithmetic on it.
-    static constexpr bool kScalable = true;
-    template <int N = 8, bool kPre = false>
-    __device__ static bool stage_scaled(const float *__restrict__ x, uint32_t b0, uint32_t nb, float *lds,
-                                        uint32_t tid, uint32_t nthreads, const XBatch<N> &pre = XBatch<N>()) {
-        float4 *xs = reinterpret_cast<float4 *>(lds);
-        float *s8 = lds + nb * 32;
-        bool big = false;
-        gather_quads<Q40, N, kPre>(x, b0 * 32, nb * 32, tid, nthreads, pre, [&](uint32_t q, float4 v) {
-            const float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-            big |= m >= 0x1p118f && m <= 0x1.fffffep127f;
-            xs[q] = make_float4(v.x * 0x1p9f, v.y * 0x1p9f, v.z * 0x1p9f, v.w * 0x1p9f);
-            s8[q] = 8.0f * ((v.x + v.y) + (v.z + v.w));
-        });
-        return big;
-    }
-
     // Row base pointers for this lane: scales of the row, and the lane's
     // 16-byte slot of chunk 0 of the row.
     struct Row {
@@ -182,9 +156,8 @@ struct Q40 {
         }
     }
 
-    // The arithmetic of blocks 4 * half + q, q < nq, of chunk `k`; kScaled:
-    // against x staged by stage_scaled().
-    template <int NR, bool FULL, bool kScaled = false>
+    // The arithmetic of blocks 4 * half + q, q < nq, of chunk `k`.
+    template <int NR, bool FULL>
     __device__ static void compute_half(const Chunk (&k)[NR], const XHalf &xh, uint32_t half, uint32_t nq,
                                         float (&t)[NR]) {
 #pragma unroll
@@ -204,21 +177,10 @@ struct Q40 {
                 if (!FULL && q >= nq) break;
 #pragma unroll
                 for (int i = 0; i < NR; ++i) {
-                    float qa, qb, qc, qd;
-                    if constexpr (kScaled) {
-                        // (A.lo, B.lo) and (A.hi, B.hi) of block 2jj + h as q * 2^-9
-                        const float2 lq = h ? fp8_pair<true>(lo4[i]) : fp8_pair<false>(lo4[i]);
-                        const float2 hq = h ? fp8_pair<true>(hi4[i]) : fp8_pair<false>(hi4[i]);
-                        qa = lq.x;
-                        qb = lq.y;
-                        qc = hq.x;
-                        qd = hq.y;
-                    } else {
-                        qa = h ? ubyte2(lo4[i]) : ubyte0(lo4[i]);
-                        qb = h ? ubyte3(lo4[i]) : ubyte1(lo4[i]);
-                        qc = h ? ubyte2(hi4[i]) : ubyte0(hi4[i]);
-                        qd = h ? ubyte3(hi4[i]) : ubyte1(hi4[i]);
-                    }
+                    // (A.lo, B.lo) and (A.hi, B.hi) of block 2jj + h, exact
+                    const float2 lq = h ? nibble_pair<true>(lo4[i]) : nibble_pair<false>(lo4[i]);
+                    const float2 hq = h ? nibble_pair<true>(hi4[i]) : nibble_pair<false>(hi4[i]);
+                    const float qa = lq.x, qb = lq.y, qc = hq.x, qd = hq.y;
                     // lo = fma(q[l], x[l], q[8+l]*x[8+l]); hi likewise for 16+l, 24+l
                     const float lo = fma_rn(qa, xh.xv[q].x, qb * xh.xv[q].y);
                     const float hi = fma_rn(qc, xh.xv[q].z, qd * xh.xv[q].w);
@@ -233,7 +195,7 @@ struct Q40 {
     // Blocks j < nblk of chunk `k` (block index within the LDS tile: tb0 + j),
     // in two halves of four blocks whose LDS reads are issued before their
     // arithmetic. FULL: all kPerChunk blocks are present.
-    template <int NR, bool FULL = false, bool kScaled = false>
+    template <int NR, bool FULL = false>
     __device__ static void step(const Chunk (&k)[NR], const float *lds, uint32_t nb_tile,
                                 uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
 #pragma unroll
@@ -242,7 +204,7 @@ struct Q40 {
             XHalf xh;
             read_half(xh, lds, nb_tile, tb0, half, l, FULL ? kPerChunk : nblk);
             const uint32_t nq = FULL ? 4 : (nblk - 4 * half < 4 ? nblk - 4 * half : 4);
-            compute_half<NR, FULL, kScaled>(k, xh, half, nq, t);
+            compute_half<NR, FULL>(k, xh, half, nq, t);
         }
     }
 
@@ -258,7 +220,6 @@ struct Q40 {
 // Block = 32; chunk = 4 blocks. LDS per block: 8 lanes x float4.
 struct Q80 {
     static constexpr uint32_t kType = FMX_TYPE_Q8_0;
-    static constexpr bool kScalable = false;
     static constexpr uint32_t kBlock = 32;
     static constexpr uint32_t kPerChunk = 4;
     static constexpr uint32_t kLdsFloatsPerBlock = 32;
@@ -339,7 +300,6 @@ struct Q80 {
 // the tile, by 8 floats of per-group sums (lo, hi) in the reference's order.
 struct Q4K {
     static constexpr uint32_t kType = FMX_TYPE_Q4_K;
-    static constexpr bool kScalable = false;
     static constexpr uint32_t kBlock = 256;
     static constexpr uint32_t kPerChunk = 1;
     static constexpr uint32_t kLdsFloatsPerBlock = 264;
@@ -414,14 +374,16 @@ struct Q4K {
             for (int i = 0; i < NR; ++i) {
                 const uint32_t w = g == 0 ? k[i].q.x : g == 1 ? k[i].q.y : g == 2 ? k[i].q.z : k[i].q.w;
                 const uint32_t lo4 = w & 0x0F0F0F0Fu, hi4 = (w >> 4) & 0x0F0F0F0Fu;
-                float alo = fma_rn(ubyte0(lo4), xl.x, 0.0f);
-                alo = fma_rn(ubyte1(lo4), xl.y, alo);
-                alo = fma_rn(ubyte2(lo4), xl.z, alo);
-                alo = fma_rn(ubyte3(lo4), xl.w, alo);
-                float ahi = fma_rn(ubyte0(hi4), xh.x, 0.0f);
-                ahi = fma_rn(ubyte1(hi4), xh.y, ahi);
-                ahi = fma_rn(ubyte2(hi4), xh.z, ahi);
-                ahi = fma_rn(ubyte3(hi4), xh.w, ahi);
+                const float2 l01 = nibble_pair<false>(lo4), l23 = nibble_pair<true>(lo4);
+                const float2 h01 = nibble_pair<false>(hi4), h23 = nibble_pair<true>(hi4);
+                float alo = fma_rn(l01.x, xl.x, 0.0f);
+                alo = fma_rn(l01.y, xl.y, alo);
+                alo = fma_rn(l23.x, xl.z, alo);
+                alo = fma_rn(l23.y, xl.w, alo);
+                float ahi = fma_rn(h01.x, xh.x, 0.0f);
+                ahi = fma_rn(h01.y, xh.y, ahi);
+                ahi = fma_rn(h23.x, xh.z, ahi);
+                ahi = fma_rn(h23.y, xh.w, ahi);
                 const float hlo = hsum8_lanes(alo), hhi = hsum8_lanes(ahi);
                 uint8_t hdr[16];
                 memcpy(hdr, &k[i].h, 16);
@@ -506,12 +468,10 @@ __device__ __forceinline__ void run_chunks_pf(const typename T::Row (&rows)[NR],
 // the LDS reads of the next half chunk are in flight during the arithmetic of
 // the current one, for kernels with too few wavefronts per SIMD to hide LDS
 // latency by switching.
-// T::step, with the scaled arithmetic when kScaled and the type has it.
-template <class T, int NR, bool FULL, bool kScaled>
+template <class T, int NR, bool FULL>
 __device__ __forceinline__ void chain_step(const typename T::Chunk (&k)[NR], const float *lds, uint32_t nb_tile,
                                            uint32_t tb0, uint32_t nblk, uint32_t l, float (&t)[NR]) {
-    if constexpr (kScaled && T::kScalable) T::template step<NR, FULL, true>(k, lds, nb_tile, tb0, nblk, l, t);
-    else T::template step<NR, FULL>(k, lds, nb_tile, tb0, nblk, l, t);
+    T::template step<NR, FULL>(k, lds, nb_tile, tb0, nblk, l, t);
 }
 
 template <class T, int NR, int PF, int U = 1, bool kPipe = false>
@@ -527,7 +487,7 @@ struct ChunkStream {
     // chunks past the stream position into `dst`. The chunk's and the next
     // chunk's first blocks sit kb and kn blocks past the blocks xs0 / s80
     // point at (read_half_at).
-    template <bool kScaled, class XH>
+    template <class XH>
     __device__ __forceinline__ void pipe_step(const typename T::Chunk (&cur)[NR], typename T::Chunk (&dst)[NR],
                                               uint32_t rel, const float4 *xs0, const float *s80, uint32_t kb,
                                               uint32_t kn, float (&t)[NR], XH &xa, XH &xb) {
@@ -536,10 +496,10 @@ struct ChunkStream {
         __builtin_amdgcn_sched_barrier(0);
         T::read_half_at(xb, xs0, s80, kb, 1);
         __builtin_amdgcn_sched_barrier(0);
-        T::template compute_half<NR, true, kScaled>(cur, xa, 0, 4, t);
+        T::template compute_half<NR, true>(cur, xa, 0, 4, t);
         T::read_half_at(xa, xs0, s80, kn, 0);
         __builtin_amdgcn_sched_barrier(0);
-        T::template compute_half<NR, true, kScaled>(cur, xb, 1, 4, t);
+        T::template compute_half<NR, true>(cur, xb, 1, 4, t);
     }
 
     __device__ __forceinline__ void advance(uint32_t n) {
@@ -561,9 +521,7 @@ struct ChunkStream {
     }
 
     // Chunks [c0, c1) against the LDS tile that starts at block tile_b0; c0
-    // is the stream's position. kScaled: the tile was staged by
-    // T::stage_scaled().
-    template <bool kScaled = false>
+    // is the stream's position.
     __device__ __forceinline__ void run(uint32_t c0, uint32_t c1, uint32_t c_end, uint32_t blocks,
                                         uint32_t tile_b0, uint32_t nb_tile, const float *lds, uint32_t l,
                                         float (&t)[NR]) {
@@ -590,7 +548,7 @@ struct ChunkStream {
                         for (int p = 0; p < kSlots; ++p) {
                             const uint32_t k = u * kSlots + p;
                             const uint32_t kn = k + 1 < kSlots * U ? (k + 1) * T::kPerChunk : kend;
-                            pipe_step<kScaled>(buf[p], buf[(p + PF) % kSlots], k + PF, xs0, s80, k * T::kPerChunk, kn,
+                            pipe_step(buf[p], buf[(p + PF) % kSlots], k + PF, xs0, s80, k * T::kPerChunk, kn,
                                                t, xa, xb);
                         }
                     }
@@ -604,7 +562,7 @@ struct ChunkStream {
 #pragma unroll
                 for (int p = 0; p < kSlots; ++p) {
                     const uint32_t kn = p + 1 < kSlots ? (p + 1) * T::kPerChunk : kend;
-                    pipe_step<kScaled>(buf[p], buf[(p + PF) % kSlots], p + PF, xs0, s80, p * T::kPerChunk, kn, t, xa,
+                    pipe_step(buf[p], buf[(p + PF) % kSlots], p + PF, xs0, s80, p * T::kPerChunk, kn, t, xa,
                                        xb);
                 }
                 advance(kSlots);
@@ -622,7 +580,7 @@ struct ChunkStream {
                         for (int i = 0; i < NR; ++i)
                             buf[(p + PF) % kSlots][i] = T::load(at[i], u * kSlots + p + PF);
                         __builtin_amdgcn_sched_barrier(0);
-                        chain_step<T, NR, true, kScaled>(buf[p], lds, nb_tile, cc * T::kPerChunk - tile_b0,
+                        chain_step<T, NR, true>(buf[p], lds, nb_tile, cc * T::kPerChunk - tile_b0,
                                                    T::kPerChunk, l, t);
                     }
                 }
@@ -637,7 +595,7 @@ struct ChunkStream {
                 // the scheduler would otherwise sink loads whose data is used
                 // late in a step down to that use, emptying the prefetch ring
                 __builtin_amdgcn_sched_barrier(0);
-                chain_step<T, NR, true, kScaled>(buf[p], lds, nb_tile, cc * T::kPerChunk - tile_b0, T::kPerChunk, l, t);
+                chain_step<T, NR, true>(buf[p], lds, nb_tile, cc * T::kPerChunk - tile_b0, T::kPerChunk, l, t);
             }
             advance(kSlots);
         }
@@ -652,9 +610,9 @@ struct ChunkStream {
             for (int i = 0; i < NR; ++i) buf[(p + PF) % kSlots][i] = T::load(at[i], nxt - c);
             const uint32_t b = cc * T::kPerChunk;
             if (cc < full_end)
-                chain_step<T, NR, true, kScaled>(buf[p], lds, nb_tile, b - tile_b0, T::kPerChunk, l, t);
+                chain_step<T, NR, true>(buf[p], lds, nb_tile, b - tile_b0, T::kPerChunk, l, t);
             else
-                chain_step<T, NR, false, kScaled>(buf[p], lds, nb_tile, b - tile_b0, blocks - b, l, t);
+                chain_step<T, NR, false>(buf[p], lds, nb_tile, b - tile_b0, blocks - b, l, t);
         }
         if (c1 > c) advance(c1 - c);
     }

@@ -54,7 +54,6 @@ struct PairQ40 {
         return X{reinterpret_cast<const float4 *>(tile) + l, tile + nb_tile * 32 + l};
     }
     // c of blocks 4 hf + q, q < 4, of chunk `ch` of the tile.
-    template <bool kScaled>
     __device__ static void values(const PairChunk &k, const X &xt, uint32_t ch, uint32_t l, uint32_t hf,
                                   float (&c)[kNV]) {
         const float4 *xs4 = xt.xs4 + ch * 64;
@@ -67,22 +66,10 @@ struct PairQ40 {
             for (uint32_t h = 0; h < 2; ++h) {
                 const uint32_t q = 2 * jj + h, b = 4 * hf + q;
                 const float4 xv = xs4[b * 8];
-                float qa, qb, qc, qd;
-                if constexpr (kScaled) {
-                    const float2 lq = h ? fp8_pair<true>(lo4) : fp8_pair<false>(lo4);
-                    const float2 hq = h ? fp8_pair<true>(hi4) : fp8_pair<false>(hi4);
-                    qa = lq.x;
-                    qb = lq.y;
-                    qc = hq.x;
-                    qd = hq.y;
-                } else {
-                    qa = h ? ubyte2(lo4) : ubyte0(lo4);
-                    qb = h ? ubyte3(lo4) : ubyte1(lo4);
-                    qc = h ? ubyte2(hi4) : ubyte0(hi4);
-                    qd = h ? ubyte3(hi4) : ubyte1(hi4);
-                }
-                const float lo = fma_rn(qa, xv.x, qb * xv.y);
-                const float hi = fma_rn(qc, xv.z, qd * xv.w);
+                const float2 lq = h ? nibble_pair<true>(lo4) : nibble_pair<false>(lo4);
+                const float2 hq = h ? nibble_pair<true>(hi4) : nibble_pair<false>(hi4);
+                const float lo = fma_rn(lq.x, xv.x, lq.y * xv.y);
+                const float hi = fma_rn(hq.x, xv.z, hq.y * xv.w);
                 c[q] = (lo + hi) - s8[b * 8];
             }
         }
@@ -126,7 +113,6 @@ struct PairQ4K {
         sc = hf ? ((b3 & 0x0Fu) | ((b1 >> 6) << 4)) : (b1 & 63u);
         m = hf ? ((b3 >> 4) | ((b2 >> 6) << 4)) : (b2 & 63u);
     }
-    template <bool kScaled>
     __device__ static void values(const PairChunk &k, const X &xt, uint32_t ch, uint32_t l, uint32_t hf,
                                   float (&c)[kNV]) {
         const float4 *xs = xt.xs;
@@ -141,14 +127,16 @@ struct PairQ4K {
             const float sum_lo = sums[(ch * 4 + g) * 2], sum_hi = sums[(ch * 4 + g) * 2 + 1];
             const uint32_t w = gg ? k.q.y : k.q.x;
             const uint32_t lo4 = w & 0x0F0F0F0Fu, hi4 = (w >> 4) & 0x0F0F0F0Fu;
-            float alo = fma_rn(ubyte0(lo4), xl.x, 0.0f);
-            alo = fma_rn(ubyte1(lo4), xl.y, alo);
-            alo = fma_rn(ubyte2(lo4), xl.z, alo);
-            alo = fma_rn(ubyte3(lo4), xl.w, alo);
-            float ahi = fma_rn(ubyte0(hi4), xh.x, 0.0f);
-            ahi = fma_rn(ubyte1(hi4), xh.y, ahi);
-            ahi = fma_rn(ubyte2(hi4), xh.z, ahi);
-            ahi = fma_rn(ubyte3(hi4), xh.w, ahi);
+            const float2 l01 = nibble_pair<false>(lo4), l23 = nibble_pair<true>(lo4);
+            const float2 h01 = nibble_pair<false>(hi4), h23 = nibble_pair<true>(hi4);
+            float alo = fma_rn(l01.x, xl.x, 0.0f);
+            alo = fma_rn(l01.y, xl.y, alo);
+            alo = fma_rn(l23.x, xl.z, alo);
+            alo = fma_rn(l23.y, xl.w, alo);
+            float ahi = fma_rn(h01.x, xh.x, 0.0f);
+            ahi = fma_rn(h01.y, xh.y, ahi);
+            ahi = fma_rn(h23.x, xh.z, ahi);
+            ahi = fma_rn(h23.y, xh.w, ahi);
             const float hlo = hsum8_lanes(alo), hhi = hsum8_lanes(ahi);
             // sub-blocks 2 g and 2 g + 1 = 4 hf + 2 gg and 4 hf + 2 gg + 1
             uint32_t sc1, m1, sc2, m2;
@@ -180,7 +168,7 @@ struct PairQ4K {
 // The row's chunks in rings of PF + 1 register slots, chunk c + PF requested
 // while chunk c is computed. The last one or two rings run with each request
 // under a (wavefront-uniform) test, so nothing past the row's end is read.
-template <class P, int PF, bool kScaled>
+template <class P, int PF>
 __device__ __forceinline__ float pair_stream(const uint8_t *qp, const uint8_t *sp, uint32_t c_end, const float *tile,
                                              uint32_t nb_tile, uint32_t l, uint32_t hf, PairChunk (&buf)[PF + 1]) {
     constexpr uint32_t kSlots = PF + 1;
@@ -195,7 +183,7 @@ __device__ __forceinline__ float pair_stream(const uint8_t *qp, const uint8_t *s
             nx.s = ld16(sp + (p + PF) * 16);
             __builtin_amdgcn_sched_barrier(0);
             float cv[P::kNV];
-            P::template values<kScaled>(buf[p], xt, c + p, l, hf, cv);
+            P::values(buf[p], xt, c + p, l, hf, cv);
             t = P::chain(buf[p], cv, t);
         }
         qp += kSlots * 128;
@@ -211,7 +199,7 @@ __device__ __forceinline__ float pair_stream(const uint8_t *qp, const uint8_t *s
             nx.s = ld16(sp + (p + PF) * 16);
         }
         float cv[P::kNV];
-        P::template values<kScaled>(buf[p % kSlots], xt, c + p, l, hf, cv);
+        P::values(buf[p % kSlots], xt, c + p, l, hf, cv);
         t = P::chain(buf[p % kSlots], cv, t);
     }
     return t;
@@ -259,37 +247,13 @@ __global__ __launch_bounds__(kPairThreads) __attribute__((amdgpu_waves_per_eu(2,
         buf[p].q = ld8nt(qp + c * 128);
         buf[p].s = ld16(sp + c * 16);
     }
-    bool scaled = false;
-    if constexpr (T::kScalable) {
-        bool big = T::template stage_scaled<kB, true>(act, 0, blocks, lds, tid, kPairThreads, b0);
-        if (K > 1)
-            big |= T::template stage_scaled<kB, true>(act + a.ffn, 0, blocks, lds + tile_floats, tid, kPairThreads, b1);
-        for (uint32_t r = 2; r < K; ++r)
-            big |= T::template stage_scaled<kB>(act + static_cast<uint64_t>(r) * a.ffn, 0, blocks, lds + r * tile_floats,
-                                                tid, kPairThreads);
-        scaled = !__syncthreads_or(big);
-    }
-    if constexpr (T::kScalable) {
-        // a tile with a value that 2^9 would overflow: staged again plainly
-        if (!scaled)
-            for (uint32_t r = 0; r < K; ++r)
-                T::template stage<kB>(act + static_cast<uint64_t>(r) * a.ffn, 0, blocks, lds + r * tile_floats, tid,
-                                      kPairThreads);
-    } else {
-        T::template stage<kB, true>(act, 0, blocks, lds, tid, kPairThreads, b0);
-        if (K > 1) T::template stage<kB, true>(act + a.ffn, 0, blocks, lds + tile_floats, tid, kPairThreads, b1);
-        for (uint32_t r = 2; r < K; ++r)
-            T::template stage<kB>(act + static_cast<uint64_t>(r) * a.ffn, 0, blocks, lds + r * tile_floats, tid,
-                                  kPairThreads);
-    }
+    T::template stage<kB, true>(act, 0, blocks, lds, tid, kPairThreads, b0);
+    if (K > 1) T::template stage<kB, true>(act + a.ffn, 0, blocks, lds + tile_floats, tid, kPairThreads, b1);
+    for (uint32_t r = 2; r < K; ++r)
+        T::template stage<kB>(act + static_cast<uint64_t>(r) * a.ffn, 0, blocks, lds + r * tile_floats, tid,
+                              kPairThreads);
     __syncthreads();
-    const float *tile = lds + rank * tile_floats;
-    float t;
-    if constexpr (T::kScalable)
-        t = scaled ? pair_stream<P, PF, true>(qp, sp, c_end, tile, blocks, l, hf, buf)
-                   : pair_stream<P, PF, false>(qp, sp, c_end, tile, blocks, l, hf, buf);
-    else
-        t = pair_stream<P, PF, false>(qp, sp, c_end, tile, blocks, l, hf, buf);
+    const float t = pair_stream<P, PF>(qp, sp, c_end, lds + rank * tile_floats, blocks, l, hf, buf);
     const float v = P::finish(t);
     if ((tid & 15) == 0) dres[slot] = bad ? 0.0f : v;
     __syncthreads();

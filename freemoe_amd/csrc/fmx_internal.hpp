@@ -76,28 +76,6 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
 }
 
-// Byte n of a dword as an exact float (v_cvt_f32_ubyte{0..3}).
-__device__ __forceinline__ float ubyte0(uint32_t v) {
-    float r;
-    asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
-    return r;
-}
-__device__ __forceinline__ float ubyte1(uint32_t v) {
-    float r;
-    asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
-    return r;
-}
-__device__ __forceinline__ float ubyte2(uint32_t v) {
-    float r;
-    asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
-    return r;
-}
-__device__ __forceinline__ float ubyte3(uint32_t v) {
-    float r;
-    asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
-    return r;
-}
-
 __device__ __forceinline__ float fma_rn(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
 // Bytes 2w and 2w + 1 of a dword read as OCP E4M3 fp8 values (one
@@ -106,6 +84,19 @@ template <bool kHighWord>
 __device__ __forceinline__ float2 fp8_pair(uint32_t v) {
     typedef float f2 __attribute__((ext_vector_type(2)));
     const f2 r = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(v), kHighWord);
+    return make_float2(r.x, r.y);
+}
+
+// Bytes 0, 1 (or, kHighWord, 2, 3) of v, each below 16, as the integers they
+// hold, in one instruction: read as fp8 a byte below 16 is byte * 2^-9
+// exactly, and v_cvt_scalef32_pk_f32_fp8 multiplies by the power of two in
+// its scale operand's exponent (2^9), so the floats are exact whatever the
+// other operand of the products they feed (all 16 values in every byte
+// position checked on the GPU).
+template <bool kHighWord>
+__device__ __forceinline__ float2 nibble_pair(uint32_t v) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 r = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(v, 0x1p9f, kHighWord);
     return make_float2(r.x, r.y);
 }
 

@@ -1121,7 +1121,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1),
         const uint32_t nb = blocks - tb < a.dn_tile ? blocks - tb : a.dn_tile;
         __syncthreads();
         const uint32_t tile_elems = nb * T::kBlock;
-        bool scaled = false;
         if (K == 2 && tile_elems <= 16 * 4 * kThreads) {
             // both ranks' activations requested together: one memory latency;
             // the first weight chunks after them, so that staging (which
@@ -1131,33 +1130,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1),
             load_batch<T>(b0, act, tb * T::kBlock, tile_elems, tid, kThreads);
             load_batch<T>(b1, act + a.ffn, tb * T::kBlock, tile_elems, tid, kThreads);
             if (tb == 0) cs.prime(rw, c_end);
-            if constexpr (T::kScalable) {
-                bool big = T::template stage_scaled<16, true>(act, tb, nb, lds, tid, kThreads, b0);
-                big |= T::template stage_scaled<16, true>(act + a.ffn, tb, nb, lds + tile_floats, tid, kThreads, b1);
-                scaled = !__syncthreads_or(big);
-            }
-            if (!scaled) {
-                T::template stage<16>(act, tb, nb, lds, tid, kThreads);
-                T::template stage<16>(act + a.ffn, tb, nb, lds + tile_floats, tid, kThreads);
-            }
+            T::template stage<16, true>(act, tb, nb, lds, tid, kThreads, b0);
+            T::template stage<16, true>(act + a.ffn, tb, nb, lds + tile_floats, tid, kThreads, b1);
         } else {
             if (tb == 0) cs.prime(rw, c_end);
-            if constexpr (T::kScalable) {
-                bool big = false;
-                for (uint32_t r = 0; r < K; ++r)
-                    big |= T::template stage_scaled<16>(act + static_cast<uint64_t>(r) * a.ffn, tb, nb,
-                                                        lds + r * tile_floats, tid, kThreads);
-                scaled = !__syncthreads_or(big);
-            }
-            if (!scaled)
-                for (uint32_t r = 0; r < K; ++r)
-                    T::template stage<16>(act + static_cast<uint64_t>(r) * a.ffn, tb, nb, lds + r * tile_floats,
-                                          tid, kThreads);
+            for (uint32_t r = 0; r < K; ++r)
+                T::template stage<16>(act + static_cast<uint64_t>(r) * a.ffn, tb, nb, lds + r * tile_floats, tid,
+                                      kThreads);
         }
         __syncthreads();
         const uint32_t c0 = tb / T::kPerChunk, c1 = (tb + nb + T::kPerChunk - 1) / T::kPerChunk;
-        if (scaled) cs.template run<true>(c0, c1, c_end, blocks, tb, nb, lds + rank * tile_floats, l, t);
-        else cs.run(c0, c1, c_end, blocks, tb, nb, lds + rank * tile_floats, l, t);
+        cs.run(c0, c1, c_end, blocks, tb, nb, lds + rank * tile_floats, l, t);
     }
     const float v = T::finish(t[0]);
     if (l == 0) dres[slot] = bad ? 0.0f : v;
