@@ -345,9 +345,10 @@ def large_value_layer(gain_log2, gate_scale_bits):
 def test_decode_large_values(gpu, case):
     """Values of magnitude 2^100 and more in h (gate/up) or in act (down),
     with every product and sum still finite: the layer must match the oracle
-    bit for bit there too. The down kernel stages act times 2^9 for its fp8
-    nibble conversion; from 2^118 on that would overflow, and the tile takes
-    the plain arithmetic instead (the last case)."""
+    bit for bit there too. The nibbles become exact integers whatever the
+    activations (a scaled conversion), so activations of 2^118 and more,
+    where scaling the activations by 2^9 instead would overflow, are exact as
+    well (the last case)."""
     if case == "h_beyond_2^100":
         lw, x = large_value_layer(101, 0x0000)  # gate ignores element 5
     elif case == "act_beyond_2^100":
