@@ -109,16 +109,19 @@ template <int M>
 __device__ __forceinline__ uint32_t lane_xor_u32(uint32_t v) {
     const int b = static_cast<int>(v);
     int r;
+    // (every lane has its source lane for M = 1, 2, 8, so bound_ctrl changes
+    // nothing there; set, it lets the compiler fold the move into the
+    // instruction that consumes it, e.g. v_add_f32_dpp)
     if constexpr (M == 1) {
-        r = __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, false); // quad_perm [1,0,3,2]
+        r = __builtin_amdgcn_mov_dpp(b, 0xB1, 0xF, 0xF, true); // quad_perm [1,0,3,2]
     } else if constexpr (M == 2) {
-        r = __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, false); // quad_perm [2,3,0,1]
+        r = __builtin_amdgcn_mov_dpp(b, 0x4E, 0xF, 0xF, true); // quad_perm [2,3,0,1]
     } else if constexpr (M == 4) {
         const int hi = __builtin_amdgcn_mov_dpp(b, 0x114, 0xF, 0xF, false); // row_shr:4
         r = __builtin_amdgcn_update_dpp(hi, b, 0x104, 0xF, 0x5, false);     // row_shl:4, banks 0, 2
     } else {
         static_assert(M == 8, "lane_xor: mask 1, 2, 4 or 8");
-        r = __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, false); // row_ror:8
+        r = __builtin_amdgcn_mov_dpp(b, 0x128, 0xF, 0xF, true); // row_ror:8
     }
     return static_cast<uint32_t>(r);
 }
