@@ -384,7 +384,7 @@ struct Q4K {
                 ahi = fma_rn(h01.y, xh.y, ahi);
                 ahi = fma_rn(h23.x, xh.z, ahi);
                 ahi = fma_rn(h23.y, xh.w, ahi);
-                const float hlo = hsum8_lanes(alo), hhi = hsum8_lanes(ahi);
+                const float hlo = hsum8_first(alo), hhi = hsum8_first(ahi);
                 uint8_t hdr[16];
                 memcpy(hdr, &k[i].h, 16);
                 const float d = half_bits_to_float(hdr[0] | (hdr[1] << 8));
@@ -402,7 +402,8 @@ struct Q4K {
         }
     }
 
-    // The running total is already the row's value in every lane.
+    // The running total is the row's value in lanes 0-3 of the row's group
+    // (its lane trees are hsum8_first's); callers read lane 0.
     __device__ static float finish(float t) { return t; }
 };
 

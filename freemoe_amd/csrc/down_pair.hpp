@@ -137,7 +137,7 @@ struct PairQ4K {
             ahi = fma_rn(h01.y, xh.y, ahi);
             ahi = fma_rn(h23.x, xh.z, ahi);
             ahi = fma_rn(h23.y, xh.w, ahi);
-            const float hlo = hsum8_lanes(alo), hhi = hsum8_lanes(ahi);
+            const float hlo = hsum8_first(alo), hhi = hsum8_first(ahi);
             // sub-blocks 2 g and 2 g + 1 = 4 hf + 2 gg and 4 hf + 2 gg + 1
             uint32_t sc1, m1, sc2, m2;
             if (gg == 0) {

@@ -171,6 +171,18 @@ __device__ __forceinline__ float hsum8_lanes(float t) {
     return a + lane_xor<2>(a);
 }
 
+// hsum8_lanes' value in lanes 0-3 of each 8-lane group only (the other four
+// hold sums that mix in the neighbouring group), for callers that read lane
+// 0 of each group: the first stage takes lane i + 4 by a rotation of the
+// 16-lane row (row_ror:12: lane i reads lane (i - 12) mod 16) instead of the
+// two masked moves of lane_xor<4>, so all three stages fold into DPP adds.
+__device__ __forceinline__ float hsum8_first(float t) {
+    const float r = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, t), 0x12C, 0xF, 0xF, true));
+    const float s = t + r;
+    const float a = s + lane_xor<1>(s);
+    return a + lane_xor<2>(a);
+}
+
 // Global-memory loads through an address-space-1 pointer. Expert slots are
 // reached through a table of generic pointers, which the compiler would
 // otherwise read with FLAT instructions; FLAT loads count against the LDS
