@@ -171,6 +171,14 @@ __device__ __forceinline__ float hsum8_lanes(float t) {
     return a + lane_xor<2>(a);
 }
 
+// Lane M's value in every lane of each 16-lane row (DPP row_newbcast:M;
+// bound_ctrl set so the move can fold into the instruction that consumes it).
+template <uint32_t M>
+__device__ __forceinline__ float row_bcast(float v) {
+    static_assert(M < 16, "a lane of the 16-lane row");
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x150 + M, 0xF, 0xF, true));
+}
+
 // hsum8_lanes' value in lanes 0-3 of each 8-lane group only (the other four
 // hold sums that mix in the neighbouring group), for callers that read lane
 // 0 of each group: the first stage takes lane i + 4 by a rotation of the

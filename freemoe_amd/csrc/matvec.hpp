@@ -2,6 +2,8 @@
 // (kernels.cpp:147-167), Q6_K in row_dot_fused_scalar's (kernels.cpp:574-590).
 #pragma once
 
+#include <utility>
+
 #include "fmx_internal.hpp"
 
 namespace fmx {
@@ -75,11 +77,14 @@ __device__ inline float q6_k_value(const uint8_t *blk, uint32_t e) {
 // (m < 16) lies in half n = m / 8, at l = 16 (m % 2) + c of the half, quarter
 // qt = (m % 8) / 2; its quant byte is ql[64 n + 16 (m % 2 + 2 (qt % 2)) + c],
 // its bit pairs qh[128 + 32 n + 16 (m % 2) + c], its scale sc[8 n + m % 2 +
-// 2 qt]. The lane loads those 8 + 4 bytes, the 16 scales and d, and its 16
-// inputs x[16 m + c], all requested together.
+// 2 qt] = sc[m]: element 16 m + c lies in sub-block m for every c. The lane
+// loads those 8 + 4 bytes, scale byte c (its sub-block's scale d sc[c] is
+// formed once per block and handed to the other lanes of its 16-lane group
+// by DPP row broadcasts) and d, and its 16 inputs x[16 m + c], all requested
+// together. The lanes of a group must be the 16 lanes of one DPP row.
 struct Q6Lane {
     uint32_t ql[2][4], qh[2][2];
-    uint32_t sc[8]; // the 16 scales as 2-byte words (blocks start 2-byte aligned)
+    uint32_t scb; // scale byte c
     uint32_t d;
     float xv[16];
     __device__ __forceinline__ void load(const uint8_t *__restrict__ blk, const float *xb, uint32_t c) {
@@ -90,27 +95,30 @@ struct Q6Lane {
 #pragma unroll
             for (uint32_t a = 0; a < 2; ++a) qh[n][a] = blk[128 + 32 * n + 16 * a + c];
         }
-        const uint16_t *s16 = reinterpret_cast<const uint16_t *>(blk + 192);
-#pragma unroll
-        for (uint32_t i = 0; i < 8; ++i) sc[i] = s16[i];
+        scb = blk[192 + c];
         d = *reinterpret_cast<const uint16_t *>(blk + 208);
 #pragma unroll
         for (uint32_t m = 0; m < 16; ++m) xv[m] = xb[16 * m + c];
     }
-    // Chain c of dot_avx2 over the block's decoded values (d * sc) * (q - 32).
-    __device__ __forceinline__ float chain() const {
-        const float df = half_bits_to_float(d);
+    // q - 32 of element 16 m + c.
+    template <uint32_t m>
+    __device__ __forceinline__ int q_of() const {
+        constexpr uint32_t n = m >> 3, a = m & 1, qt = (m & 7) >> 1;
+        const uint32_t qlb = ql[n][a + 2 * (qt & 1)];
+        return static_cast<int>((qt >= 2 ? qlb >> 4 : qlb & 0x0Fu) | (((qh[n][a] >> (2 * qt)) & 3u) << 4)) - 32;
+    }
+    template <uint32_t... M>
+    __device__ __forceinline__ float chain_over(float dsc, std::integer_sequence<uint32_t, M...>) const {
         float acc = 0.0f;
-#pragma unroll
-        for (uint32_t m = 0; m < 16; ++m) {
-            const uint32_t n = m >> 3, a = m & 1, qt = (m & 7) >> 1;
-            const uint32_t qlb = ql[n][a + 2 * (qt & 1)];
-            const int q = static_cast<int>((qt >= 2 ? qlb >> 4 : qlb & 0x0Fu) | (((qh[n][a] >> (2 * qt)) & 3u) << 4)) - 32;
-            const uint32_t si = 8 * n + a + 2 * qt;
-            const float scf = static_cast<float>(static_cast<int8_t>((sc[si >> 1] >> (8 * (si & 1))) & 0xFFu));
-            acc = fma_rn(df * scf * static_cast<float>(q), xv[m], acc);
-        }
+        ((acc = fma_rn(row_bcast<M>(dsc) * static_cast<float>(q_of<M>()), xv[M], acc)), ...);
         return acc;
+    }
+    // Chain c of dot_avx2 over the block's decoded values (d * sc) * (q - 32)
+    // in element order: d * sc[m] (exact) from lane m of the row, handed over
+    // as the multiply's DPP operand.
+    __device__ __forceinline__ float chain() const {
+        const float dsc = half_bits_to_float(d) * static_cast<float>(static_cast<int8_t>(scb & 0xFFu));
+        return chain_over(dsc, std::make_integer_sequence<uint32_t, 16>());
     }
 };
 
