@@ -141,8 +141,10 @@ __device__ inline float q6_k_row_chains(const uint8_t *__restrict__ row, const f
                 q[u ^ 1].load(row + static_cast<uint64_t>(b + u + 1) * 210, x + static_cast<uint64_t>(b + u + 1) * 256,
                               c);
             const float acc = q[u].chain();
+            // t is the same in lanes i and i + 8, so hsum8_first's rotation
+            // reads a lane holding the xor-4 partner's value in every lane
             const float t = acc + lane_xor<8>(acc);
-            total = total + hsum8_lanes(t);
+            total = total + hsum8_first(t);
         }
     }
     return total;
@@ -174,7 +176,7 @@ __device__ __forceinline__ void q6_k_block_dots(const uint8_t *__restrict__ row,
                 q[u ^ 1].load(row + static_cast<uint64_t>(nb) * 210, x + static_cast<uint64_t>(nb) * xstride, c);
             const float acc = q[u].chain();
             const float t = acc + lane_xor<8>(acc);
-            const float dot = hsum8_lanes(t);
+            const float dot = hsum8_first(t); // exact in every lane, as above
             if (c == 0) out[bu] = dot;
         }
     }
