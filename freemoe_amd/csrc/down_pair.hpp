@@ -53,24 +53,35 @@ struct PairQ40 {
     __device__ static X x_of(const float *tile, uint32_t nb_tile, uint32_t l) {
         return X{reinterpret_cast<const float4 *>(tile) + l, tile + nb_tile * 32 + l};
     }
-    // c of blocks 4 hf + q, q < 4, of chunk `ch` of the tile.
-    __device__ static void values(const PairChunk &k, const X &xt, uint32_t ch, uint32_t l, uint32_t hf,
-                                  float (&c)[kNV]) {
+    // The lane's LDS operands of one chunk: blocks 4 hf + q, q < 4.
+    struct XC {
+        float4 xv[4];
+        float s8[4];
+    };
+    __device__ static void read_x(const X &xt, uint32_t ch, uint32_t /*l*/, uint32_t hf, XC &o) {
         const float4 *xs4 = xt.xs4 + ch * 64;
         const float *s8 = xt.s8 + ch * 64;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            o.xv[q] = xs4[(4 * hf + q) * 8];
+            o.s8[q] = s8[(4 * hf + q) * 8];
+        }
+    }
+    // c of blocks 4 hf + q, q < 4, of the chunk whose operands `xc` holds.
+    __device__ static void values(const PairChunk &k, const XC &xc, uint32_t /*hf*/, float (&c)[kNV]) {
 #pragma unroll
         for (uint32_t jj = 0; jj < 2; ++jj) {
             const uint32_t qw = jj ? k.q.y : k.q.x;
             const uint32_t lo4 = qw & 0x0F0F0F0Fu, hi4 = (qw >> 4) & 0x0F0F0F0Fu;
 #pragma unroll
             for (uint32_t h = 0; h < 2; ++h) {
-                const uint32_t q = 2 * jj + h, b = 4 * hf + q;
-                const float4 xv = xs4[b * 8];
+                const uint32_t q = 2 * jj + h;
+                const float4 xv = xc.xv[q];
                 const float2 lq = h ? nibble_pair<true>(lo4) : nibble_pair<false>(lo4);
                 const float2 hq = h ? nibble_pair<true>(hi4) : nibble_pair<false>(hi4);
                 const float lo = fma_rn(lq.x, xv.x, lq.y * xv.y);
                 const float hi = fma_rn(hq.x, xv.z, hq.y * xv.w);
-                c[q] = (lo + hi) - s8[b * 8];
+                c[q] = (lo + hi) - xc.s8[q];
             }
         }
     }
@@ -113,18 +124,29 @@ struct PairQ4K {
         sc = hf ? ((b3 & 0x0Fu) | ((b1 >> 6) << 4)) : (b1 & 63u);
         m = hf ? ((b3 >> 4) | ((b2 >> 6) << 4)) : (b2 & 63u);
     }
-    __device__ static void values(const PairChunk &k, const X &xt, uint32_t ch, uint32_t l, uint32_t hf,
-                                  float (&c)[kNV]) {
-        const float4 *xs = xt.xs;
-        const float *sums = xt.sums;
-        const float d = half_bits_to_float(k.s.x & 0xFFFFu);
-        const float dmin = half_bits_to_float(k.s.x >> 16);
+    // The lane's LDS operands of one super-block: groups 2 hf and 2 hf + 1.
+    struct XC {
+        float4 xl[2], xh[2];
+        float sum_lo[2], sum_hi[2];
+    };
+    __device__ static void read_x(const X &xt, uint32_t ch, uint32_t l, uint32_t hf, XC &o) {
 #pragma unroll
         for (uint32_t gg = 0; gg < 2; ++gg) {
             const uint32_t g = 2 * hf + gg;
             const uint32_t e = (ch * 4 + g) * 8 + l;
-            const float4 xl = xs[2 * e], xh = xs[2 * e + 1];
-            const float sum_lo = sums[(ch * 4 + g) * 2], sum_hi = sums[(ch * 4 + g) * 2 + 1];
+            o.xl[gg] = xt.xs[2 * e];
+            o.xh[gg] = xt.xs[2 * e + 1];
+            o.sum_lo[gg] = xt.sums[(ch * 4 + g) * 2];
+            o.sum_hi[gg] = xt.sums[(ch * 4 + g) * 2 + 1];
+        }
+    }
+    __device__ static void values(const PairChunk &k, const XC &xc, uint32_t hf, float (&c)[kNV]) {
+        const float d = half_bits_to_float(k.s.x & 0xFFFFu);
+        const float dmin = half_bits_to_float(k.s.x >> 16);
+#pragma unroll
+        for (uint32_t gg = 0; gg < 2; ++gg) {
+            const float4 xl = xc.xl[gg], xh = xc.xh[gg];
+            const float sum_lo = xc.sum_lo[gg], sum_hi = xc.sum_hi[gg];
             const uint32_t w = gg ? k.q.y : k.q.x;
             const uint32_t lo4 = w & 0x0F0F0F0Fu, hi4 = (w >> 4) & 0x0F0F0F0Fu;
             const float2 l01 = nibble_pair<false>(lo4), l23 = nibble_pair<true>(lo4);
@@ -166,13 +188,18 @@ struct PairQ4K {
 };
 
 // The row's chunks in rings of PF + 1 register slots, chunk c + PF requested
-// while chunk c is computed. The last one or two rings run with each request
-// under a (wavefront-uniform) test, so nothing past the row's end is read.
+// while chunk c is computed, and chunk c + 1's LDS operands read during chunk
+// c's arithmetic (two operand sets, alternating with the slot's parity). The
+// last one or two rings run with each request under a (wavefront-uniform)
+// test, so nothing past the row's end is read.
 template <class P, int PF>
 __device__ __forceinline__ float pair_stream(const uint8_t *qp, const uint8_t *sp, uint32_t c_end, const float *tile,
                                              uint32_t nb_tile, uint32_t l, uint32_t hf, PairChunk (&buf)[PF + 1]) {
     constexpr uint32_t kSlots = PF + 1;
+    static_assert(kSlots % 2 == 0, "the operand sets alternate with the parity of the ring slot");
     const typename P::X xt = P::x_of(tile, nb_tile, l);
+    typename P::XC xc[2];
+    P::read_x(xt, 0, l, hf, xc[0]);
     float t = 0.0f;
     uint32_t c = 0;
     for (; c + 2 * kSlots <= c_end; c += kSlots) {
@@ -182,8 +209,9 @@ __device__ __forceinline__ float pair_stream(const uint8_t *qp, const uint8_t *s
             nx.q = ld8nt(qp + (p + PF) * 128);
             nx.s = ld16(sp + (p + PF) * 16);
             __builtin_amdgcn_sched_barrier(0);
+            P::read_x(xt, c + p + 1, l, hf, xc[(p + 1) & 1]); // c + p + 1 < c_end in this loop
             float cv[P::kNV];
-            P::values(buf[p], xt, c + p, l, hf, cv);
+            P::values(buf[p], xc[p & 1], hf, cv);
             t = P::chain(buf[p], cv, t);
         }
         qp += kSlots * 128;
@@ -198,8 +226,9 @@ __device__ __forceinline__ float pair_stream(const uint8_t *qp, const uint8_t *s
             nx.q = ld8nt(qp + (p + PF) * 128);
             nx.s = ld16(sp + (p + PF) * 16);
         }
+        if (c + p + 1 < c_end) P::read_x(xt, c + p + 1, l, hf, xc[(p + 1) & 1]);
         float cv[P::kNV];
-        P::values(buf[p % kSlots], xt, c + p, l, hf, cv);
+        P::values(buf[p % kSlots], xc[p & 1], hf, cv);
         t = P::chain(buf[p % kSlots], cv, t);
     }
     return t;
